@@ -1,0 +1,256 @@
+"""Benchmark of the MI355X ternary linear layer (one GPU).
+
+Headline workload: the large-shape HBM stress at M=1 (K=8192 -> N=28672 and
+K=28672 -> N=8192, fp16 scales |N(0,0.01)|, x ~ N(0,1)), each matrix in 8
+rotating device copies (about 500 MB, more than the 256 MB Infinity Cache),
+so every call streams its weights from HBM.  One step is one cold GEMV of
+each shape through the reference-named entry point ``gemv_plain_store``
+(quantize + GEMV); the step sequence is recorded once into a HIP graph and
+replayed.  ``value`` is algorithmic bytes / second over the timed steps:
+bytes(M,N,K) = N*ceil(K/4) + 2*N*ceil(K/128) + 4*M*K + 4*M*N.
+
+Also reported on the same line: the GEMV kernel alone (pre-quantized
+activations, HIP events on the launch stream) as the roofline figure, the
+single-linear case (K=1024 -> N=4096), the 32-token prefill tile GEMM TOPS,
+and the CPU baseline (the reference's numba GEMV restated in C++/OpenMP)
+on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "ivonar-inference_amd"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATING_COPIES = 8
+
+
+def gemv_bytes(m: int, n: int, k: int) -> int:
+    return n * ((k + 3) // 4) + 2 * n * ((k + 127) // 128) + 4 * m * k + 4 * m * n
+
+
+def parse() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
+    parser.add_argument("--skip-cpu", action="store_true")
+    return parser.parse_args()
+
+
+def graph_of(step, stream):
+    import torch
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, replays: int, warmup: int) -> float:
+    """Seconds per replay, HIP events around `replays` replays on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / replays
+
+
+def device_copies(layer, device, copies: int):
+    import torch
+    from ivonar_amd.matrix import Matrix
+
+    base = Matrix.from_tensors(torch.from_numpy(layer.packed), torch.from_numpy(layer.scales), layer.in_features,
+                               device=device)
+    mats = [base]
+    for _ in range(copies - 1):
+        clone = Matrix.__new__(Matrix)
+        for slot in Matrix.__slots__:
+            setattr(clone, slot, getattr(base, slot))
+        clone.packed = base.packed.clone()
+        clone.scales = base.scales.clone()
+        mats.append(clone)
+    return mats
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU figures are not part of this build",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from ivonar_amd import ops, runtime, synthetic
+
+    device = torch.device("cuda", 0)
+    runtime.initialise(0)
+    stream = torch.cuda.Stream()
+    results: dict[str, object] = {}
+
+    # ---- headline: cold-cache GEMV at the stress shapes -------------------------------------
+    stress = synthetic.stress_layers(seed=3)
+    matrices, inputs, outputs, bytes_per_step = [], [], [], 0
+    for layer, x in stress:
+        matrices.append(device_copies(layer, device, ROTATING_COPIES))
+        inputs.append(torch.from_numpy(x[0]).to(device))
+        outputs.append(torch.empty(layer.rows, dtype=torch.float32, device=device))
+        bytes_per_step += gemv_bytes(1, layer.rows, layer.in_features)
+
+    def stress_steps(count: int):
+        def run():
+            for step in range(count):
+                copy = step % ROTATING_COPIES
+                for shape in range(len(stress)):
+                    ops.gemv(matrices[shape][copy], inputs[shape], out=outputs[shape])
+        return run
+
+    per_graph = ROTATING_COPIES
+    graph = graph_of(stress_steps(per_graph), stream)
+    replays = max(1, args.steps // per_graph)
+    seconds = time_graph(graph, replays, max(1, args.warmup // per_graph))
+    steps = replays * per_graph
+    step_seconds = seconds / per_graph
+    value = bytes_per_step / step_seconds / 1e9
+
+    # ---- dominant kernel alone: GEMV on pre-quantized activations ----------------------------
+    kernel = {}
+    for shape, (layer, x) in enumerate(stress):
+        q8, xsum, sx = ops.quantize_rows(inputs[shape].reshape(1, -1))
+
+        def prequant(shape=shape, q8=q8, xsum=xsum, sx=sx):
+            for copy in range(ROTATING_COPIES):
+                ops.gemv_prequant(matrices[shape][copy], q8, xsum, sx, out=outputs[shape])
+
+        g = graph_of(prequant, stream)
+        t = time_graph(g, max(1, args.steps // ROTATING_COPIES), 2) / ROTATING_COPIES
+        b = gemv_bytes(1, layer.rows, layer.in_features)
+        kernel[f"{layer.in_features}x{layer.rows}"] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
+    kernel_bytes = sum(v["bytes"] for v in kernel.values())
+    kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
+    achieved = kernel_bytes / kernel_seconds / 1e9
+
+    # ---- single linear K=1024 -> N=4096 (launch-latency bound) ------------------------------
+    layer0, x0 = synthetic.single_linear(seed=0)
+    m0 = device_copies(layer0, device, 1)[0]
+    xin0 = torch.from_numpy(x0[0]).to(device)
+    y0 = torch.empty(layer0.rows, dtype=torch.float32, device=device)
+    g0 = graph_of(lambda: [ops.gemv(m0, xin0, out=y0) for _ in range(64)], stream)
+    t0 = time_graph(g0, 20, 2) / 64
+    results["single_linear_1024x4096_us"] = round(t0 * 1e6, 3)
+
+    # ---- prefill tile GEMM at M=32 -----------------------------------------------------------
+    rng = np.random.default_rng(2)
+    prefill = {}
+    for layer, k in synthetic.prefill_layers(seed=2):
+        mat = device_copies(layer, device, 1)[0]
+        for m in (32, 2048):
+            xs = torch.from_numpy(synthetic.prefill_activations(rng, m, k)).to(device)
+            q8, xsum, sx = ops.quantize_rows(xs)
+            out = torch.empty((m, layer.rows), dtype=torch.float32, device=device)
+            g = graph_of(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream)
+            t = time_graph(g, 50, 5)
+            prefill[f"{k}x{layer.rows}_m{m}"] = {"us": round(t * 1e6, 3), "TOPS": round(2 * m * layer.rows * k / t / 1e12, 3)}
+    results["prefill_gemm"] = prefill
+
+    # ---- CPU baseline on a bounded sample -------------------------------------------------------
+    cpu = None
+    if not args.skip_cpu:
+        cpu = cpu_baseline(stress, args.cpu_seconds)
+
+    line = {
+        "metric": "ternary GEMV HBM GB/s (% peak) at M=1; prefill GEMM int8 TOPS; decode tok/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_seconds * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random-init ternary weights)",
+        "config": {
+            "workload": "ternary GEMV M=1 cold cache: K=8192->N=28672 and K=28672->N=8192, 8 rotating copies",
+            "entry_point": "gemv_plain_store (quantize + GEMV)",
+            "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "gemv_kernel (pre-quantized activations)",
+            "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)} for k, v in kernel.items()},
+        },
+        "cpu_baseline": cpu,
+        "extra": results,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(stress, budget_seconds: float):
+    """The numba GEMV restated in C++/OpenMP, timed on this host on the stress shapes."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import ternary_oracle as T
+
+    cb = T.CpuBaseline()
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(threads, 16))
+    cb.set_threads(threads)
+    total_bytes, total_seconds, calls = 0, 0.0, 0
+    prepared = []
+    for layer, x in stress:
+        planes = cb.planes_of(layer.packed, layer.in_features)
+        scales = layer.scales.astype(np.float32)
+        prepared.append((planes, scales, np.ascontiguousarray(x[0]), np.zeros(layer.rows, np.float32),
+                         cb.workspace(layer.in_features), layer))
+    deadline = time.perf_counter() + budget_seconds
+    while time.perf_counter() < deadline:
+        for planes, scales, x, out, ws, layer in prepared:
+            start = time.perf_counter()
+            cb.gemv(x, planes, scales, None, out, ws=ws)
+            total_seconds += time.perf_counter() - start
+            total_bytes += gemv_bytes(1, layer.rows, layer.in_features)
+            calls += 1
+    return {
+        "value": round(total_bytes / total_seconds / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{calls} GEMV calls over both stress shapes (~{budget_seconds:.0f} s), planes layout, OpenMP",
+    }
+
+
+if __name__ == "__main__":
+    main()

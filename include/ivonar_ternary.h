@@ -1,0 +1,163 @@
+/*
+ * ivonar_ternary.h - C ABI of the MI355X (gfx950) ternary linear layer.
+ *
+ * Drop-in replacement for the CUDA kernels the reference decoder launches
+ * for its ternary linear ops.  Each entry point has the name and argument
+ * order of the reference kernel it replaces (reference paths relative to
+ * src/ivonar_inference/), with the launch stream first.  It computes its own
+ * grid; the `lanes` argument and the `next`/`next_bytes` L2-prefetch slots
+ * are accepted for ABI compatibility and ignored (MI355X has no persisting-L2
+ * window; its Infinity Cache needs no hint).
+ *
+ * Conventions
+ *   - Every function returns hipSuccess or a HIP error code; nothing is
+ *     synchronised, allocated or read back, so the calls may be recorded
+ *     into a HIP graph once ivonar_init() has run for the device.
+ *   - All pointers are device pointers on the stream's device.
+ *   - packed: uint8 [rows, row_bytes], row_bytes a multiple of 16 and at
+ *     least 16*ceil(n/64); byte b holds inputs 4b..4b+3, input 4b+k in bits
+ *     2k..2k+1 as code = w + 1 (w in {-1,0,+1}).  16-byte aligned.
+ *   - scales: fp16 bit patterns [rows, groups], groups >= ceil(n/128), one
+ *     scale per 128 inputs.  bias: fp32 [rows] or NULL.
+ *   - q8/xsum/scale buffers hold quantized activations in this library's
+ *     private layout; capacity per token row: ceil(n/64)*64 int8,
+ *     ceil(n/64) int32 and one fp32 (the reference's q8/q8sum/q8scale sizes).
+ *   - fp32 results follow this library's summation order, which the CPU
+ *     oracle restates exactly; per-128-group int32 partials are exact.
+ */
+#ifndef IVONAR_TERNARY_H
+#define IVONAR_TERNARY_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IVONAR_ABI_VERSION 1
+
+/* ---------------------------------------------------------------- set-up */
+
+/* Allocates the per-device activation scratch used when a GEMV quantizes
+ * rows longer than the fused limit.  Call once per device outside graph
+ * capture; replaces the reference's compile_module set-up step
+ * (kernels/runtime.py:301-324).  Calls with the device current. */
+hipError_t ivonar_init(int device);
+
+/* Process-wide values the reference passes as -D defines to NVRTC
+ * (kernel_decoder.py:215, ternary.cu:1-46): "HEAD_DIM" (ATTN prologue head
+ * width, default 64), "TILE" (token rows of quantize_tile_*, default 32),
+ * "MAX_CHUNKS" (caller q8 capacity, default 70).  Unknown names return
+ * hipErrorInvalidValue. */
+hipError_t ivonar_define(const char* name, int value);
+
+const char* ivonar_error_string(hipError_t status);
+int ivonar_abi_version(void);
+
+/* Lane layout of the decode GEMV for a K-wide row: lanes per row and rows
+ * per lane; the lane count fixes its fp32 summation order.  Host only. */
+void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane);
+
+/* ------------------------------------------------------------ decode GEMV
+ * GEMV_ARGS of ternary.cu:293-298.  y[r] = s_x * sum_g P[r,g]*scale[r,g]
+ * (+ bias[r]).  Prologue: PLAIN quantizes `input`, NORM applies RMSNorm
+ * (eps, clip +-8, weight `aux`) first, ATTN merges split-softmax partials
+ * [heads, splits, HEAD_DIM+2] first; prequant reads q8_in/xsum_in/scale_in.
+ * Epilogue: store, residual (output[r] += y), silu pair (interleaved
+ * gate/up rows; output[r/2] = silu(y[r]) * y[r+1], rows even). */
+#define IVONAR_GEMV_ARGS                                                                                    \
+  const float *input, const float *aux, const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, \
+      const uint8_t *packed, const uint16_t *scales, const float *bias, float *output, int rows, int n,      \
+      int row_bytes, int groups, int lanes, int splits, float eps, const uint8_t *next, int next_bytes
+
+/* ternary.cu:356-358 */
+hipError_t gemv_plain_store(hipStream_t stream, IVONAR_GEMV_ARGS);
+/* ternary.cu:359-361 */
+hipError_t gemv_plain_residual(hipStream_t stream, IVONAR_GEMV_ARGS);
+/* ternary.cu:365-367 */
+hipError_t gemv_norm_store(hipStream_t stream, IVONAR_GEMV_ARGS);
+/* ternary.cu:368-370 */
+hipError_t gemv_norm_silu_pair(hipStream_t stream, IVONAR_GEMV_ARGS);
+/* ternary.cu:371-373 */
+hipError_t gemv_attn_residual(hipStream_t stream, IVONAR_GEMV_ARGS);
+/* ternary.cu:374-376 (LM head: reads q8_in/xsum_in/scale_in) */
+hipError_t gemv_prequant_store(hipStream_t stream, IVONAR_GEMV_ARGS);
+/* ternary.cu:377-388: the _wide variants (K > 1024) share the kernels above. */
+hipError_t gemv_plain_store_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
+hipError_t gemv_plain_residual_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
+hipError_t gemv_norm_store_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
+hipError_t gemv_norm_silu_pair_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
+hipError_t gemv_attn_residual_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
+
+/* Test export (no reference counterpart; requested by the decode-path parity
+ * checks): the exact int32 partials P[r, g] of the GEMV's integer core, from
+ * pre-quantized activations, into partials int32 [rows, groups]. */
+hipError_t gemv_group_partials(hipStream_t stream, const int8_t* q8_in, const int32_t* xsum_in,
+                               const uint8_t* packed, int rows, int n, int row_bytes, int groups,
+                               int32_t* partials);
+
+/* -------------------------------------------------------------- quantizer */
+
+/* QUANT_ARGS of ternary.cu:390-392 (quantize_norm :404-409): one token row. */
+hipError_t quantize_norm(hipStream_t stream, const float* input, const float* aux, int n, float eps, int splits,
+                         int8_t* q8_out, int32_t* xsum_out, float* scale_out);
+hipError_t quantize_norm_wide(hipStream_t stream, const float* input, const float* aux, int n, float eps,
+                              int splits, int8_t* q8_out, int32_t* xsum_out, float* scale_out);
+
+/* QUANT_TILE_ARGS of ternary.cu:632-634 (quantize_tile_* :652-669): TILE
+ * token rows, row t read from input + t*in_stride; q8 row stride
+ * ceil(n/64)*64, xsum row stride ceil(n/64). */
+#define IVONAR_QUANT_TILE_ARGS                                                                           \
+  const float *input, int in_stride, const float *aux, int n, float eps, int splits, int8_t *q8_out, \
+      int32_t *xsum_out, float *scale_out
+hipError_t quantize_tile_plain(hipStream_t stream, IVONAR_QUANT_TILE_ARGS);
+hipError_t quantize_tile_plain_wide(hipStream_t stream, IVONAR_QUANT_TILE_ARGS);
+hipError_t quantize_tile_norm(hipStream_t stream, IVONAR_QUANT_TILE_ARGS);
+hipError_t quantize_tile_norm_wide(hipStream_t stream, IVONAR_QUANT_TILE_ARGS);
+hipError_t quantize_tile_attn(hipStream_t stream, IVONAR_QUANT_TILE_ARGS);
+hipError_t quantize_tile_attn_wide(hipStream_t stream, IVONAR_QUANT_TILE_ARGS);
+
+/* Same quantizer for an explicit row count m and mode (0 PLAIN, 1 NORM,
+ * 2 ATTN); the reference launches its tile quantizers with grid = m
+ * (kernel_decoder.py:370-386). */
+hipError_t ivonar_quantize_rows(hipStream_t stream, int mode, const float* input, int in_stride, const float* aux,
+                                int n, float eps, int splits, int m, int8_t* q8_out, int32_t* xsum_out,
+                                float* scale_out);
+
+/* ---------------------------------------------------------- token GEMM
+ * GEMM_ARGS of ternary.cu:671-674 (gemm_tile_* :767-784): m token rows of
+ * pre-quantized activations against `rows` weight rows on int8 MFMA; output
+ * row t at output + t*out_stride. */
+#define IVONAR_GEMM_ARGS                                                                                      \
+  const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, const uint8_t *packed,              \
+      const uint16_t *scales, const float *bias, float *output, int rows, int n, int row_bytes, int groups, \
+      int lanes, int out_stride, int m
+hipError_t gemm_tile_store(hipStream_t stream, IVONAR_GEMM_ARGS);
+hipError_t gemm_tile_residual(hipStream_t stream, IVONAR_GEMM_ARGS);
+hipError_t gemm_tile_silu_pair(hipStream_t stream, IVONAR_GEMM_ARGS);
+hipError_t gemm_tile_store_wide(hipStream_t stream, IVONAR_GEMM_ARGS);
+hipError_t gemm_tile_residual_wide(hipStream_t stream, IVONAR_GEMM_ARGS);
+hipError_t gemm_tile_silu_pair_wide(hipStream_t stream, IVONAR_GEMM_ARGS);
+
+/* ------------------------------------------------------------- embedding */
+
+/* ternary.cu:411-419: output[i] = (code[token, i] - 1) * scale[token, i/128]. */
+hipError_t embed_token(hipStream_t stream, const int64_t* token, const uint8_t* packed, const uint16_t* scales,
+                       float* output, int n, int row_bytes, int groups);
+/* ternary.cu:613-622: m token rows into output [m, n]. */
+hipError_t embed_tile(hipStream_t stream, const int64_t* tokens, const uint8_t* packed, const uint16_t* scales,
+                      float* output, int n, int row_bytes, int groups, int m);
+/* ternary.cu:624-630: output = tile[max(*valid - 1, 0)]. */
+hipError_t gather_token(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid);
+
+/* Greedy token: first index of the maximum of values[0..n) (no reference
+ * counterpart as a kernel; the reference's greedy sampler is top_k = 1 of
+ * sample_token, ternary.cu:1099-1337). */
+hipError_t ivonar_argmax(hipStream_t stream, const float* values, int n, int64_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IVONAR_TERNARY_H */

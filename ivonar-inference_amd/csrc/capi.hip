@@ -1,0 +1,343 @@
+// C-ABI entry points (declared in include/ivonar_ternary.h): argument checks,
+// process defines, the per-device scratch, and dispatch to the launchers.
+#include <stdint.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "../../include/ivonar_ternary.h"
+#include "internal.hpp"
+#include "ternary_device.hpp"
+
+namespace ivo {
+
+Defines& defines() {
+  static Defines values;
+  return values;
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kScratchChunks = 16384;  // rows up to 1,048,576 inputs
+std::mutex g_scratch_lock;
+Scratch g_scratch[kMaxDevices];
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+hipError_t allocate_scratch(int device) {
+  Scratch& s = g_scratch[device];
+  if (s.q8 != nullptr) return hipSuccess;
+  void* q8 = nullptr;
+  void* xsum = nullptr;
+  void* scale = nullptr;
+  hipError_t status = hipMalloc(&q8, (size_t)kScratchChunks * kChunk);
+  if (status == hipSuccess) status = hipMalloc(&xsum, (size_t)kScratchChunks * sizeof(int32_t));
+  if (status == hipSuccess) status = hipMalloc(&scale, 256);
+  if (status != hipSuccess) {
+    if (q8) (void)hipFree(q8);
+    if (xsum) (void)hipFree(xsum);
+    return status;
+  }
+  s.q8 = static_cast<int8_t*>(q8);
+  s.xsum = static_cast<int32_t*>(xsum);
+  s.scale = static_cast<float*>(scale);
+  s.capacity_chunks = kScratchChunks;
+  return hipSuccess;
+}
+
+// Checks shared by the GEMV and GEMM entry points.
+hipError_t check_matrix(const uint8_t* packed, const uint16_t* scales, int rows, int n, int row_bytes, int groups) {
+  if (rows < 0 || n <= 0 || packed == nullptr || scales == nullptr) return hipErrorInvalidValue;
+  const int chunks = ceil_div(n, kChunk);
+  if (row_bytes < chunks * 16 || (row_bytes & 15) != 0 || !aligned16(packed)) return hipErrorInvalidValue;
+  if (groups < ceil_div(n, kGroup)) return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, const float* input, const float* aux,
+                      const int8_t* q8_in, const int32_t* xsum_in, const float* scale_in, const uint8_t* packed,
+                      const uint16_t* scales, const float* bias, float* output, int rows, int n, int row_bytes,
+                      int groups, int splits, float eps) {
+  hipError_t status = check_matrix(packed, scales, rows, n, row_bytes, groups);
+  if (status != hipSuccess) return status;
+  if (output == nullptr) return hipErrorInvalidValue;
+  if (epi == kSiluPair && (rows & 1) != 0) return hipErrorInvalidValue;
+  if (prequant) {
+    if (q8_in == nullptr || xsum_in == nullptr || scale_in == nullptr || !aligned16(q8_in))
+      return hipErrorInvalidValue;
+  } else {
+    if (input == nullptr) return hipErrorInvalidValue;
+    if (mode == kNorm && aux == nullptr) return hipErrorInvalidValue;
+    if (mode == kAttn && (splits <= 0 || n % defines().head_dim != 0)) return hipErrorInvalidValue;
+  }
+  GemvArgs a{};
+  a.mode = mode;
+  a.epi = epi;
+  a.input = input;
+  a.aux = aux;
+  a.q8_in = prequant ? q8_in : nullptr;
+  a.xsum_in = prequant ? xsum_in : nullptr;
+  a.scale_in = prequant ? scale_in : nullptr;
+  a.packed = packed;
+  a.scales = scales;
+  a.bias = bias;
+  a.output = output;
+  a.partials = nullptr;
+  a.rows = rows;
+  a.n = n;
+  a.row_bytes = row_bytes;
+  a.groups = groups;
+  a.splits = splits > 0 ? splits : 1;
+  a.eps = eps;
+  a.head_dim = defines().head_dim;
+  return launch_gemv(stream, a);
+}
+
+hipError_t quant_entry(hipStream_t stream, int mode, const float* input, int in_stride, const float* aux, int n,
+                       float eps, int splits, int m, int8_t* q8_out, int32_t* xsum_out, float* scale_out) {
+  if (n <= 0 || m < 0 || input == nullptr || q8_out == nullptr || xsum_out == nullptr || scale_out == nullptr)
+    return hipErrorInvalidValue;
+  if (!aligned16(q8_out) || ((uintptr_t)xsum_out & 3u) != 0) return hipErrorInvalidValue;
+  if (mode == kNorm && aux == nullptr) return hipErrorInvalidValue;
+  if (mode == kAttn && (splits <= 0 || n % defines().head_dim != 0)) return hipErrorInvalidValue;
+  if (mode < kPlain || mode > kAttn) return hipErrorInvalidValue;
+  if (m > 1 && in_stride < (mode == kAttn ? 1 : n)) return hipErrorInvalidValue;
+  QuantArgs q{mode, input, in_stride, aux, n, eps, splits > 0 ? splits : 1, defines().head_dim, m,
+              q8_out, xsum_out, scale_out};
+  return launch_quantize(stream, q);
+}
+
+hipError_t gemm_entry(hipStream_t stream, int epi, const int8_t* q8_in, const int32_t* xsum_in,
+                      const float* scale_in, const uint8_t* packed, const uint16_t* scales, const float* bias,
+                      float* output, int rows, int n, int row_bytes, int groups, int out_stride, int m) {
+  hipError_t status = check_matrix(packed, scales, rows, n, row_bytes, groups);
+  if (status != hipSuccess) return status;
+  if (m < 0 || q8_in == nullptr || xsum_in == nullptr || scale_in == nullptr || output == nullptr)
+    return hipErrorInvalidValue;
+  if (!aligned16(q8_in)) return hipErrorInvalidValue;
+  if (epi == kSiluPair && (rows & 1) != 0) return hipErrorInvalidValue;
+  const int width = epi == kSiluPair ? rows / 2 : rows;
+  if (m > 1 && out_stride < width) return hipErrorInvalidValue;
+  GemmArgs a{epi, q8_in, xsum_in, scale_in, packed, scales, bias, output, rows, n, row_bytes, groups, out_stride, m};
+  return launch_gemm(stream, a);
+}
+
+}  // namespace
+
+hipError_t init_device(int device) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  int current = 0;
+  hipError_t status = hipGetDevice(&current);
+  if (status != hipSuccess) return status;
+  if (current != device) {
+    status = hipSetDevice(device);
+    if (status != hipSuccess) return status;
+  }
+  status = allocate_scratch(device);
+  if (current != device) (void)hipSetDevice(current);
+  return status;
+}
+
+hipError_t scratch_for_stream(hipStream_t stream, Scratch** out) {
+  int device = 0;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) return status;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch[device].q8 == nullptr) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    status = hipStreamIsCapturing(stream, &capture);
+    if (status != hipSuccess) return status;
+    if (capture != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+    status = allocate_scratch(device);
+    if (status != hipSuccess) return status;
+  }
+  *out = &g_scratch[device];
+  return hipSuccess;
+}
+
+}  // namespace ivo
+
+using namespace ivo;
+
+extern "C" {
+
+hipError_t ivonar_init(int device) { return init_device(device); }
+
+hipError_t ivonar_define(const char* name, int value) {
+  if (name == nullptr || value <= 0) return hipErrorInvalidValue;
+  if (strcmp(name, "HEAD_DIM") == 0) defines().head_dim = value;
+  else if (strcmp(name, "TILE") == 0) defines().tile = value;
+  else if (strcmp(name, "MAX_CHUNKS") == 0) defines().max_chunks = value;
+  else return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+const char* ivonar_error_string(hipError_t status) { return hipGetErrorString(status); }
+
+int ivonar_abi_version(void) { return IVONAR_ABI_VERSION; }
+
+void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane) { gemv_plan(rows, n, lanes, rows_per_lane); }
+
+#define GEMV_PASS_ENTRY(MODE, EPI, PREQUANT)                                                                      \
+  gemv_entry(stream, MODE, EPI, PREQUANT, input, aux, q8_in, xsum_in, scale_in, packed, scales, bias, output, rows, \
+             n, row_bytes, groups, splits, eps)
+#define GEMV_UNUSED \
+  (void)lanes;      \
+  (void)next;       \
+  (void)next_bytes
+
+hipError_t gemv_plain_store(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kPlain, kStore, false);
+}
+hipError_t gemv_plain_residual(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kPlain, kResidual, false);
+}
+hipError_t gemv_norm_store(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kNorm, kStore, false);
+}
+hipError_t gemv_norm_silu_pair(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kNorm, kSiluPair, false);
+}
+hipError_t gemv_attn_residual(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kAttn, kResidual, false);
+}
+hipError_t gemv_prequant_store(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kPlain, kStore, true);
+}
+hipError_t gemv_plain_store_wide(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kPlain, kStore, false);
+}
+hipError_t gemv_plain_residual_wide(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kPlain, kResidual, false);
+}
+hipError_t gemv_norm_store_wide(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kNorm, kStore, false);
+}
+hipError_t gemv_norm_silu_pair_wide(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kNorm, kSiluPair, false);
+}
+hipError_t gemv_attn_residual_wide(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  return GEMV_PASS_ENTRY(kAttn, kResidual, false);
+}
+
+hipError_t gemv_group_partials(hipStream_t stream, const int8_t* q8_in, const int32_t* xsum_in,
+                               const uint8_t* packed, int rows, int n, int row_bytes, int groups,
+                               int32_t* partials) {
+  static const uint16_t kNoScales = 0;
+  hipError_t status = check_matrix(packed, &kNoScales, rows, n, row_bytes, groups);
+  if (status != hipSuccess) return status;
+  if (q8_in == nullptr || xsum_in == nullptr || partials == nullptr || !aligned16(q8_in))
+    return hipErrorInvalidValue;
+  GemvArgs a{};
+  a.mode = kPlain;
+  a.epi = kPartials;
+  a.q8_in = q8_in;
+  a.xsum_in = xsum_in;
+  a.scale_in = nullptr;
+  a.packed = packed;
+  a.scales = nullptr;
+  a.partials = partials;
+  a.rows = rows;
+  a.n = n;
+  a.row_bytes = row_bytes;
+  a.groups = groups;
+  a.splits = 1;
+  a.head_dim = defines().head_dim;
+  return launch_gemv(stream, a);
+}
+
+hipError_t quantize_norm(hipStream_t stream, const float* input, const float* aux, int n, float eps, int splits,
+                         int8_t* q8_out, int32_t* xsum_out, float* scale_out) {
+  return quant_entry(stream, kNorm, input, n, aux, n, eps, splits, 1, q8_out, xsum_out, scale_out);
+}
+hipError_t quantize_norm_wide(hipStream_t stream, const float* input, const float* aux, int n, float eps,
+                              int splits, int8_t* q8_out, int32_t* xsum_out, float* scale_out) {
+  return quant_entry(stream, kNorm, input, n, aux, n, eps, splits, 1, q8_out, xsum_out, scale_out);
+}
+
+#define QUANT_TILE_PASS(MODE) \
+  quant_entry(stream, MODE, input, in_stride, aux, n, eps, splits, defines().tile, q8_out, xsum_out, scale_out)
+
+hipError_t quantize_tile_plain(hipStream_t stream, IVONAR_QUANT_TILE_ARGS) { return QUANT_TILE_PASS(kPlain); }
+hipError_t quantize_tile_plain_wide(hipStream_t stream, IVONAR_QUANT_TILE_ARGS) { return QUANT_TILE_PASS(kPlain); }
+hipError_t quantize_tile_norm(hipStream_t stream, IVONAR_QUANT_TILE_ARGS) { return QUANT_TILE_PASS(kNorm); }
+hipError_t quantize_tile_norm_wide(hipStream_t stream, IVONAR_QUANT_TILE_ARGS) { return QUANT_TILE_PASS(kNorm); }
+hipError_t quantize_tile_attn(hipStream_t stream, IVONAR_QUANT_TILE_ARGS) { return QUANT_TILE_PASS(kAttn); }
+hipError_t quantize_tile_attn_wide(hipStream_t stream, IVONAR_QUANT_TILE_ARGS) { return QUANT_TILE_PASS(kAttn); }
+
+hipError_t ivonar_quantize_rows(hipStream_t stream, int mode, const float* input, int in_stride, const float* aux,
+                                int n, float eps, int splits, int m, int8_t* q8_out, int32_t* xsum_out,
+                                float* scale_out) {
+  return quant_entry(stream, mode, input, in_stride, aux, n, eps, splits, m, q8_out, xsum_out, scale_out);
+}
+
+#define GEMM_PASS_ENTRY(EPI)                                                                                      \
+  gemm_entry(stream, EPI, q8_in, xsum_in, scale_in, packed, scales, bias, output, rows, n, row_bytes, groups, \
+             out_stride, m)
+
+hipError_t gemm_tile_store(hipStream_t stream, IVONAR_GEMM_ARGS) {
+  (void)lanes;
+  return GEMM_PASS_ENTRY(kStore);
+}
+hipError_t gemm_tile_residual(hipStream_t stream, IVONAR_GEMM_ARGS) {
+  (void)lanes;
+  return GEMM_PASS_ENTRY(kResidual);
+}
+hipError_t gemm_tile_silu_pair(hipStream_t stream, IVONAR_GEMM_ARGS) {
+  (void)lanes;
+  return GEMM_PASS_ENTRY(kSiluPair);
+}
+hipError_t gemm_tile_store_wide(hipStream_t stream, IVONAR_GEMM_ARGS) {
+  (void)lanes;
+  return GEMM_PASS_ENTRY(kStore);
+}
+hipError_t gemm_tile_residual_wide(hipStream_t stream, IVONAR_GEMM_ARGS) {
+  (void)lanes;
+  return GEMM_PASS_ENTRY(kResidual);
+}
+hipError_t gemm_tile_silu_pair_wide(hipStream_t stream, IVONAR_GEMM_ARGS) {
+  (void)lanes;
+  return GEMM_PASS_ENTRY(kSiluPair);
+}
+
+hipError_t embed_token(hipStream_t stream, const int64_t* token, const uint8_t* packed, const uint16_t* scales,
+                       float* output, int n, int row_bytes, int groups) {
+  if (token == nullptr || packed == nullptr || scales == nullptr || output == nullptr || n <= 0 ||
+      row_bytes < ceil_div(n, 4) || groups < ceil_div(n, kGroup))
+    return hipErrorInvalidValue;
+  return launch_embed(stream, token, 1, packed, scales, output, n, row_bytes, groups);
+}
+
+hipError_t embed_tile(hipStream_t stream, const int64_t* tokens, const uint8_t* packed, const uint16_t* scales,
+                      float* output, int n, int row_bytes, int groups, int m) {
+  if (tokens == nullptr || packed == nullptr || scales == nullptr || output == nullptr || n <= 0 || m < 0 ||
+      row_bytes < ceil_div(n, 4) || groups < ceil_div(n, kGroup))
+    return hipErrorInvalidValue;
+  return launch_embed(stream, tokens, m, packed, scales, output, n, row_bytes, groups);
+}
+
+hipError_t gather_token(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid) {
+  if (tile == nullptr || output == nullptr || valid == nullptr || n <= 0) return hipErrorInvalidValue;
+  return launch_gather(stream, tile, output, n, valid);
+}
+
+hipError_t ivonar_argmax(hipStream_t stream, const float* values, int n, int64_t* out) {
+  if (values == nullptr || out == nullptr || n <= 0) return hipErrorInvalidValue;
+  return launch_argmax(stream, values, n, out);
+}
+
+}  // extern "C"

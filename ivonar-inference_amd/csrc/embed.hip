@@ -1,0 +1,97 @@
+// Ternary row decode for the tied embedding (reference: kernels/ternary.cu
+// embed_token :411-419, embed_tile :613-622, gather_token :624-630) and the
+// greedy argmax used by the decode driver.
+#include "internal.hpp"
+#include "ternary_device.hpp"
+
+namespace ivo {
+namespace {
+
+// out[t, i] = (code[tokens[t], i] - 1) * scale[tokens[t], i / 128]; exact.
+__global__ __launch_bounds__(kThreads) void embed_kernel(const int64_t* __restrict__ tokens,
+                                                         const uint8_t* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         float* __restrict__ output, int n, int row_bytes,
+                                                         int groups) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const size_t row = (size_t)tokens[t];
+  const int code = (packed[row * row_bytes + (i >> 2)] >> ((i & 3) * 2)) & 3;
+  output[(size_t)t * n + i] = (float)(code - 1) * h2f(scales[row * groups + (i >> 7)]);
+}
+
+__global__ __launch_bounds__(kThreads) void gather_kernel(const float* __restrict__ tile, float* __restrict__ output,
+                                                          int n, const int64_t* __restrict__ valid) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const long long last = *valid - 1;
+  const size_t t = last > 0 ? (size_t)last : 0;
+  output[i] = tile[t * n + i];
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+// First index of the maximum over n values (one block).
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ values, int n,
+                                                                 int64_t* __restrict__ out) {
+  __shared__ float best_value[kArgmaxThreads / 64];
+  __shared__ int best_index[kArgmaxThreads / 64];
+  float value = -__builtin_inff();
+  int index = n;
+  for (int i = threadIdx.x; i < n; i += kArgmaxThreads) {
+    const float v = values[i];
+    if (v > value || (v == value && i < index)) {
+      value = v;
+      index = i;
+    }
+  }
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const float other = __shfl_xor(value, offset);
+    const int other_index = __shfl_xor(index, offset);
+    if (other > value || (other == value && other_index < index)) {
+      value = other;
+      index = other_index;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    best_value[threadIdx.x >> 6] = value;
+    best_index[threadIdx.x >> 6] = index;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = best_value[0];
+    int k = best_index[0];
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) {
+      if (best_value[w] > v || (best_value[w] == v && best_index[w] < k)) {
+        v = best_value[w];
+        k = best_index[w];
+      }
+    }
+    *out = k < n ? k : 0;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const uint8_t* packed,
+                        const uint16_t* scales, float* output, int n, int row_bytes, int groups) {
+  if (m <= 0 || n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(n, kThreads), m), dim3(kThreads), 0, stream, tokens, packed, scales,
+                     output, n, row_bytes, groups);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_kernel, dim3(ceil_div(n, kThreads)), dim3(kThreads), 0, stream, tile, output, n, valid);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(hipStream_t stream, const float* values, int n, int64_t* out) {
+  if (n <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, stream, values, n, out);
+  return hipGetLastError();
+}
+
+}  // namespace ivo

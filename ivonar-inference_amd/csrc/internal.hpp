@@ -1,0 +1,99 @@
+// Host-side launchers shared by the C-ABI entry points (capi.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ivo {
+
+// Process-wide values the reference passes as compile-time defines
+// (kernel_decoder.py:215): HEAD_DIM for the ATTN prologue, TILE for the
+// token count of the quantize_tile_* entry points, MAX_CHUNKS (capacity of
+// the caller's q8 buffers, used only for argument checks).
+struct Defines {
+  int head_dim = 64;
+  int tile = 32;
+  int max_chunks = 70;
+};
+Defines& defines();
+
+// Per-device activation scratch for the two-pass GEMV (quantize, then GEMV).
+struct Scratch {
+  int8_t* q8 = nullptr;
+  int32_t* xsum = nullptr;
+  float* scale = nullptr;
+  int capacity_chunks = 0;
+};
+hipError_t scratch_for_stream(hipStream_t stream, Scratch** out);
+hipError_t init_device(int device);
+
+struct QuantArgs {
+  int mode;
+  const float* input;
+  int in_stride;
+  const float* aux;
+  int n;
+  float eps;
+  int splits;
+  int head_dim;
+  int m;
+  int8_t* q8;
+  int32_t* xsum;
+  float* scale;
+};
+hipError_t launch_quantize(hipStream_t stream, const QuantArgs& a);
+
+struct GemvArgs {
+  int mode;    // kPlain / kNorm / kAttn (ignored when q8_in is set)
+  int epi;     // kStore / kResidual / kSiluPair / kPartials
+  const float* input;
+  const float* aux;
+  const int8_t* q8_in;  // pre-quantized activations (q8 layout) or null
+  const int32_t* xsum_in;
+  const float* scale_in;
+  const uint8_t* packed;
+  const uint16_t* scales;
+  const float* bias;
+  float* output;
+  int32_t* partials;  // kPartials only: int32 [rows, groups]
+  int rows;
+  int n;
+  int row_bytes;
+  int groups;
+  int splits;
+  float eps;
+  int head_dim;
+};
+hipError_t launch_gemv(hipStream_t stream, const GemvArgs& a);
+
+// Lane layout the decode GEMV uses for a K-wide row (also defines its fp32
+// summation order): lanes per row (power of two in [2, 64]) and rows per lane.
+void gemv_plan(int rows, int n, int* lanes, int* rows_per_lane);
+int gemv_fused_limit();
+
+struct GemmArgs {
+  int epi;  // kStore / kResidual / kSiluPair
+  const int8_t* q8_in;
+  const int32_t* xsum_in;
+  const float* scale_in;
+  const uint8_t* packed;
+  const uint16_t* scales;
+  const float* bias;
+  float* output;
+  int rows;
+  int n;
+  int row_bytes;
+  int groups;
+  int out_stride;
+  int m;
+};
+hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a);
+
+hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const uint8_t* packed,
+                        const uint16_t* scales, float* output, int n, int row_bytes, int groups);
+hipError_t launch_gather(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid);
+hipError_t launch_argmax(hipStream_t stream, const float* values, int n, int64_t* out);
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace ivo

@@ -1,0 +1,206 @@
+// Device-side building blocks shared by the ternary kernels (gfx950, wave64).
+//
+// Packed weights (reference format, quantization.py:10-18): row r of a
+// matrix holds ceil(K/4) bytes padded to a multiple of 16 (row_bytes); byte b
+// carries inputs 4b..4b+3, input 4b+k in bits 2k..2k+1 as code = w + 1 with
+// w in {-1, 0, +1}.  One fp16 scale per 128 inputs, scales[r * groups + g].
+//
+// Activation scratch ("q8 layout", private to this library): token row t
+// holds C = ceil(K/64) chunks of 64 int8 (t * C * 64), zero padded past K.
+// Inside chunk u, the 16-byte quad w covers inputs 64u+16w .. 64u+16w+15 and
+// its 32-bit word k holds inputs {16w+k, 16w+4+k, 16w+8+k, 16w+12+k}, so
+// (packed_word >> 2k) & 0x03030303 lines up byte for byte with word k.
+// xsum[t * C + u] is the int32 sum of chunk u; scale[t] the fp32 token scale.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ivo {
+
+constexpr int kThreads = 256;  // every kernel here runs 256-thread blocks (4 waves)
+constexpr int kChunk = 64;
+constexpr int kGroup = 128;
+constexpr unsigned kLow2 = 0x03030303u;
+
+enum Mode : int { kPlain = 0, kNorm = 1, kAttn = 2 };
+enum Epi : int { kStore = 0, kResidual = 1, kSiluPair = 2, kPartials = 3 };
+
+__device__ __forceinline__ float h2f(uint16_t bits) {
+  _Float16 h;
+  __builtin_memcpy(&h, &bits, 2);
+  return (float)h;
+}
+
+// exp(x): Cody-Waite reduction x = n*ln2 + r, degree-7 Taylor polynomial of
+// e^r in Horner form, scaling by 2^n in two exact steps.  Every operation is
+// an explicit IEEE fp32 op, so the CPU oracle reproduces it bit for bit.
+__device__ __forceinline__ float ivo_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(n, -0.693145751953125f, x);
+  r = __builtin_fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.9841270113829523e-04f;
+  p = __builtin_fmaf(p, r, 1.3888889225199819e-03f);
+  p = __builtin_fmaf(p, r, 8.3333337679505348e-03f);
+  p = __builtin_fmaf(p, r, 4.1666667908430099e-02f);
+  p = __builtin_fmaf(p, r, 1.6666667163372040e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int n1 = ni / 2, n2 = ni - n1;
+  const float s1 = __int_as_float((n1 + 127) << 23);
+  const float s2 = __int_as_float((n2 + 127) << 23);
+  return (p * s1) * s2;
+}
+
+__device__ __forceinline__ float ivo_silu(float x) { return x / (1.0f + ivo_expf(-x)); }
+
+__device__ __forceinline__ int sdot4(unsigned a, int b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, b, c, false);
+}
+
+// Sum over one 64-input chunk of code * q: 16 packed words against 16 q8 words.
+__device__ __forceinline__ int chunk_code_dot(const uint4 w, const int4 q0, const int4 q1, const int4 q2,
+                                              const int4 q3, int acc) {
+  acc = sdot4(w.x & kLow2, q0.x, acc);
+  acc = sdot4((w.x >> 2) & kLow2, q0.y, acc);
+  acc = sdot4((w.x >> 4) & kLow2, q0.z, acc);
+  acc = sdot4((w.x >> 6) & kLow2, q0.w, acc);
+  acc = sdot4(w.y & kLow2, q1.x, acc);
+  acc = sdot4((w.y >> 2) & kLow2, q1.y, acc);
+  acc = sdot4((w.y >> 4) & kLow2, q1.z, acc);
+  acc = sdot4((w.y >> 6) & kLow2, q1.w, acc);
+  acc = sdot4(w.z & kLow2, q2.x, acc);
+  acc = sdot4((w.z >> 2) & kLow2, q2.y, acc);
+  acc = sdot4((w.z >> 4) & kLow2, q2.z, acc);
+  acc = sdot4((w.z >> 6) & kLow2, q2.w, acc);
+  acc = sdot4(w.w & kLow2, q3.x, acc);
+  acc = sdot4((w.w >> 2) & kLow2, q3.y, acc);
+  acc = sdot4((w.w >> 4) & kLow2, q3.z, acc);
+  acc = sdot4((w.w >> 6) & kLow2, q3.w, acc);
+  return acc;
+}
+
+// Lane value of the partner in the same lane pair (quad_perm [1,0,3,2]).
+__device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));
+  return v;
+}
+
+// Block-wide max over the 4 waves; every thread gets the result.
+__device__ __forceinline__ float block_max(float v, float* slots) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float peak = fmaxf(fmaxf(slots[0], slots[1]), fmaxf(slots[2], slots[3]));
+  __syncthreads();
+  return peak;
+}
+
+// The reference kernel's reduction tree for a sum of squares over a 256-thread
+// block (ternary.cu:157-170, :81-84, :101-109): strided per-thread fma
+// partials, xor butterfly inside each 32-lane half (offsets 16..1), then the
+// eight half-wave totals added in order.
+template <class Value>
+__device__ __forceinline__ float tree_sum_squares(const Value& value_at, int n, float* slots) {
+  const int tid = threadIdx.x;
+  float s = 0.0f;
+  for (int i = tid; i < n; i += kThreads) {
+    const float v = value_at(i);
+    s = __builtin_fmaf(v, v, s);
+  }
+  for (int offset = 16; offset > 0; offset >>= 1) s = s + __shfl_xor(s, offset);
+  if ((tid & 31) == 0) slots[tid >> 5] = s;
+  __syncthreads();
+  float total = 0.0f;
+  for (int w = 0; w < kThreads / 32; ++w) total = total + slots[w];
+  __syncthreads();
+  return total;
+}
+
+// Source value of input i (ternary.cu:128-146 for the split-softmax merge).
+template <int MODE>
+__device__ __forceinline__ float source_value(const float* __restrict__ input, int i, int splits, int head_dim) {
+  if constexpr (MODE == kAttn) {
+    const int stride = head_dim + 2;
+    const int head = i / head_dim, dim = i - head * head_dim;
+    const float* base = input + (size_t)head * splits * stride;
+    float peak = -__builtin_inff();
+    for (int s = 0; s < splits; ++s) peak = fmaxf(peak, base[s * stride]);
+    float total = 0.0f, value = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+      const float* part = base + s * stride;
+      const float weight = part[0] == -__builtin_inff() ? 0.0f : ivo_expf(part[0] - peak);
+      total = __builtin_fmaf(weight, part[1], total);
+      value = __builtin_fmaf(weight, part[2 + dim], value);
+    }
+    return value / total;
+  } else {
+    return input[i];
+  }
+}
+
+// Everything a block needs to quantize one token row.
+struct RowSource {
+  const float* input;  // row start
+  const float* aux;    // NORM weights (may be null otherwise)
+  int n;
+  float eps;
+  int splits;
+  int head_dim;
+};
+
+// Per-row prologue shared by all quantizing kernels: returns the token scale
+// and, for NORM, sets inv_rms.  All 256 threads must call it.
+template <int MODE>
+__device__ __forceinline__ float row_scale(const RowSource& src, float& inv_rms, float* slots) {
+  inv_rms = 1.0f;
+  if constexpr (MODE == kNorm) {
+    const float* x = src.input;
+    const float squares = tree_sum_squares([&](int i) { return x[i]; }, src.n, slots);
+    inv_rms = 1.0f / __builtin_sqrtf(squares / (float)src.n + src.eps);
+  }
+  float amax = 0.0f;
+  for (int i = threadIdx.x; i < src.n; i += kThreads) {
+    float v = source_value<MODE>(src.input, i, src.splits, src.head_dim);
+    if constexpr (MODE == kNorm) v = fminf(fmaxf(v * inv_rms, -8.0f), 8.0f) * src.aux[i];
+    amax = fmaxf(amax, fabsf(v));
+  }
+  amax = block_max(amax, slots + 32);
+  return fmaxf(amax / 127.0f, 1e-5f);
+}
+
+// q8 word (chunk u, quad w, field k) of one token: 4 quantized inputs.
+template <int MODE>
+__device__ __forceinline__ int quantize_word(const RowSource& src, int u, int w, int k, float inv_rms, float scale) {
+  unsigned word = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int i = u * kChunk + w * 16 + 4 * b + k;
+    int q = 0;
+    if (i < src.n) {
+      float v = source_value<MODE>(src.input, i, src.splits, src.head_dim);
+      if constexpr (MODE == kNorm) v = fminf(fmaxf(v * inv_rms, -8.0f), 8.0f) * src.aux[i];
+      q = (int)__builtin_rintf(v / scale);
+    }
+    word |= ((unsigned)q & 0xffu) << (8 * b);
+  }
+  return (int)word;
+}
+
+// Sum of the four int8 lanes of a word.
+__device__ __forceinline__ int word_sum(int word) { return sdot4((unsigned)word, 0x01010101, 0); }
+
+// Sum over the 16 consecutive lanes that hold one chunk's 16 words.
+__device__ __forceinline__ int chunk_lane_sum(int v) {
+  for (int offset = 1; offset < 16; offset <<= 1) v += __shfl_xor(v, offset);
+  return v;
+}
+
+}  // namespace ivo

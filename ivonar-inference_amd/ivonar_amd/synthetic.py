@@ -1,0 +1,133 @@
+"""Seeded synthetic ternary layers and activations for the benchmark workloads.
+
+There are no checkpoints here, so every workload uses random-init packed
+weights with the stated statistics.  Codes are drawn categorically over
+{0, 1, 2} (code = w + 1) and packed four per byte in the reference layout;
+fp16 group scales that would round to zero are raised to the smallest
+positive fp16 value, since packed checkpoints require positive scales
+(reference loader.py:106-112).  Generators are numpy PCG64 streams seeded by
+the workload number.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+GROUP = 128
+SMALLEST_HALF = np.float16(np.finfo(np.float16).smallest_subnormal)
+
+
+@dataclass
+class Layer:
+    """One packed ternary matrix on the host: packed uint8 [N, ceil(K/4)], fp16 scales [N, G]."""
+
+    packed: np.ndarray
+    scales: np.ndarray
+    in_features: int
+    bias: np.ndarray | None = None
+
+    @property
+    def rows(self) -> int:
+        return int(self.packed.shape[0])
+
+    @property
+    def scale_bits(self) -> np.ndarray:
+        return self.scales.view(np.uint16)
+
+
+def sample_codes(rng: np.random.Generator, rows: int, k: int, p=(0.3, 0.4, 0.3)) -> np.ndarray:
+    """uint8 codes [rows, k] with P(code 0, 1, 2) = p (w = code - 1)."""
+    u = rng.random((rows, k), dtype=np.float32)
+    return ((u >= np.float32(p[0])).astype(np.uint8) + (u >= np.float32(p[0] + p[1])).astype(np.uint8))
+
+
+def pack_codes(codes: np.ndarray) -> np.ndarray:
+    rows, k = codes.shape
+    width = math.ceil(k / 4)
+    if k % 4:
+        codes = np.concatenate([codes, np.ones((rows, width * 4 - k), dtype=np.uint8)], axis=1)
+    q = codes.reshape(rows, width, 4)
+    return (q[..., 0] | (q[..., 1] << 2) | (q[..., 2] << 4) | (q[..., 3] << 6)).astype(np.uint8)
+
+
+def to_half_scales(values: np.ndarray) -> np.ndarray:
+    half = values.astype(np.float16)
+    return np.where(half > 0, half, SMALLEST_HALF).astype(np.float16)
+
+
+def abs_normal_scales(rng: np.random.Generator, rows: int, groups: int, sigma: float, offset: float = 0.0):
+    return to_half_scales(np.abs(rng.normal(0.0, sigma, size=(rows, groups))) + offset)
+
+
+def lognormal_scales(rng: np.random.Generator, rows: int, groups: int, mu: float, sigma: float):
+    return to_half_scales(np.exp(rng.normal(mu, sigma, size=(rows, groups))))
+
+
+def ternary_layer(
+    rng: np.random.Generator, rows: int, k: int, p=(0.3, 0.4, 0.3), scale: str = "abs_normal", sigma: float = 0.02,
+    offset: float = 1e-4, mu: float = -4.0, with_codes: bool = False,
+):
+    """A packed layer; with_codes also returns the uint8 codes [rows, k]."""
+    codes = sample_codes(rng, rows, k, p)
+    groups = math.ceil(k / GROUP)
+    if scale == "lognormal":
+        scales = lognormal_scales(rng, rows, groups, mu, sigma)
+    else:
+        scales = abs_normal_scales(rng, rows, groups, sigma, offset)
+    layer = Layer(pack_codes(codes), scales, k)
+    return (layer, codes) if with_codes else layer
+
+
+# Workloads -----------------------------------------------------------------
+
+GEMV_SHAPE = (1024, 4096)  # single ternary linear at M=1: K -> N
+STRESS_SHAPES = ((8192, 28672), (28672, 8192))  # large-shape HBM stress at M=1
+PREFILL_SHAPES = ((1024, 4096), (4096, 1024))  # prefill tile GEMM shapes
+SWEEP_SHAPE = (4096, 14336)
+SWEEP_M = (1, 2, 4, 8, 16, 32, 64, 128, 512, 2048)
+
+
+def single_linear(seed: int = 0):
+    """K=1024 -> N=4096, p=(0.3,0.4,0.3), scale |N(0,0.02)|+1e-4, x ~ N(0,1) [1, 1024]."""
+    rng = np.random.default_rng(seed)
+    k, n = GEMV_SHAPE
+    layer = ternary_layer(rng, n, k, sigma=0.02, offset=1e-4)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    return layer, x
+
+
+def stress_layers(seed: int = 3):
+    """8192->28672 and 28672->8192, scale |N(0,0.01)|, x ~ N(0,1)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for k, n in STRESS_SHAPES:
+        layer = ternary_layer(rng, n, k, sigma=0.01, offset=0.0)
+        out.append((layer, rng.standard_normal((1, k)).astype(np.float32)))
+    return out
+
+
+def prefill_activations(rng: np.random.Generator, length: int, k: int, outlier_fraction: float = 0.01):
+    """N(0,1) [length, k] with a fixed 1% of channels scaled by 20."""
+    x = rng.standard_normal((length, k)).astype(np.float32)
+    channels = np.sort(np.random.default_rng(1000 + k).choice(k, max(1, int(k * outlier_fraction)), replace=False))
+    x[:, channels] *= np.float32(20.0)
+    return x
+
+
+def prefill_layers(seed: int = 2):
+    rng = np.random.default_rng(seed)
+    return [(ternary_layer(rng, n, k, sigma=0.02, offset=1e-4), k) for k, n in PREFILL_SHAPES]
+
+
+def sweep_layer(seed: int = 4):
+    """4096->14336 with p(0)=0.6, p(+-1)=0.2, lognormal(-4, 0.5) scales."""
+    rng = np.random.default_rng(seed)
+    k, n = SWEEP_SHAPE
+    return ternary_layer(rng, n, k, p=(0.2, 0.6, 0.2), scale="lognormal", mu=-4.0, sigma=0.5), rng
+
+
+def student_t(rng: np.random.Generator, shape, dof: float = 3.0) -> np.ndarray:
+    return rng.standard_t(dof, size=shape).astype(np.float32)

@@ -1,0 +1,69 @@
+"""Shared helpers for the parity tests: host layers, device matrices and oracle calls."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+RTOL, ATOL = 1e-5, 1e-6  # fp32 output tolerance against the reference's order and the fp64 truth
+
+
+def make_layer(rng: np.random.Generator, rows: int, k: int, p=(0.3, 0.4, 0.3), sigma: float = 0.02,
+               bias: bool = False):
+    """(codes uint8 [rows,k], packed16 uint8 [rows, rb16], scale bits uint16 [rows,G], bias or None)."""
+    import ternary_oracle as T
+
+    u = rng.random((rows, k))
+    codes = ((u >= p[0]).astype(np.uint8) + (u >= p[0] + p[1]).astype(np.uint8))
+    packed = T.pad_rows16(T.pack_codes(codes))
+    groups = math.ceil(k / 128)
+    scales = (np.abs(rng.normal(0.0, sigma, size=(rows, groups))) + 1e-4).astype(np.float16)
+    b = (rng.normal(0.0, 0.02, size=rows)).astype(np.float32) if bias else None
+    return codes, packed, scales.view(np.uint16), b
+
+
+def device_matrix(packed16: np.ndarray, scale_bits: np.ndarray, k: int, bias=None, device=None):
+    import torch
+    from ivonar_amd.matrix import Matrix
+
+    packed_t = torch.from_numpy(np.ascontiguousarray(packed16))
+    scales_t = torch.from_numpy(np.ascontiguousarray(scale_bits)).view(torch.float16)
+    bias_t = None if bias is None else torch.from_numpy(bias)
+    return Matrix.from_tensors(packed_t, scales_t, k, bias_t, device=device)
+
+
+def reference_lanes(k: int, rows: int, max_lanes: int = 32) -> int:
+    from ivonar_amd.matrix import _lanes_for
+
+    return _lanes_for((k + 63) // 64, rows, max_lanes)
+
+
+def to_np(tensor) -> np.ndarray:
+    return tensor.detach().cpu().numpy()
+
+
+def assert_within(actual, expected, rtol: float = RTOL, atol: float = ATOL, what: str = "") -> None:
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    bad = np.abs(actual - expected) > atol + rtol * np.abs(expected)
+    if bad.any():
+        index = np.argwhere(bad)[0]
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {bad.size} outside rel {rtol} / abs {atol}; first at {tuple(index)}: "
+            f"{actual[tuple(index)]!r} vs {expected[tuple(index)]!r}")
+
+
+def assert_bits_equal(actual, expected, what: str = "") -> None:
+    actual = np.asarray(actual)
+    expected = np.asarray(expected)
+    if actual.shape != expected.shape:
+        raise AssertionError(f"{what}: shape {actual.shape} != {expected.shape}")
+    if actual.dtype.kind == "f":
+        same = (actual == expected) | (np.isnan(actual) & np.isnan(expected))
+    else:
+        same = actual == expected
+    if not same.all():
+        index = np.argwhere(~same)[0]
+        raise AssertionError(f"{what}: {int((~same).sum())} of {same.size} differ; first at {tuple(index)}: "
+                             f"{actual[tuple(index)]!r} vs {expected[tuple(index)]!r}")

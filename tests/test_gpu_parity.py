@@ -1,0 +1,392 @@
+"""GPU parity of the HIP ternary kernels against the CPU oracle, through the C ABI.
+
+Integer work (q8, xsum, scales, per-128-group partials, embeddings) must be
+bit-exact.  fp32 outputs must equal the oracle's restatement of the kernel's
+own summation order bit for bit, and lie within rel 1e-5 / abs 1e-6 of both
+the reference kernel's order and the fp64 truth.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import ternary_oracle as T
+from _util import (ATOL, RTOL, assert_bits_equal, assert_within, device_matrix, make_layer, reference_lanes,
+                   to_np)
+
+pytestmark = pytest.mark.gpu
+
+EDGE_K = [8, 16, 24, 32, 64, 96, 100, 256, 1024, 1100]
+
+
+def _t(array, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+# ------------------------------------------------------------------ quantizer
+
+
+def _edge_rows(n: int, rng) -> np.ndarray:
+    rows = [
+        rng.standard_normal(n).astype(np.float32),
+        np.zeros(n, dtype=np.float32),                                      # s = 1e-5, q = 0
+        (rng.standard_normal(n) * 1e-4).astype(np.float32),                 # amax < 1.27e-3: floor applies
+        (rng.standard_normal(n) * 50).astype(np.float32),
+    ]
+    ties = np.zeros(n, dtype=np.float32)                                    # amax 127 -> s = 1: exact halves
+    ties[: min(n, 8)] = np.float32([127.0, 2.5, -3.5, 0.5, -0.5, 1.5, -126.5, -0.0])[: min(n, 8)]
+    rows.append(ties)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("n", EDGE_K + [4096, 4097, 28672])
+def test_quantize_plain_rows_bit_exact(cuda, oracle, n):
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(n)
+    x = _edge_rows(n, rng)
+    q8, xsum, scale = ops.quantize_rows(_t(x, cuda))
+    eq8, exsum, escale = oracle.quantize_rows(T.MODE_PLAIN, x, n)
+    assert_bits_equal(to_np(q8), eq8, "q8")
+    assert_bits_equal(to_np(xsum), exsum, "xsum")
+    assert_bits_equal(to_np(scale), escale, "scale")
+    q, s = T.quantize_closed_form(x[0])
+    assert s == escale[0]
+    assert_bits_equal(eq8[0], T.q8_layout(q)[0], "oracle vs closed form")
+
+
+@pytest.mark.parametrize("n", [16, 96, 1024, 1100, 4096, 8192])
+def test_quantize_norm_bit_exact(cuda, oracle, n):
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(7 + n)
+    x = (rng.standard_normal((3, n)) * np.float32(3.0)).astype(np.float32)
+    x[2, ::7] *= 40.0  # rows whose normalised values reach the +-8 clip
+    weight = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    q8, xsum, scale = ops.quantize_rows(_t(x, cuda), mode=ops.MODE_NORM, aux=_t(weight, cuda), eps=1e-6)
+    eq8, exsum, escale = oracle.quantize_rows(T.MODE_NORM, x, n, aux=weight, eps=1e-6)
+    assert_bits_equal(to_np(scale), escale, "scale")
+    assert_bits_equal(to_np(q8), eq8, "q8")
+    assert_bits_equal(to_np(xsum), exsum, "xsum")
+
+
+@pytest.mark.parametrize("head_dim,heads,splits", [(4, 4, 3), (16, 4, 4), (64, 16, 4)])
+def test_quantize_attn_bit_exact(cuda, oracle, head_dim, heads, splits):
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(head_dim * 31 + splits)
+    check = runtime.library().ivonar_define(b"HEAD_DIM", head_dim)
+    assert check == 0
+    try:
+        parts = rng.standard_normal((2, heads, splits, head_dim + 2)).astype(np.float32)
+        parts[..., 1] = np.abs(parts[..., 1]) + 0.5
+        parts[0, 0, 0, 0] = -np.inf  # an empty split
+        n = heads * head_dim
+        stride = heads * splits * (head_dim + 2)
+        flat = parts.reshape(2, stride)
+        q8, xsum, scale = ops.quantize_rows(_t(flat, cuda), mode=ops.MODE_ATTN, splits=splits, n=n)
+        eq8, exsum, escale = oracle.quantize_rows(T.MODE_ATTN, flat, n, splits=splits, head_dim=head_dim, m=2,
+                                                  in_stride=stride)
+        assert_bits_equal(to_np(scale), escale, "scale")
+        assert_bits_equal(to_np(q8), eq8, "q8")
+        assert_bits_equal(to_np(xsum), exsum, "xsum")
+    finally:
+        runtime.library().ivonar_define(b"HEAD_DIM", 64)
+
+
+# ------------------------------------------------------------ integer core
+
+
+@pytest.mark.parametrize("rows,k", [(1, 8), (7, 16), (9, 24), (64, 96), (130, 100), (33, 1024), (64, 4096),
+                                    (16, 8192), (8, 28672)])
+def test_group_partials_bit_exact_against_brute_force(cuda, oracle, rows, k):
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(rows * 1000 + k)
+    codes, packed, scale_bits, _ = make_layer(rng, rows, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    q, _ = T.quantize_closed_form(x)
+    q8, xsum = T.q8_layout(q)
+    matrix = device_matrix(packed, scale_bits, k, device=cuda)
+    got = to_np(ops.group_partials(matrix, _t(q8, cuda), _t(xsum, cuda)))
+    expected = T.group_partials_int64(codes, q)
+    assert np.abs(expected).max() <= 127 * 128
+    assert_bits_equal(got.astype(np.int64), expected, "partials")
+    assert_bits_equal(oracle.group_partials(q8, xsum, packed, rows, k).astype(np.int64), expected, "oracle partials")
+
+
+# ------------------------------------------------------------------- GEMV
+
+
+def _gemv_case(rng, rows, k, bias=False, p=(0.3, 0.4, 0.3)):
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, p=p, bias=bias)
+    x = rng.standard_normal(k).astype(np.float32)
+    return codes, packed, scale_bits, b, x
+
+
+def _check_gemv_store(cuda, oracle, rows, k, bias):
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(rows + 17 * k + int(bias))
+    codes, packed, scale_bits, b, x = _gemv_case(rng, rows, k, bias)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    y = to_np(ops.gemv(matrix, _t(x, cuda)))
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    mine = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, b,
+                             np.zeros(rows, np.float32), k, lanes)
+    assert_bits_equal(y, mine, "gemv vs oracle (kernel order)")
+    ref = oracle.reforder(T.EPI_STORE, False, q8, xsum, sx, packed, scale_bits, b, np.zeros(rows, np.float32), k,
+                          reference_lanes(k, rows), rows, 1)
+    assert_within(y, ref, what="gemv vs reference-kernel order")
+    q, s = T.quantize_closed_form(x)
+    truth = T.truth_fp64(T.group_partials_int64(codes, q), T.half_bits_to_float(scale_bits), s, b)
+    assert_within(y, truth, what="gemv vs fp64 truth")
+
+
+@pytest.mark.parametrize("k", EDGE_K)
+@pytest.mark.parametrize("rows", [1, 6, 64, 257])
+def test_gemv_plain_store_edge_shapes(cuda, oracle, rows, k):
+    _check_gemv_store(cuda, oracle, rows, k, bias=rows == 6)
+
+
+@pytest.mark.parametrize("rows,k", [(4096, 1024), (1024, 4096), (3072, 1024), (512, 8192), (256, 28672),
+                                    (333, 5000)])
+def test_gemv_plain_store_model_shapes(cuda, oracle, rows, k):
+    _check_gemv_store(cuda, oracle, rows, k, bias=False)
+
+
+@pytest.mark.parametrize("k", [24, 1024, 4096, 8192])
+def test_gemv_residual_and_silu_pair(cuda, oracle, k):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(k + 5)
+    rows = 64
+    codes, packed, scale_bits, b, x = _gemv_case(rng, rows, k, bias=True)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    base = rng.standard_normal(rows).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemv(matrix, _t(x, cuda), out=out, epilogue="residual")
+    expected = oracle.gemv_pairs(T.EPI_RESIDUAL, q8[0], xsum[0], sx[0], packed, scale_bits, b, base.copy(), k, lanes)
+    assert_bits_equal(to_np(out), expected, "residual")
+    # silu pair on interleaved rows: output[j] = silu(row 2j) * row 2j+1
+    weight = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    half = torch.empty(rows // 2, dtype=torch.float32, device=cuda)
+    ops.gemv(matrix, _t(x, cuda), out=half, mode="norm", epilogue="silu_pair", aux=_t(weight, cuda), eps=1e-6)
+    nq8, nxsum, nsx = oracle.quantize_rows(T.MODE_NORM, x, k, aux=weight, eps=1e-6)
+    expected = oracle.gemv_pairs(T.EPI_SILU_PAIR, nq8[0], nxsum[0], nsx[0], packed, scale_bits, b,
+                                 np.zeros(rows // 2, np.float32), k, lanes)
+    assert_bits_equal(to_np(half), expected, "silu pair")
+    ref = oracle.reforder(T.EPI_SILU_PAIR, False, nq8, nxsum, nsx, packed, scale_bits, b,
+                          np.zeros(rows // 2, np.float32), k, reference_lanes(k, rows, 16), rows // 2, 1)
+    assert_within(to_np(half), ref, rtol=1e-5, atol=1e-6, what="silu pair vs reference order")
+
+
+@pytest.mark.parametrize("k", [96, 1024, 8192])
+def test_gemv_norm_store_and_prequant(cuda, oracle, k):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(k + 11)
+    rows = 200
+    codes, packed, scale_bits, b, x = _gemv_case(rng, rows, k)
+    weight = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, device=cuda)
+    y = to_np(ops.gemv(matrix, _t(x, cuda), mode="norm", aux=_t(weight, cuda), eps=1e-6))
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_NORM, x, k, aux=weight, eps=1e-6)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    expected = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, None,
+                                 np.zeros(rows, np.float32), k, lanes)
+    assert_bits_equal(y, expected, "norm store")
+    # quantize_norm + gemv_prequant_store (the LM-head pair of launches)
+    lib = runtime.library()
+    dq8, dxsum, dscale = ops.activation_buffers(1, k, cuda)
+    xin, win = _t(x, cuda), _t(weight, cuda)
+    runtime.check(lib.quantize_norm(runtime.current_stream(cuda), runtime.pointer(xin), runtime.pointer(win),
+                                    k, runtime.float32(1e-6), 1, runtime.pointer(dq8), runtime.pointer(dxsum),
+                                    runtime.pointer(dscale)))
+    assert_bits_equal(to_np(dq8), q8, "quantize_norm q8")
+    head = to_np(ops.gemv_prequant(matrix, dq8, dxsum, dscale))
+    assert_bits_equal(head, expected, "prequant")
+
+
+@pytest.mark.parametrize("head_dim,heads,splits", [(4, 4, 4), (64, 16, 4)])
+def test_gemv_attn_residual(cuda, oracle, head_dim, heads, splits):
+    from ivonar_amd import ops, runtime
+
+    lib = runtime.library()
+    assert lib.ivonar_define(b"HEAD_DIM", head_dim) == 0
+    try:
+        rng = np.random.default_rng(head_dim + splits)
+        k = heads * head_dim
+        rows = 48
+        codes, packed, scale_bits, b, _ = _gemv_case(rng, rows, k, bias=True)
+        parts = rng.standard_normal((heads, splits, head_dim + 2)).astype(np.float32)
+        parts[..., 1] = np.abs(parts[..., 1]) + 0.5
+        matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+        base = rng.standard_normal(rows).astype(np.float32)
+        out = _t(base, cuda)
+        ops.gemv(matrix, _t(parts.reshape(-1), cuda), out=out, mode="attn", epilogue="residual", splits=splits)
+        q8, xsum, sx = oracle.quantize_rows(T.MODE_ATTN, parts.reshape(-1), k, splits=splits, head_dim=head_dim)
+        lanes, _ = runtime.gemv_plan(rows, k)
+        expected = oracle.gemv_pairs(T.EPI_RESIDUAL, q8[0], xsum[0], sx[0], packed, scale_bits, b, base.copy(), k,
+                                     lanes)
+        assert_bits_equal(to_np(out), expected, "attn residual")
+    finally:
+        lib.ivonar_define(b"HEAD_DIM", 64)
+
+
+# ------------------------------------------------------------------- GEMM
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 32, 33, 70])
+@pytest.mark.parametrize("k,rows", [(24, 16), (96, 64), (1024, 256), (4096, 96), (1100, 48)])
+def test_gemm_tile_store(cuda, oracle, m, k, rows):
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(m * 7919 + k + rows)
+    codes, packed, scale_bits, b, _ = make_layer(rng, rows, k, bias=(m == 5))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[:, :: max(1, k // 10)] *= 20.0
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    assert_bits_equal(to_np(q8), eq8, "tile q8")
+    expected = oracle.gemm_seq(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b, np.zeros((m, rows), np.float32),
+                               k, rows, m)
+    assert_bits_equal(y, expected, "gemm vs oracle (kernel order)")
+    ref = oracle.reforder(T.EPI_STORE, True, eq8, exsum, esx, packed, scale_bits, b, np.zeros((m, rows), np.float32),
+                          k, reference_lanes(k, rows), rows, m)
+    assert_within(y, ref, what="gemm vs reference-kernel order")
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_gemm_tile_epilogues(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(99 if epilogue == "residual" else 98)
+    m, k, rows = 32, 1024, 128
+    codes, packed, scale_bits, b, _ = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    width = rows if epilogue == "residual" else rows // 2
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
+    expected = oracle.gemm_seq(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m)
+    assert_bits_equal(to_np(out), expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
+
+
+# ------------------------------------------------------- embedding, argmax
+
+
+def test_embed_gather_and_argmax(cuda, oracle):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(3)
+    vocab, hidden = 300, 100
+    codes, packed, scale_bits, _, _ = _gemv_case(rng, vocab, hidden)
+    matrix = device_matrix(packed, scale_bits, hidden, device=cuda)
+    tokens = np.array([0, 5, 299, 17, 5], dtype=np.int64)
+    got = to_np(ops.embed(matrix, _t(tokens, cuda)))
+    expected = oracle.embed(tokens, packed, scale_bits, hidden)
+    assert_bits_equal(got, expected, "embed_tile")
+    closed = (codes[tokens].astype(np.float32) - 1.0) * np.repeat(T.half_bits_to_float(scale_bits)[tokens], 128,
+                                                                 axis=1)[:, :hidden]
+    assert_bits_equal(expected, closed, "oracle embed vs closed form")
+    lib = runtime.library()
+    single = torch.empty(hidden, dtype=torch.float32, device=cuda)
+    runtime.check(lib.embed_token(runtime.current_stream(cuda), runtime.pointer(_t(tokens[2:3], cuda)),
+                                  runtime.pointer(matrix.packed), runtime.pointer(matrix.scales),
+                                  runtime.pointer(single), hidden, matrix.row_bytes, matrix.groups))
+    assert_bits_equal(to_np(single), expected[2], "embed_token")
+    tile = _t(expected, cuda)
+    for valid in (0, 1, 3, 5):
+        out = torch.empty(hidden, dtype=torch.float32, device=cuda)
+        runtime.check(lib.gather_token(runtime.current_stream(cuda), runtime.pointer(tile), runtime.pointer(out),
+                                       hidden, runtime.pointer(_t(np.array([valid], np.int64), cuda))))
+        assert_bits_equal(to_np(out), expected[max(valid - 1, 0)], f"gather valid={valid}")
+    values = rng.standard_normal(32000).astype(np.float32)
+    values[[123, 31000]] = values.max() + 1.0  # tie: the first index wins
+    assert int(to_np(ops.argmax(_t(values, cuda)))[0]) == oracle.argmax(values) == 123
+
+
+# ----------------------------------------------------------- graph capture
+
+
+def test_graph_replays_match_eager(cuda, oracle):
+    """A captured GEMV (two-pass: quantize + GEMV) and GEMM replay bit-identically several times."""
+    import torch
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(5)
+    k, rows, m = 8192, 256, 32
+    codes, packed, scale_bits, b, x = _gemv_case(rng, rows, k)
+    matrix = device_matrix(packed, scale_bits, k, device=cuda)
+    xs = _t(rng.standard_normal((m, k)).astype(np.float32), cuda)
+    xv = _t(x, cuda)
+    y = torch.empty(rows, dtype=torch.float32, device=cuda)
+    q8, xsum, sx = ops.activation_buffers(m, k, cuda)
+    out = torch.empty((m, rows), dtype=torch.float32, device=cuda)
+
+    def step():
+        ops.gemv(matrix, xv, out=y)
+        ops.quantize_rows(xs, out=(q8, xsum, sx))
+        ops.gemm(matrix, q8, xsum, sx, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    eager_y, eager_out = y.clone(), out.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    for _ in range(3):
+        y.zero_()
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager_y)
+        assert torch.equal(out, eager_out)
+
+
+# ----------------------------------------------------------------- errors
+
+
+def test_invalid_arguments_raise(cuda):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(0)
+    codes, packed, scale_bits, _, x = _gemv_case(rng, 7, 64)
+    matrix = device_matrix(packed, scale_bits, 64, device=cuda)
+    with pytest.raises(runtime.KernelError):  # odd row count for a silu pair
+        ops.gemv(matrix, _t(x, cuda), out=torch.empty(4, device=cuda), epilogue="silu_pair", mode="norm",
+                 aux=_t(np.ones(64, np.float32), cuda))
+    lib = runtime.library()
+    status = lib.gemv_plain_store(runtime.current_stream(cuda), runtime.pointer(_t(x, cuda)), None, None, None, None,
+                                  runtime.pointer(matrix.packed), runtime.pointer(matrix.scales), None,
+                                  runtime.pointer(torch.empty(7, device=cuda)), 7, 64, 8, matrix.groups, 2, 1,
+                                  runtime.float32(1e-6), None, 0)
+    assert status != 0  # row_bytes below 16 * chunks
