@@ -46,7 +46,35 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--probe", choices=["gemv-stress"], default=None,
+                        help="profiling mode: only the named kernel workload, no JSON line")
+    parser.add_argument("--probe-calls", type=int, default=16)
     return parser.parse_args()
+
+
+def probe_gemv_stress(calls: int) -> None:
+    """GEMV kernel alone (pre-quantized input) on both stress shapes, cycling 8 copies; then a
+    512 MiB device copy of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    from ivonar_amd import ops, runtime, synthetic
+
+    device = torch.device("cuda", 0)
+    runtime.initialise(0)
+    for layer, x in synthetic.stress_layers(seed=3):
+        mats = device_copies(layer, device, ROTATING_COPIES)
+        q8, xsum, sx = ops.quantize_rows(torch.from_numpy(x).to(device))
+        out = torch.empty(layer.rows, dtype=torch.float32, device=device)
+        torch.cuda.synchronize()
+        for call in range(calls):
+            ops.gemv_prequant(mats[call % ROTATING_COPIES], q8, xsum, sx, out=out)
+        torch.cuda.synchronize()
+        print(f"probe: gemv {layer.in_features}->{layer.rows} x{calls} done", flush=True)
+    src = torch.empty(512 * 2**20, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print("probe: 512 MiB copy done", flush=True)
 
 
 def graph_of(step, stream):
@@ -103,6 +131,9 @@ def main() -> None:
         print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU figures are not part of this build",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.probe == "gemv-stress":
+        probe_gemv_stress(args.probe_calls)
+        return
     import numpy as np
     import torch
 

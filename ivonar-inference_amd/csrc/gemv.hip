@@ -3,52 +3,159 @@
 //
 // Work split.  A row of the packed matrix is covered by `lanes` lanes of a
 // wave (a power of two, 2..64, the smallest that spans the row's chunks); a
-// wave holds 64/lanes row slots and every lane streams R rows, so one wave
-// step reads R * 64 lanes * 16 bytes with 128-bit loads that are contiguous
-// across the lanes of a slot.  Lane `sub` takes chunk u = j*lanes + sub, so
-// the two chunks of a 128-input group land on a lane pair: each lane forms
-// its chunk's exact int32 sum of code*q minus the chunk's q sum, and one DPP
-// swap (quad_perm [1,0,3,2]) adds the pair into the group partial P[r, g].
-// The pair folds P * scale[r, g] into an fp32 fma chain over its groups
-// (g = pair, pair + lanes/2, ...); an xor butterfly over the pairs, the token
-// scale and the bias finish the row.  That order is restated bit for bit by
-// the CPU oracle (orc_gemv_pairs).
+// wave holds 64/lanes row slots and each lane streams kRows rows, so one
+// wave step reads kRows * 64 lanes * 16 bytes with 128-bit loads that are
+// contiguous across the lanes of a slot.  Lane `sub` takes chunks
+// u = j*lanes + sub (j = 0..NJ-1), so the two chunks of a 128-input group
+// land on a lane pair: each lane forms its chunk's exact int32 sum of
+// code*q minus the chunk's q sum, and one DPP swap (quad_perm [1,0,3,2])
+// adds the pair into the group partial P[r, g].  The pair folds
+// P * scale[r, g] into an fp32 fma chain over its groups (g = pair,
+// pair + lanes/2, ...); an xor butterfly over the pairs, the token scale and
+// the bias finish the row.  The CPU oracle restates that order bit for bit
+// (orc_gemv_pairs).
 //
-// Activations.  The block keeps the token's q8 row in LDS in a quad-planar
-// layout (quad w of chunk u at int4 index w*C + u), so the 16-byte reads of
-// one instruction are contiguous across a slot's lanes and identical across
-// slots.  For rows up to gemv_fused_limit() inputs the block quantizes the
-// fp32 input itself (the fused prologue of gemv_plain_*, gemv_norm_*,
-// gemv_attn_*); longer rows are quantized once by the quantizer into the
-// device scratch and the blocks copy the result, which keeps the per-block
-// prologue short when the GEMV streams tens of megabytes.
+// Memory.  Loads are unconditional: indices past the row or the matrix are
+// clamped to valid addresses and the integer result is masked, which keeps
+// the loop free of exec-mask branches.  The first weight loads are issued
+// before the activation prologue, and when a row needs at most two steps
+// per lane the next row step's weights are prefetched while the current one
+// is computed (double buffering), so each wave keeps 2-4 KB in flight.
+//
+// Activations.  The block holds the token's q8 row in LDS, quad-planar (quad
+// w of chunk u at int4 index w*C + u: the 16-byte reads of a slot's lanes are
+// contiguous).  With at most two steps per lane the lane's q8 words stay in
+// registers for the whole kernel.  For rows up to kFusedLimit inputs the
+// block quantizes the fp32 input itself (the fused prologue of gemv_plain_*,
+// gemv_norm_*, gemv_attn_*); longer rows are quantized once by the quantizer
+// into the device scratch and each block copies the result to LDS.
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
 namespace ivo {
 namespace {
 
-constexpr int kRowsPerLane = 2;  // even, so a silu pair never straddles lanes
+constexpr int kRows = 2;  // rows per lane; even, so a silu pair stays in one lane
 constexpr int kFusedLimit = 4096;
 constexpr int kMaxLdsBytes = 64 * 1024;
+constexpr int kMaxSteps = 8;
+constexpr int kBlocksPerCu = 4;
 
-struct GemvGeometry {
-  int lanes;
-  int lane_shift;
-  int iters;  // row steps of one wave
+struct GemvShape {
+  int rows, n, row_bytes, groups, splits, head_dim;
+  float eps;
+  int lanes, lane_shift, iters;
 };
 
-template <int MODE, int EPI, bool FUSED, int JB>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, GemvGeometry geo) {
+struct GemvPtrs {
+  const float* input;
+  const float* aux;
+  const int8_t* q8_in;
+  const int32_t* xsum_in;
+  const float* scale_in;
+};
+
+template <int NJ>
+struct Step {
+  uint4 w[NJ][kRows];
+  uint16_t s[NJ][kRows];
+};
+
+__device__ __forceinline__ uint4 load16(const uint8_t* __restrict__ p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+template <int NJ, bool SCALES>
+__device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restrict__ packed,
+                                          const uint16_t* __restrict__ scales, const GemvShape& sh, int row0,
+                                          int j0, int sub, int chunks) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int u = min((j0 + j) * sh.lanes + sub, chunks - 1);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int row = min(row0 + r, sh.rows - 1);
+      st.w[j][r] = load16(packed + (size_t)row * sh.row_bytes + (size_t)u * 16);
+      st.s[j][r] = SCALES ? scales[(size_t)row * sh.groups + (u >> 1)] : (uint16_t)0;
+    }
+  }
+}
+
+template <int EPI, int NJ, bool QREG>
+__device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr)[QREG ? NJ : 1][4],
+                                             const int (&xr)[QREG ? NJ : 1], const int4* __restrict__ lds_q,
+                                             const int* __restrict__ lds_x, float (&acc)[kRows],
+                                             int32_t* __restrict__ partials, const GemvShape& sh, int row0, int j0,
+                                             int sub, int chunks) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int u_raw = (j0 + j) * sh.lanes + sub;
+    const bool live = u_raw < chunks;
+    const int g = u_raw >> 1;
+    const bool group_live = 2 * g < chunks;
+    int4 q0, q1, q2, q3;
+    int xs;
+    if constexpr (QREG) {
+      q0 = qr[j][0];
+      q1 = qr[j][1];
+      q2 = qr[j][2];
+      q3 = qr[j][3];
+      xs = xr[j];
+    } else {
+      const int u = min(u_raw, chunks - 1);
+      q0 = lds_q[u];
+      q1 = lds_q[chunks + u];
+      q2 = lds_q[2 * chunks + u];
+      q3 = lds_q[3 * chunks + u];
+      xs = lds_x[u];
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      int d = chunk_code_dot(st.w[j][r], q0, q1, q2, q3, 0) - xs;
+      d = live ? d : 0;
+      d += pair_swap(d);
+      const int row = row0 + r;
+      if constexpr (EPI == kPartials) {
+        if (group_live && (sub & 1) == 0 && row < sh.rows) partials[(size_t)row * sh.groups + g] = d;
+      } else {
+        const float contribution = group_live ? (float)d : 0.0f;
+        acc[r] = __builtin_fmaf(contribution, h2f(st.s[j][r]), acc[r]);
+      }
+    }
+  }
+}
+
+template <int MODE, int EPI, bool FUSED, int NJ>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
+                                                        const uint16_t* __restrict__ scales,
+                                                        const float* __restrict__ bias, float* __restrict__ output,
+                                                        int32_t* __restrict__ partials, GemvShape sh) {
+  constexpr bool QREG = NJ <= 2;
+  constexpr bool DOUBLE = NJ <= 2;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ float slots[64];
-  const int chunks = (a.n + kChunk - 1) / kChunk;
+  const int chunks = (sh.n + kChunk - 1) / kChunk;
   int4* lds_q = reinterpret_cast<int4*>(lds_raw);
   int* lds_x = reinterpret_cast<int*>(lds_raw + (size_t)chunks * kChunk);
 
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & (sh.lanes - 1);
+  const int slot = lane >> sh.lane_shift;
+  const int rows_per_iter = (64 >> sh.lane_shift) * kRows;
+  const int waves = gridDim.x * (kThreads / 64);
+  const int first = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int steps = (chunks + sh.lanes - 1) / sh.lanes;
+
+  // Weights of the first row step go out before the activation prologue.
+  // Loads are never predicated (rows past the matrix are clamped inside
+  // load_step), so the wait counts before each use stay exact.
+  Step<NJ> a, b;
+  int it = first;
+  load_step<NJ, EPI != kPartials>(a, packed, scales, sh, it * rows_per_iter + slot * kRows, 0, sub, chunks);
+
   float sx;
   if constexpr (FUSED) {
-    const RowSource src{a.input, a.aux, a.n, a.eps, a.splits, a.head_dim};
+    const RowSource src{in.input, in.aux, sh.n, sh.eps, sh.splits, sh.head_dim};
     float inv_rms;
     sx = row_scale<MODE>(src, inv_rms, slots);
     for (int d = threadIdx.x; d < chunks * 16; d += kThreads) {
@@ -59,111 +166,91 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, GemvGeometry
       if ((d & 15) == 0) lds_x[u] = total;
     }
   } else {
-    const int4* gq = reinterpret_cast<const int4*>(a.q8_in);
+    const int4* gq = reinterpret_cast<const int4*>(in.q8_in);
     for (int e = threadIdx.x; e < chunks * 4; e += kThreads) lds_q[(e & 3) * chunks + (e >> 2)] = gq[e];
-    for (int u = threadIdx.x; u < chunks; u += kThreads) lds_x[u] = a.xsum_in[u];
-    sx = *a.scale_in;
+    for (int u = threadIdx.x; u < chunks; u += kThreads) lds_x[u] = in.xsum_in[u];
+    sx = *in.scale_in;
   }
   __syncthreads();
 
-  const int lanes = geo.lanes;
-  const int lane = threadIdx.x & 63;
-  const int sub = lane & (lanes - 1);
-  const int slot = lane >> geo.lane_shift;
-  const int rows_per_iter = (64 >> geo.lane_shift) * kRowsPerLane;
-  const int waves = gridDim.x * (kThreads / 64);
-  const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
-  const int4 zeroq = make_int4(0, 0, 0, 0);
-
-  for (int it = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); it < geo.iters; it += waves) {
-    const int row0 = it * rows_per_iter + slot * kRowsPerLane;
-    float acc[kRowsPerLane];
+  int4 qr[QREG ? NJ : 1][4];
+  int xr[QREG ? NJ : 1];
+  if constexpr (QREG) {
 #pragma unroll
-    for (int r = 0; r < kRowsPerLane; ++r) acc[r] = 0.0f;
-    for (int j0 = 0; j0 * lanes < chunks; j0 += JB) {
-      uint4 wv[JB][kRowsPerLane];
+    for (int j = 0; j < NJ; ++j) {
+      const int u = min(j * sh.lanes + sub, chunks - 1);
 #pragma unroll
-      for (int jb = 0; jb < JB; ++jb) {
-        const int u = (j0 + jb) * lanes + sub;
-#pragma unroll
-        for (int r = 0; r < kRowsPerLane; ++r) {
-          const int row = row0 + r;
-          wv[jb][r] = (u < chunks && row < a.rows)
-                          ? *reinterpret_cast<const uint4*>(a.packed + (size_t)row * a.row_bytes + (size_t)u * 16)
-                          : zero4;
-        }
-      }
-#pragma unroll
-      for (int jb = 0; jb < JB; ++jb) {
-        const int u = (j0 + jb) * lanes + sub;
-        const bool live = u < chunks;
-        const int4 q0 = live ? lds_q[u] : zeroq;
-        const int4 q1 = live ? lds_q[chunks + u] : zeroq;
-        const int4 q2 = live ? lds_q[2 * chunks + u] : zeroq;
-        const int4 q3 = live ? lds_q[3 * chunks + u] : zeroq;
-        const int xs = live ? lds_x[u] : 0;
-        const int g = u >> 1;
-        const bool group_live = 2 * g < chunks;
-#pragma unroll
-        for (int r = 0; r < kRowsPerLane; ++r) {
-          int d = chunk_code_dot(wv[jb][r], q0, q1, q2, q3, 0) - xs;
-          d += pair_swap(d);
-          const int row = row0 + r;
-          if constexpr (EPI == kPartials) {
-            if (group_live && (sub & 1) == 0 && row < a.rows) a.partials[(size_t)row * a.groups + g] = d;
-          } else {
-            if (group_live && row < a.rows)
-              acc[r] = __builtin_fmaf((float)d, h2f(a.scales[(size_t)row * a.groups + g]), acc[r]);
-          }
-        }
-      }
+      for (int w = 0; w < 4; ++w) qr[j][w] = lds_q[w * chunks + u];
+      xr[j] = lds_x[u];
     }
+  }
+
+  auto finish = [&](float (&acc)[kRows], int row0) {
     if constexpr (EPI != kPartials) {
 #pragma unroll
-      for (int r = 0; r < kRowsPerLane; ++r) {
-        for (int offset = 2; offset < lanes; offset <<= 1) acc[r] = acc[r] + __shfl_xor(acc[r], offset);
+      for (int r = 0; r < kRows; ++r) {
+        for (int offset = 2; offset < sh.lanes; offset <<= 1) acc[r] = acc[r] + __shfl_xor(acc[r], offset);
       }
       if (sub == 0) {
-        float y[kRowsPerLane];
+        float y[kRows];
 #pragma unroll
-        for (int r = 0; r < kRowsPerLane; ++r) {
+        for (int r = 0; r < kRows; ++r) {
           const int row = row0 + r;
           y[r] = acc[r] * sx;
-          if (a.bias != nullptr && row < a.rows) y[r] = y[r] + a.bias[row];
+          if (bias != nullptr && row < sh.rows) y[r] = y[r] + bias[row];
         }
 #pragma unroll
-        for (int r = 0; r < kRowsPerLane; ++r) {
+        for (int r = 0; r < kRows; ++r) {
           const int row = row0 + r;
           if constexpr (EPI == kStore) {
-            if (row < a.rows) a.output[row] = y[r];
+            if (row < sh.rows) output[row] = y[r];
           } else if constexpr (EPI == kResidual) {
-            if (row < a.rows) a.output[row] = a.output[row] + y[r];
+            if (row < sh.rows) output[row] = output[row] + y[r];
           } else if constexpr (EPI == kSiluPair) {
-            if ((r & 1) == 0 && row + 1 < a.rows) a.output[row >> 1] = ivo_silu(y[r]) * y[r + 1];
+            if ((r & 1) == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y[r]) * y[r + 1];
           }
         }
       }
     }
-  }
-}
+  };
 
-template <int MODE, int EPI, bool FUSED>
-hipError_t launch_jb(hipStream_t stream, const GemvArgs& a, const GemvGeometry& geo, int blocks, size_t lds, int jb) {
-  switch (jb) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, 1>), dim3(blocks), dim3(kThreads), lds, stream, a, geo); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, 2>), dim3(blocks), dim3(kThreads), lds, stream, a, geo); break;
-    default: hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, 4>), dim3(blocks), dim3(kThreads), lds, stream, a, geo); break;
-  }
-  return hipGetLastError();
-}
-
-template <int MODE>
-hipError_t launch_fused(hipStream_t stream, const GemvArgs& a, const GemvGeometry& geo, int blocks, size_t lds, int jb) {
-  switch (a.epi) {
-    case kStore: return launch_jb<MODE, kStore, true>(stream, a, geo, blocks, lds, jb);
-    case kResidual: return launch_jb<MODE, kResidual, true>(stream, a, geo, blocks, lds, jb);
-    case kSiluPair: return launch_jb<MODE, kSiluPair, true>(stream, a, geo, blocks, lds, jb);
-    default: return hipErrorInvalidValue;
+  if constexpr (DOUBLE) {
+    // steps <= NJ: one Step covers the whole row; prefetch the next row step.
+    while (it < sh.iters) {
+      const int row0 = it * rows_per_iter + slot * kRows;
+      const int next = it + waves;
+      load_step<NJ, EPI != kPartials>(b, packed, scales, sh, next * rows_per_iter + slot * kRows, 0, sub, chunks);
+      float acc[kRows];
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+      compute_step<EPI, NJ, QREG>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, 0, sub, chunks);
+      finish(acc, row0);
+      it = next;
+      if (it >= sh.iters) break;
+      const int row1 = it * rows_per_iter + slot * kRows;
+      const int next2 = it + waves;
+      load_step<NJ, EPI != kPartials>(a, packed, scales, sh, next2 * rows_per_iter + slot * kRows, 0, sub, chunks);
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+      compute_step<EPI, NJ, QREG>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row1, 0, sub, chunks);
+      finish(acc, row1);
+      it = next2;
+    }
+  } else {
+    // Long rows: the row is covered in blocks of NJ steps; all of a block's loads are in flight together.
+    bool preloaded = true;
+    for (; it < sh.iters; it += waves) {
+      const int row0 = it * rows_per_iter + slot * kRows;
+      float acc[kRows];
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+      for (int j0 = 0; j0 < steps; j0 += NJ) {
+        if (!preloaded) load_step<NJ, EPI != kPartials>(a, packed, scales, sh, row0, j0, sub, chunks);
+        preloaded = false;
+        compute_step<EPI, NJ, QREG>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, j0, sub, chunks);
+      }
+      finish(acc, row0);
+    }
   }
 }
 
@@ -173,10 +260,49 @@ int device_cus() {
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
   if (cached[device] == 0) {
     int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+      cus = 256;
     cached[device] = cus;
   }
   return cached[device];
+}
+
+template <int MODE, int EPI, bool FUSED, int NJ>
+void launch_one(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
+                size_t lds) {
+  hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, NJ>), dim3(blocks), dim3(kThreads), lds, stream, p, a.packed,
+                     a.scales, a.bias, a.output, a.partials, sh);
+}
+
+template <int MODE, int EPI, bool FUSED>
+hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
+                     size_t lds, int steps) {
+  if constexpr (FUSED) {
+    launch_one<MODE, EPI, FUSED, 1>(stream, p, a, sh, blocks, lds);  // fused rows need one step per lane
+  } else {
+    switch (steps) {
+      case 1: launch_one<MODE, EPI, FUSED, 1>(stream, p, a, sh, blocks, lds); break;
+      case 2: launch_one<MODE, EPI, FUSED, 2>(stream, p, a, sh, blocks, lds); break;
+      case 3: launch_one<MODE, EPI, FUSED, 3>(stream, p, a, sh, blocks, lds); break;
+      case 4: launch_one<MODE, EPI, FUSED, 4>(stream, p, a, sh, blocks, lds); break;
+      case 5: launch_one<MODE, EPI, FUSED, 5>(stream, p, a, sh, blocks, lds); break;
+      case 6: launch_one<MODE, EPI, FUSED, 6>(stream, p, a, sh, blocks, lds); break;
+      case 7: launch_one<MODE, EPI, FUSED, 7>(stream, p, a, sh, blocks, lds); break;
+      default: launch_one<MODE, EPI, FUSED, kMaxSteps>(stream, p, a, sh, blocks, lds); break;
+    }
+  }
+  return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_fused(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
+                        size_t lds) {
+  switch (a.epi) {
+    case kStore: return launch_nj<MODE, kStore, true>(stream, p, a, sh, blocks, lds, 1);
+    case kResidual: return launch_nj<MODE, kResidual, true>(stream, p, a, sh, blocks, lds, 1);
+    case kSiluPair: return launch_nj<MODE, kSiluPair, true>(stream, p, a, sh, blocks, lds, 1);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
@@ -189,7 +315,7 @@ void gemv_plan(int rows, int n, int* lanes, int* rows_per_lane) {
   int l = 2;
   while (l < 64 && l < chunks) l <<= 1;
   *lanes = l;
-  *rows_per_lane = kRowsPerLane;
+  *rows_per_lane = kRows;
 }
 
 hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
@@ -198,27 +324,33 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   const int chunks = ceil_div(a.n, kChunk);
   const size_t lds = (size_t)chunks * (kChunk + 4);
   if (lds > (size_t)kMaxLdsBytes) return hipErrorInvalidValue;
-  int lanes, rpl;
-  gemv_plan(a.rows, a.n, &lanes, &rpl);
-  GemvGeometry geo;
-  geo.lanes = lanes;
-  geo.lane_shift = __builtin_ctz((unsigned)lanes);
-  const int rows_per_iter = (64 / lanes) * rpl;
-  geo.iters = ceil_div(a.rows, rows_per_iter);
+  int lanes, rows_per_lane;
+  gemv_plan(a.rows, a.n, &lanes, &rows_per_lane);
+  GemvShape sh;
+  sh.rows = a.rows;
+  sh.n = a.n;
+  sh.row_bytes = a.row_bytes;
+  sh.groups = a.groups;
+  sh.splits = a.splits;
+  sh.head_dim = a.head_dim;
+  sh.eps = a.eps;
+  sh.lanes = lanes;
+  sh.lane_shift = __builtin_ctz((unsigned)lanes);
+  sh.iters = ceil_div(a.rows, (64 / lanes) * rows_per_lane);
   const int steps = ceil_div(chunks, lanes);
-  const int jb = steps >= 4 ? 4 : (steps >= 2 ? 2 : 1);
   const int cus = device_cus();
   const bool fused = a.q8_in == nullptr && a.n <= kFusedLimit;
-  const int cap = fused ? 2 * cus : 4 * cus;
-  int blocks = ceil_div(geo.iters, kThreads / 64);
+  int blocks = ceil_div(sh.iters, kThreads / 64);
+  const int cap = (fused ? 2 : kBlocksPerCu) * cus;
   if (blocks > cap) blocks = cap;
 
   if (fused) {
     if (a.epi == kPartials) return hipErrorInvalidValue;
+    const GemvPtrs p{a.input, a.aux, nullptr, nullptr, nullptr};
     switch (a.mode) {
-      case kPlain: return launch_fused<kPlain>(stream, a, geo, blocks, lds, jb);
-      case kNorm: return launch_fused<kNorm>(stream, a, geo, blocks, lds, jb);
-      case kAttn: return launch_fused<kAttn>(stream, a, geo, blocks, lds, jb);
+      case kPlain: return launch_fused<kPlain>(stream, p, a, sh, blocks, lds);
+      case kNorm: return launch_fused<kNorm>(stream, p, a, sh, blocks, lds);
+      case kAttn: return launch_fused<kAttn>(stream, p, a, sh, blocks, lds);
       default: return hipErrorInvalidValue;
     }
   }
@@ -235,11 +367,12 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
     a.xsum_in = scratch->xsum;
     a.scale_in = scratch->scale;
   }
+  const GemvPtrs p{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in};
   switch (a.epi) {
-    case kStore: return launch_jb<kPlain, kStore, false>(stream, a, geo, blocks, lds, jb);
-    case kResidual: return launch_jb<kPlain, kResidual, false>(stream, a, geo, blocks, lds, jb);
-    case kSiluPair: return launch_jb<kPlain, kSiluPair, false>(stream, a, geo, blocks, lds, jb);
-    case kPartials: return launch_jb<kPlain, kPartials, false>(stream, a, geo, blocks, lds, jb);
+    case kStore: return launch_nj<kPlain, kStore, false>(stream, p, a, sh, blocks, lds, steps);
+    case kResidual: return launch_nj<kPlain, kResidual, false>(stream, p, a, sh, blocks, lds, steps);
+    case kSiluPair: return launch_nj<kPlain, kSiluPair, false>(stream, p, a, sh, blocks, lds, steps);
+    case kPartials: return launch_nj<kPlain, kPartials, false>(stream, p, a, sh, blocks, lds, steps);
     default: return hipErrorInvalidValue;
   }
 }

@@ -104,16 +104,25 @@ __device__ __forceinline__ float block_max(float v, float* slots) {
 }
 
 // The reference kernel's reduction tree for a sum of squares over a 256-thread
-// block (ternary.cu:157-170, :81-84, :101-109): strided per-thread fma
-// partials, xor butterfly inside each 32-lane half (offsets 16..1), then the
-// eight half-wave totals added in order.
-template <class Value>
-__device__ __forceinline__ float tree_sum_squares(const Value& value_at, int n, float* slots) {
+// block (ternary.cu:157-170, :81-84, :101-109): per-thread fma partials over
+// i = tid, tid+256, ... in order, xor butterfly inside each 32-lane half
+// (offsets 16..1), then the eight half-wave totals added in order.  Loads go
+// out in batches of kBatch independent reads (indices clamped, values past
+// the row masked to zero, which leaves a non-negative fma chain unchanged).
+constexpr int kBatch = 16;
+
+__device__ __forceinline__ float tree_sum_squares(const float* __restrict__ x, int n, float* slots) {
   const int tid = threadIdx.x;
   float s = 0.0f;
-  for (int i = tid; i < n; i += kThreads) {
-    const float v = value_at(i);
-    s = __builtin_fmaf(v, v, s);
+  for (int base = 0; base < n; base += kThreads * kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) v[b] = x[min(base + b * kThreads + tid, n - 1)];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const float value = base + b * kThreads + tid < n ? v[b] : 0.0f;
+      s = __builtin_fmaf(value, value, s);
+    }
   }
   for (int offset = 16; offset > 0; offset >>= 1) s = s + __shfl_xor(s, offset);
   if ((tid & 31) == 0) slots[tid >> 5] = s;
@@ -157,20 +166,49 @@ struct RowSource {
 };
 
 // Per-row prologue shared by all quantizing kernels: returns the token scale
-// and, for NORM, sets inv_rms.  All 256 threads must call it.
+// and, for NORM, sets inv_rms.  All 256 threads must call it.  amax is
+// order-free, so its loads are clamped duplicates rather than masked, and a
+// 16-byte aligned PLAIN row is read as float4.
 template <int MODE>
 __device__ __forceinline__ float row_scale(const RowSource& src, float& inv_rms, float* slots) {
+  const int tid = threadIdx.x;
+  const int n = src.n;
   inv_rms = 1.0f;
   if constexpr (MODE == kNorm) {
-    const float* x = src.input;
-    const float squares = tree_sum_squares([&](int i) { return x[i]; }, src.n, slots);
-    inv_rms = 1.0f / __builtin_sqrtf(squares / (float)src.n + src.eps);
+    const float squares = tree_sum_squares(src.input, n, slots);
+    inv_rms = 1.0f / __builtin_sqrtf(squares / (float)n + src.eps);
   }
   float amax = 0.0f;
-  for (int i = threadIdx.x; i < src.n; i += kThreads) {
-    float v = source_value<MODE>(src.input, i, src.splits, src.head_dim);
-    if constexpr (MODE == kNorm) v = fminf(fmaxf(v * inv_rms, -8.0f), 8.0f) * src.aux[i];
-    amax = fmaxf(amax, fabsf(v));
+  if constexpr (MODE == kAttn) {
+    for (int i = tid; i < n; i += kThreads)
+      amax = fmaxf(amax, fabsf(source_value<MODE>(src.input, i, src.splits, src.head_dim)));
+  } else if (MODE == kPlain && (n & 3) == 0 && (((uintptr_t)src.input) & 15) == 0) {
+    const float4* x4 = reinterpret_cast<const float4*>(src.input);
+    const int n4 = n >> 2;
+    for (int base = 0; base < n4; base += kThreads * kBatch) {
+      float4 v[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) v[b] = x4[min(base + b * kThreads + tid, n4 - 1)];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+        amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[b].x), fabsf(v[b].y))), fmaxf(fabsf(v[b].z), fabsf(v[b].w)));
+    }
+  } else {
+    for (int base = 0; base < n; base += kThreads * kBatch) {
+      float v[kBatch];
+      int idx[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        idx[b] = min(base + b * kThreads + tid, n - 1);
+        v[b] = src.input[idx[b]];
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        float value = v[b];
+        if constexpr (MODE == kNorm) value = fminf(fmaxf(value * inv_rms, -8.0f), 8.0f) * src.aux[idx[b]];
+        amax = fmaxf(amax, fabsf(value));
+      }
+    }
   }
   amax = block_max(amax, slots + 32);
   return fmaxf(amax / 127.0f, 1e-5f);

@@ -253,7 +253,7 @@ def test_gemm_tile_store(cuda, oracle, m, k, rows):
     from ivonar_amd import ops
 
     rng = np.random.default_rng(m * 7919 + k + rows)
-    codes, packed, scale_bits, b, _ = make_layer(rng, rows, k, bias=(m == 5))
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=(m == 5))
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[:, :: max(1, k // 10)] *= 20.0
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
@@ -276,7 +276,7 @@ def test_gemm_tile_epilogues(cuda, oracle, epilogue):
 
     rng = np.random.default_rng(99 if epilogue == "residual" else 98)
     m, k, rows = 32, 1024, 128
-    codes, packed, scale_bits, b, _ = make_layer(rng, rows, k, bias=True)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
     x = rng.standard_normal((m, k)).astype(np.float32)
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
