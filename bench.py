@@ -46,7 +46,7 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     parser.add_argument("--skip-cpu", action="store_true")
-    parser.add_argument("--probe", choices=["gemv-stress"], default=None,
+    parser.add_argument("--probe", choices=["gemv-stress", "gemm-prefill"], default=None,
                         help="profiling mode: only the named kernel workload, no JSON line")
     parser.add_argument("--probe-calls", type=int, default=16)
     return parser.parse_args()
@@ -75,6 +75,32 @@ def probe_gemv_stress(calls: int) -> None:
     dst.copy_(src)
     torch.cuda.synchronize()
     print("probe: 512 MiB copy done", flush=True)
+
+
+def probe_gemm_prefill(calls: int) -> None:
+    """Prefill GEMM alone at M=2048 and M=32 on both prefill shapes (pre-quantized activations)."""
+    import numpy as np
+    import torch
+
+    from ivonar_amd import ops, runtime, synthetic
+
+    device = torch.device("cuda", 0)
+    runtime.initialise(0)
+    props = torch.cuda.get_device_properties(device)
+    print(f"probe: {props.name} CUs={props.multi_processor_count} "
+          f"lds_per_block={getattr(props, 'shared_memory_per_block', '?')}", flush=True)
+    rng = np.random.default_rng(2)
+    for layer, k in synthetic.prefill_layers(seed=2):
+        mat = device_copies(layer, device, 1)[0]
+        for m in (2048, 32):
+            xs = torch.from_numpy(synthetic.prefill_activations(rng, m, k)).to(device)
+            q8, xsum, sx = ops.quantize_rows(xs)
+            out = torch.empty((m, layer.rows), dtype=torch.float32, device=device)
+            torch.cuda.synchronize()
+            for _ in range(calls):
+                ops.gemm(mat, q8, xsum, sx, out=out)
+            torch.cuda.synchronize()
+            print(f"probe: gemm m={m} {k}->{layer.rows} x{calls} done", flush=True)
 
 
 def graph_of(step, stream):
@@ -134,6 +160,9 @@ def main() -> None:
     if args.probe == "gemv-stress":
         probe_gemv_stress(args.probe_calls)
         return
+    if args.probe == "gemm-prefill":
+        probe_gemm_prefill(args.probe_calls)
+        return
     import numpy as np
     import torch
 
@@ -182,6 +211,21 @@ def main() -> None:
         t = time_graph(g, max(1, args.steps // ROTATING_COPIES), 2) / ROTATING_COPIES
         b = gemv_bytes(1, layer.rows, layer.in_features)
         kernel[f"{layer.in_features}x{layer.rows}"] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
+    # the same shapes through the K-split MFMA kernel (gemm_tile_store with one token)
+    skinny = {}
+    for shape, (layer, x) in enumerate(stress):
+        q8, xsum, sx = ops.quantize_rows(inputs[shape].reshape(1, -1))
+        out2 = torch.empty((1, layer.rows), dtype=torch.float32, device=device)
+
+        def mfma_m1(shape=shape, q8=q8, xsum=xsum, sx=sx, out2=out2):
+            for copy in range(ROTATING_COPIES):
+                ops.gemm(matrices[shape][copy], q8, xsum, sx, out=out2)
+
+        g = graph_of(mfma_m1, stream)
+        t = time_graph(g, max(1, args.steps // ROTATING_COPIES), 2) / ROTATING_COPIES
+        b = gemv_bytes(1, layer.rows, layer.in_features)
+        skinny[f"{layer.in_features}x{layer.rows}"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1)}
+    results["mfma_m1_stress"] = skinny
     kernel_bytes = sum(v["bytes"] for v in kernel.values())
     kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
     achieved = kernel_bytes / kernel_seconds / 1e9

@@ -59,6 +59,12 @@ int ivonar_abi_version(void);
  * per lane; the lane count fixes its fp32 summation order.  Host only. */
 void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane);
 
+/* K-splits S of the token GEMM (gemm_tile_*) for m tokens: its fp32 order is S
+ * contiguous ranges of the 128-input groups, each summed in ascending order,
+ * then the S partial sums added in order (S = 1: one chain).  Uses the
+ * current device's LDS size. */
+int ivonar_gemm_plan(int m, int rows, int n);
+
 /* ------------------------------------------------------------ decode GEMV
  * GEMV_ARGS of ternary.cu:293-298.  y[r] = s_x * sum_g P[r,g]*scale[r,g]
  * (+ bias[r]).  Prologue: PLAIN quantizes `input`, NORM applies RMSNorm

@@ -5,7 +5,7 @@
 
 #include <mutex>
 
-#include "../../include/ivonar_ternary.h"
+#include "ivonar_ternary.h"
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -180,6 +180,8 @@ const char* ivonar_error_string(hipError_t status) { return hipGetErrorString(st
 int ivonar_abi_version(void) { return IVONAR_ABI_VERSION; }
 
 void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane) { gemv_plan(rows, n, lanes, rows_per_lane); }
+
+int ivonar_gemm_plan(int m, int rows, int n) { return gemm_splits(m, rows, n); }
 
 #define GEMV_PASS_ENTRY(MODE, EPI, PREQUANT)                                                                      \
   gemv_entry(stream, MODE, EPI, PREQUANT, input, aux, q8_in, xsum_in, scale_in, packed, scales, bias, output, rows, \

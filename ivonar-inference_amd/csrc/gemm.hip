@@ -1,20 +1,30 @@
-// Token-tile GEMM on CDNA4 int8 MFMA (reference: kernels/ternary.cu:688-784,
+// Token GEMM on CDNA4 int8 MFMA (reference: kernels/ternary.cu:688-784,
 // entry points gemm_tile_* with GEMM_ARGS; the reference uses dp4a).
 //
 // y[t, r] = s_x[t] * sum_g P[t, r, g] * scale[r, g] (+ bias[r]), where
 // P[t, r, g] = sum over the 128 inputs of group g of (code - 1) * q is exact.
 //
-// Each wave owns 16 weight rows and MT 16-token tiles.  Per 128-input group a
-// lane (row = lane % 16, k-block = lane / 16) loads 8 packed bytes, i.e.
-// words 2kb and 2kb+1 of the group's 32 bytes, and expands each word to 16
-// int8 codes in registers ((w >> 2k) & 0x03030303); those are the B operands
-// of two v_mfma_i32_16x16x64_i8.  The A operands are the 16-byte q8 quads of
-// the same words, which the q8 layout stores in exactly the order the
-// expansion produces, so one MFMA pair gives sum(code * q) for 16 tokens x 16
-// rows over the group with int32 accumulation.  Subtracting the group's
-// activation sum turns codes into ternary values; one fmaf per output folds
-// P * scale[r, g] into an fp32 accumulator in ascending group order (the
-// order restated by the CPU oracle, orc_gemm_seq).
+// Block tile: (64*WM) tokens x (64*WN) weight rows, WM*WN waves, each wave a
+// 64 x 64 output tile = 4 x 4 MFMA tiles of v_mfma_i32_16x16x64_i8.  The K
+// loop walks the 128-input groups.  For each group the block stages, double
+// buffered in LDS:
+//   * the q8 bytes of its tokens (128 per token, the q8 layout's two chunks);
+//   * its weight rows' 32 packed bytes, expanded once per block to signed
+//     int8 (code - 1) with one v_perm_b32 table lookup per 4 codes, so the
+//     MFMA produces P directly (no activation-sum correction);
+//   * the fp16 group scales of its rows.
+// LDS rows are padded from 128 to 144 bytes, which spreads the 16 lanes of
+// each 16-byte operand read over distinct banks.  The global loads of group
+// g+1 are issued before the MFMAs of group g and written to the other buffer
+// after them, with one barrier per group.
+//
+// Operand pairing: MFMA half h of a group takes, in lane (c = lane % 16,
+// kb = lane / 16), the 16 bytes of word 2*kb + h of the group (inputs
+// 16*(2kb+h) .. +15).  The q8 layout stores a word's quad in exactly the
+// order the expansion (w >> 2k) & 0x03030303 produces, so both operands see
+// the same input in the same byte slot.  Each group's int32 tile is folded
+// into fp32 with one fmaf per output in ascending group order (the order the
+// CPU oracle restates as orc_gemm_seq).
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -23,103 +33,242 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ v4i expand_word(unsigned w) {
-  v4i v;
-  v.x = (int)(w & kLow2);
-  v.y = (int)((w >> 2) & kLow2);
-  v.z = (int)((w >> 4) & kLow2);
-  v.w = (int)((w >> 6) & kLow2);
-  return v;
+constexpr int kRowPitch = 144;        // bytes per staged LDS row (128 + 16 padding)
+constexpr unsigned kSignedLut = 0x000100FFu;  // v_perm table: code 0 -> -1, 1 -> 0, 2 -> +1
+
+__device__ __forceinline__ unsigned signed_codes(unsigned w, int k) {
+  return __builtin_amdgcn_perm(0u, kSignedLut, (w >> (2 * k)) & kLow2);
 }
 
-template <int EPI, int MT>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
+template <int WM, int WN>
+struct Tile {
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreadsPerBlock = 64 * kWaves;
+  static constexpr int kTokens = 64 * WM;
+  static constexpr int kRowsPerBlock = 64 * WN;
+  static constexpr int kStageBytes = (kTokens + kRowsPerBlock) * kRowPitch + kRowsPerBlock * 4;
+};
+
+template <int EPI, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __restrict__ q8,
+                                                            const float* __restrict__ scale_in,
+                                                            const uint8_t* __restrict__ packed,
+                                                            const uint16_t* __restrict__ scales,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ output, GemmArgs a) {
+  using T = Tile<WM, WN>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int col = lane & 15, kb = lane >> 4;
   const int chunks = (a.n + kChunk - 1) / kChunk;
   const int groups = (a.n + kGroup - 1) / kGroup;
-  const int lane = threadIdx.x & 63;
-  const int col = lane & 15;   // weight row inside the wave's 16 and token inside an A tile
-  const int kb = lane >> 4;    // k-block of the MFMA operands; also the output token quad
-  const int row = (blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * 16 + col;
-  const int token0 = blockIdx.y * (16 * MT);
-  const bool row_live = row < a.rows;
-  const uint8_t* wrow = a.packed + (size_t)(row_live ? row : 0) * a.row_bytes;
-  const uint16_t* srow = a.scales + (size_t)(row_live ? row : 0) * a.groups;
   const size_t q8_stride = (size_t)chunks * kChunk;
+  const int token0 = blockIdx.y * T::kTokens;
+  const int row0 = blockIdx.x * T::kRowsPerBlock;
 
-  float acc[MT][4];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
+  // Staging: A in 64-byte pieces (two per token), B in 16-byte packed pieces
+  // (two per weight row, each expanding to 64 bytes), one scale per row.
+  constexpr int kThreadsN = T::kThreadsPerBlock;
+  constexpr int kPiecesA = (2 * T::kTokens + kThreadsN - 1) / kThreadsN;
+  constexpr int kPiecesB = (2 * T::kRowsPerBlock + kThreadsN - 1) / kThreadsN;
+  uint4 ra[kPiecesA][4];
+  uint4 rb[kPiecesB];
+  uint16_t rs = 0;
+  const bool s_thread = tid < T::kRowsPerBlock;
+  const uint16_t* s_src = scales + (size_t)min(row0 + tid % T::kRowsPerBlock, a.rows - 1) * a.groups;
 
-  for (int g = 0; g < groups; ++g) {
-    // Bytes [8kb, 8kb+8) of the group: chunk 2g for kb < 2, chunk 2g+1 otherwise.
-    const bool part_live = (2 * g + (kb >> 1)) < chunks;
-    uint2 w = make_uint2(0u, 0u);
-    if (row_live && part_live) w = *reinterpret_cast<const uint2*>(wrow + (size_t)g * 32 + kb * 8);
-    const v4i b0 = expand_word(w.x);
-    const v4i b1 = expand_word(w.y);
-    const float scale = row_live ? h2f(srow[g]) : 0.0f;
+  auto fetch = [&](int g) {
+    const bool second_live = 2 * g + 1 < chunks;  // does chunk 2g+1 exist?
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int t_in = token0 + mt * 16 + col;
-      v4i a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-      if (t_in < a.m && part_live) {
-        const v4i* q = reinterpret_cast<const v4i*>(a.q8_in + (size_t)t_in * q8_stride + (size_t)g * kGroup +
-                                                    (size_t)kb * 32);
-        a0 = q[0];
-        a1 = q[1];
-      }
-      v4i d = {0, 0, 0, 0};
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+    for (int k = 0; k < kPiecesA; ++k) {
+      const int piece = tid + k * kThreadsN;
+      const int token = min(token0 + piece % T::kTokens, a.m - 1), half = piece / T::kTokens;
+      const bool live = piece < 2 * T::kTokens && (half == 0 || second_live);
+      const int8_t* src = q8 + (size_t)token * q8_stride + (size_t)g * kGroup + half * 64;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = token0 + mt * 16 + kb * 4 + i;
-        int xs = 0;
-        if (t < a.m) {
-          const int32_t* xrow = a.xsum_in + (size_t)t * chunks;
-          xs = xrow[2 * g] + (2 * g + 1 < chunks ? xrow[2 * g + 1] : 0);
-        }
-        acc[mt][i] = __builtin_fmaf((float)(d[i] - xs), scale, acc[mt][i]);
+      for (int i = 0; i < 4; ++i)
+        ra[k][i] = live ? *reinterpret_cast<const uint4*>(src + i * 16) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < kPiecesB; ++k) {
+      const int piece = tid + k * kThreadsN;
+      const int row = min(row0 + piece % T::kRowsPerBlock, a.rows - 1), half = piece / T::kRowsPerBlock;
+      const bool live = piece < 2 * T::kRowsPerBlock && (half == 0 || second_live);
+      rb[k] = live ? *reinterpret_cast<const uint4*>(packed + (size_t)row * a.row_bytes + (size_t)g * 32 + half * 16)
+                   : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (s_thread) rs = s_src[g];
+  };
+  auto stage = [&](int g, int buffer) {
+    unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
+#pragma unroll
+    for (int k = 0; k < kPiecesA; ++k) {
+      const int piece = tid + k * kThreadsN;
+      if (piece < 2 * T::kTokens) {
+        unsigned char* dst = base + (piece % T::kTokens) * kRowPitch + (piece / T::kTokens) * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(dst + i * 16) = ra[k][i];
       }
     }
+#pragma unroll
+    for (int k = 0; k < kPiecesB; ++k) {
+      const int piece = tid + k * kThreadsN;
+      if (piece < 2 * T::kRowsPerBlock) {
+        // A dead second chunk stages zero activations, so its weight bytes need no masking.
+        unsigned char* dst = base + (T::kTokens + piece % T::kRowsPerBlock) * kRowPitch + (piece / T::kRowsPerBlock) * 64;
+        const unsigned words[4] = {rb[k].x, rb[k].y, rb[k].z, rb[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint4 e;
+          e.x = signed_codes(words[j], 0);
+          e.y = signed_codes(words[j], 1);
+          e.z = signed_codes(words[j], 2);
+          e.w = signed_codes(words[j], 3);
+          *reinterpret_cast<uint4*>(dst + j * 16) = e;
+        }
+      }
+    }
+    if (s_thread) reinterpret_cast<float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch)[tid] = h2f(rs);
+  };
+
+  float acc[4][4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
+
+  fetch(0);
+  stage(0, 0);
+  __syncthreads();
+  for (int g = 0; g < groups; ++g) {
+    const int buffer = g & 1;
+    if (g + 1 < groups) fetch(g + 1);
+    const unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
+    const unsigned char* a_lds = base + (wm * 64 + col) * kRowPitch;
+    const unsigned char* b_lds = base + (T::kTokens + wn * 64 + col) * kRowPitch;
+    v4i p[4][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i af[4], bf[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        af[mt] = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb + h) * 16);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        bf[nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb + h) * 16);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const v4i zero = {0, 0, 0, 0};
+          p[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bf[nt], h == 0 ? zero : p[mt][nt], 0, 0, 0);
+        }
+    }
+    const float* s_lds = reinterpret_cast<const float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const float s = s_lds[wn * 64 + nt * 16 + col];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][nt][i] = __builtin_fmaf((float)p[mt][nt][i], s, acc[mt][nt][i]);
+    }
+    if (g + 1 < groups) stage(g + 1, buffer ^ 1);
+    __syncthreads();
   }
 
-  const float bias = (a.bias != nullptr && row_live) ? a.bias[row] : 0.0f;
+  // Epilogue: lane holds rows row0 + wn*64 + nt*16 + col, tokens token0 + wm*64 + mt*16 + 4*kb + i.
+  const bool full = token0 + T::kTokens <= a.m && row0 + T::kRowsPerBlock <= a.rows;
+  float sx[4][4];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = token0 + mt * 16 + kb * 4 + i;
-      const bool live = t < a.m && row_live;
-      float y = acc[mt][i] * (t < a.m ? a.scale_in[t] : 0.0f);
-      if (a.bias != nullptr) y = y + bias;
-      float* orow = a.output + (size_t)(t < a.m ? t : 0) * a.out_stride;
-      if constexpr (EPI == kSiluPair) {
-        const float partner = __shfl_xor(y, 1);
-        if (live && (row & 1) == 0 && row + 1 < a.rows) orow[row >> 1] = ivo_silu(y) * partner;
-      } else if constexpr (EPI == kResidual) {
-        if (live) orow[row] = orow[row] + y;
-      } else {
-        if (live) orow[row] = y;
+    for (int i = 0; i < 4; ++i) sx[mt][i] = scale_in[min(token0 + wm * 64 + mt * 16 + 4 * kb + i, a.m - 1)];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int row = row0 + wn * 64 + nt * 16 + col;
+    const bool row_live = row < a.rows;
+    const float b = (bias != nullptr && row_live) ? bias[row] : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = token0 + wm * 64 + mt * 16 + 4 * kb + i;
+        const bool live = full || (row_live && t < a.m);
+        float y = acc[mt][nt][i] * sx[mt][i];
+        if (bias != nullptr) y = y + b;
+        float* orow = output + (size_t)min(t, a.m - 1) * a.out_stride;
+        if constexpr (EPI == kSiluPair) {
+          const float partner = __shfl_xor(y, 1);
+          if (live && (row & 1) == 0 && row + 1 < a.rows) orow[row >> 1] = ivo_silu(y) * partner;
+        } else if constexpr (EPI == kResidual) {
+          if (live) orow[row] = orow[row] + y;
+        } else {
+          if (live) orow[row] = y;
+        }
       }
     }
   }
 }
 
-template <int EPI>
-hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
-  constexpr int MT = 2;
-  const dim3 grid(ceil_div(a.rows, 16 * (kThreads / 64)), ceil_div(a.m, 16 * MT));
-  hipLaunchKernelGGL((gemm_kernel<EPI, MT>), grid, dim3(kThreads), 0, stream, a);
+template <int EPI, int WM, int WN>
+hipError_t launch_shape(hipStream_t stream, const GemmArgs& a) {
+  using T = Tile<WM, WN>;
+  const dim3 grid(ceil_div(a.rows, T::kRowsPerBlock), ceil_div(a.m, T::kTokens));
+  const size_t lds = 2 * (size_t)T::kStageBytes;
+  hipLaunchKernelGGL((gemm_kernel<EPI, WM, WN>), grid, dim3(T::kThreadsPerBlock), lds, stream, a.q8_in, a.scale_in,
+                     a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
+int max_lds_per_block() {
+  static int cached[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 64 * 1024;
+  if (cached[device] == 0) {
+    int bytes = 0;
+    if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess || bytes <= 0)
+      bytes = 64 * 1024;
+    cached[device] = bytes;
+  }
+  return cached[device];
+}
+
+namespace {
+
+template <int WM, int WN>
+bool fits() {
+  return 2 * Tile<WM, WN>::kStageBytes <= max_lds_per_block();
+}
+
+// Block shape: the largest tile that still gives about one block per CU and
+// whose double-buffered stage fits the device's LDS per block.
+template <int EPI>
+hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
+  const long long tiles_2x2 = (long long)ceil_div(a.rows, 128) * ceil_div(a.m, 128);
+  if (a.m > 64 && tiles_2x2 >= 200 && fits<2, 2>()) return launch_shape<EPI, 2, 2>(stream, a);
+  if (a.m > 64) return launch_shape<EPI, 2, 1>(stream, a);
+  return launch_shape<EPI, 1, 1>(stream, a);
+}
+
+}  // namespace
+
+int gemm_splits(int m, int rows, int n) {
+  const int splits = skinny_splits(m, rows, n, (size_t)max_lds_per_block());
+  return splits > 0 ? splits : 1;
+}
+
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (a.rows <= 0 || a.m <= 0) return hipSuccess;
+  const int splits = skinny_splits(a.m, a.rows, a.n, (size_t)max_lds_per_block());
+  if (splits > 0) return launch_skinny(stream, a, splits);
   switch (a.epi) {
     case kStore: return launch_epi<kStore>(stream, a);
     case kResidual: return launch_epi<kResidual>(stream, a);

@@ -38,13 +38,13 @@ namespace {
 constexpr int kRows = 2;  // rows per lane; even, so a silu pair stays in one lane
 constexpr int kFusedLimit = 4096;
 constexpr int kMaxLdsBytes = 64 * 1024;
-constexpr int kMaxSteps = 8;
 constexpr int kBlocksPerCu = 4;
 
 struct GemvShape {
   int rows, n, row_bytes, groups, splits, head_dim;
   float eps;
   int lanes, lane_shift, iters;
+  int exact;  // every lane's chunks exist (C is a multiple of lanes): no per-chunk masks
 };
 
 struct GemvPtrs {
@@ -65,13 +65,14 @@ __device__ __forceinline__ uint4 load16(const uint8_t* __restrict__ p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-template <int NJ, bool SCALES>
+template <int NJ, bool SCALES, int LANES>
 __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restrict__ packed,
                                           const uint16_t* __restrict__ scales, const GemvShape& sh, int row0,
                                           int j0, int sub, int chunks) {
+  const int lanes = LANES ? LANES : sh.lanes;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int u = min((j0 + j) * sh.lanes + sub, chunks - 1);
+    const int u = min((j0 + j) * lanes + sub, chunks - 1);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
       const int row = min(row0 + r, sh.rows - 1);
@@ -81,18 +82,19 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
   }
 }
 
-template <int EPI, int NJ, bool QREG>
+template <int EPI, int NJ, bool QREG, int LANES, bool EXACT>
 __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr)[QREG ? NJ : 1][4],
                                              const int (&xr)[QREG ? NJ : 1], const int4* __restrict__ lds_q,
                                              const int* __restrict__ lds_x, float (&acc)[kRows],
                                              int32_t* __restrict__ partials, const GemvShape& sh, int row0, int j0,
                                              int sub, int chunks) {
+  const int lanes = LANES ? LANES : sh.lanes;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int u_raw = (j0 + j) * sh.lanes + sub;
-    const bool live = u_raw < chunks;
+    const int u_raw = (j0 + j) * lanes + sub;
+    const bool live = EXACT || u_raw < chunks;
     const int g = u_raw >> 1;
-    const bool group_live = 2 * g < chunks;
+    const bool group_live = EXACT || 2 * g < chunks;
     int4 q0, q1, q2, q3;
     int xs;
     if constexpr (QREG) {
@@ -111,27 +113,28 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
     }
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-      int d = chunk_code_dot(st.w[j][r], q0, q1, q2, q3, 0) - xs;
-      d = live ? d : 0;
+      int d = chunk_code_dot(st.w[j][r], q0, q1, q2, q3, -xs);
+      if constexpr (!EXACT) d = live ? d : 0;
       d += pair_swap(d);
       const int row = row0 + r;
       if constexpr (EPI == kPartials) {
         if (group_live && (sub & 1) == 0 && row < sh.rows) partials[(size_t)row * sh.groups + g] = d;
       } else {
-        const float contribution = group_live ? (float)d : 0.0f;
+        const float contribution = EXACT || group_live ? (float)d : 0.0f;
         acc[r] = __builtin_fmaf(contribution, h2f(st.s[j][r]), acc[r]);
       }
     }
   }
 }
 
-template <int MODE, int EPI, bool FUSED, int NJ>
+template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
                                                         const float* __restrict__ bias, float* __restrict__ output,
                                                         int32_t* __restrict__ partials, GemvShape sh) {
-  constexpr bool QREG = NJ <= 2;
-  constexpr bool DOUBLE = NJ <= 2;
+  // One block of steps per row (no rolling over steps) keeps the lane's q8
+  // words in registers; rows of several blocks read them from LDS.
+  constexpr bool QREG = !ROLL;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ float slots[64];
   const int chunks = (sh.n + kChunk - 1) / kChunk;
@@ -139,19 +142,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
   int* lds_x = reinterpret_cast<int*>(lds_raw + (size_t)chunks * kChunk);
 
   const int lane = threadIdx.x & 63;
-  const int sub = lane & (sh.lanes - 1);
-  const int slot = lane >> sh.lane_shift;
-  const int rows_per_iter = (64 >> sh.lane_shift) * kRows;
+  const int lanes = LANES ? LANES : sh.lanes;
+  const int lane_shift = LANES ? __builtin_ctz(LANES) : sh.lane_shift;
+  const int sub = lane & (lanes - 1);
+  const int slot = lane >> lane_shift;
+  const int rows_per_iter = (64 >> lane_shift) * kRows;
   const int waves = gridDim.x * (kThreads / 64);
   const int first = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  const int steps = (chunks + sh.lanes - 1) / sh.lanes;
+  const int steps = (chunks + lanes - 1) / lanes;
 
   // Weights of the first row step go out before the activation prologue.
   // Loads are never predicated (rows past the matrix are clamped inside
   // load_step), so the wait counts before each use stay exact.
   Step<NJ> a, b;
   int it = first;
-  load_step<NJ, EPI != kPartials>(a, packed, scales, sh, it * rows_per_iter + slot * kRows, 0, sub, chunks);
+  load_step<NJ, EPI != kPartials, LANES>(a, packed, scales, sh, it * rows_per_iter + slot * kRows, 0, sub, chunks);
 
   float sx;
   if constexpr (FUSED) {
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
   if constexpr (QREG) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int u = min(j * sh.lanes + sub, chunks - 1);
+      const int u = min(j * lanes + sub, chunks - 1);
 #pragma unroll
       for (int w = 0; w < 4; ++w) qr[j][w] = lds_q[w * chunks + u];
       xr[j] = lds_x[u];
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
     if constexpr (EPI != kPartials) {
 #pragma unroll
       for (int r = 0; r < kRows; ++r) {
-        for (int offset = 2; offset < sh.lanes; offset <<= 1) acc[r] = acc[r] + __shfl_xor(acc[r], offset);
+        for (int offset = 2; offset < lanes; offset <<= 1) acc[r] = acc[r] + __shfl_xor(acc[r], offset);
       }
       if (sub == 0) {
         float y[kRows];
@@ -214,42 +219,52 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
     }
   };
 
-  if constexpr (DOUBLE) {
-    // steps <= NJ: one Step covers the whole row; prefetch the next row step.
-    while (it < sh.iters) {
-      const int row0 = it * rows_per_iter + slot * kRows;
-      const int next = it + waves;
-      load_step<NJ, EPI != kPartials>(b, packed, scales, sh, next * rows_per_iter + slot * kRows, 0, sub, chunks);
-      float acc[kRows];
+  // Rolling pipeline over items (row step, block of NJ steps): the next
+  // item's weights are in flight while the current one is computed.
+  const int blocks_per_row = (steps + NJ - 1) / NJ;
+  int jb = 0;
+  float acc[kRows];
 #pragma unroll
-      for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
-      compute_step<EPI, NJ, QREG>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, 0, sub, chunks);
-      finish(acc, row0);
-      it = next;
-      if (it >= sh.iters) break;
-      const int row1 = it * rows_per_iter + slot * kRows;
-      const int next2 = it + waves;
-      load_step<NJ, EPI != kPartials>(a, packed, scales, sh, next2 * rows_per_iter + slot * kRows, 0, sub, chunks);
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
-      compute_step<EPI, NJ, QREG>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row1, 0, sub, chunks);
-      finish(acc, row1);
-      it = next2;
-    }
-  } else {
-    // Long rows: the row is covered in blocks of NJ steps; all of a block's loads are in flight together.
-    bool preloaded = true;
-    for (; it < sh.iters; it += waves) {
-      const int row0 = it * rows_per_iter + slot * kRows;
-      float acc[kRows];
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
-      for (int j0 = 0; j0 < steps; j0 += NJ) {
-        if (!preloaded) load_step<NJ, EPI != kPartials>(a, packed, scales, sh, row0, j0, sub, chunks);
-        preloaded = false;
-        compute_step<EPI, NJ, QREG>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, j0, sub, chunks);
+  for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+  while (it < sh.iters) {
+    {
+      int it_next = it, jb_next = jb + 1;
+      if (jb_next == blocks_per_row) {
+        jb_next = 0;
+        it_next = it + waves;
       }
-      finish(acc, row0);
+      const int row0 = it * rows_per_iter + slot * kRows;
+      load_step<NJ, EPI != kPartials, LANES>(b, packed, scales, sh, it_next * rows_per_iter + slot * kRows,
+                                             jb_next * NJ, sub, chunks);
+      compute_step<EPI, NJ, QREG, LANES, EXACT>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
+                                                chunks);
+      if (jb == blocks_per_row - 1) {
+        finish(acc, row0);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+      }
+      it = it_next;
+      jb = jb_next;
+    }
+    if (it >= sh.iters) break;
+    {
+      int it_next = it, jb_next = jb + 1;
+      if (jb_next == blocks_per_row) {
+        jb_next = 0;
+        it_next = it + waves;
+      }
+      const int row0 = it * rows_per_iter + slot * kRows;
+      load_step<NJ, EPI != kPartials, LANES>(a, packed, scales, sh, it_next * rows_per_iter + slot * kRows,
+                                             jb_next * NJ, sub, chunks);
+      compute_step<EPI, NJ, QREG, LANES, EXACT>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
+                                                chunks);
+      if (jb == blocks_per_row - 1) {
+        finish(acc, row0);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+      }
+      it = it_next;
+      jb = jb_next;
     }
   }
 }
@@ -267,29 +282,47 @@ int device_cus() {
   return cached[device];
 }
 
-template <int MODE, int EPI, bool FUSED, int NJ>
+template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
 void launch_one(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                 size_t lds) {
-  hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, NJ>), dim3(blocks), dim3(kThreads), lds, stream, p, a.packed,
-                     a.scales, a.bias, a.output, a.partials, sh);
+  hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, NJ, LANES, EXACT, ROLL>), dim3(blocks), dim3(kThreads), lds,
+                     stream, p, a.packed, a.scales, a.bias, a.output, a.partials, sh);
+}
+
+// Compiled layouts: 64 lanes per row (rows of more than 32 chunks) with or
+// without dead lanes, and any narrower power of two (one step) likewise.
+template <int MODE, int EPI, bool FUSED, int NJ, bool ROLL>
+void launch_layout(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
+                   size_t lds) {
+  if (sh.lanes == 64) {
+    if (sh.exact) launch_one<MODE, EPI, FUSED, NJ, 64, true, ROLL>(stream, p, a, sh, blocks, lds);
+    else launch_one<MODE, EPI, FUSED, NJ, 64, false, ROLL>(stream, p, a, sh, blocks, lds);
+  } else if constexpr (NJ == 1 && !ROLL) {
+    if (sh.exact) launch_one<MODE, EPI, FUSED, 1, 0, true, false>(stream, p, a, sh, blocks, lds);
+    else launch_one<MODE, EPI, FUSED, 1, 0, false, false>(stream, p, a, sh, blocks, lds);
+  }
+}
+
+// Steps per pipeline item: a whole row of up to two steps (q8 in registers),
+// else the largest of 4, 2, 1 that divides the row's steps (no dead steps).
+int steps_per_item(int steps) {
+  if (steps <= 2) return steps;
+  if (steps % 4 == 0) return 4;
+  if (steps % 2 == 0) return 2;
+  return 1;
 }
 
 template <int MODE, int EPI, bool FUSED>
 hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                      size_t lds, int steps) {
-  if constexpr (FUSED) {
-    launch_one<MODE, EPI, FUSED, 1>(stream, p, a, sh, blocks, lds);  // fused rows need one step per lane
-  } else {
-    switch (steps) {
-      case 1: launch_one<MODE, EPI, FUSED, 1>(stream, p, a, sh, blocks, lds); break;
-      case 2: launch_one<MODE, EPI, FUSED, 2>(stream, p, a, sh, blocks, lds); break;
-      case 3: launch_one<MODE, EPI, FUSED, 3>(stream, p, a, sh, blocks, lds); break;
-      case 4: launch_one<MODE, EPI, FUSED, 4>(stream, p, a, sh, blocks, lds); break;
-      case 5: launch_one<MODE, EPI, FUSED, 5>(stream, p, a, sh, blocks, lds); break;
-      case 6: launch_one<MODE, EPI, FUSED, 6>(stream, p, a, sh, blocks, lds); break;
-      case 7: launch_one<MODE, EPI, FUSED, 7>(stream, p, a, sh, blocks, lds); break;
-      default: launch_one<MODE, EPI, FUSED, kMaxSteps>(stream, p, a, sh, blocks, lds); break;
-    }
+  const int nj = steps_per_item(steps);
+  if (steps <= 2) {
+    if (nj == 1) launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
+    else launch_layout<MODE, EPI, FUSED, 2, false>(stream, p, a, sh, blocks, lds);
+  } else if constexpr (!FUSED) {
+    if (nj == 4) launch_layout<MODE, EPI, FUSED, 4, true>(stream, p, a, sh, blocks, lds);
+    else if (nj == 2) launch_layout<MODE, EPI, FUSED, 2, true>(stream, p, a, sh, blocks, lds);
+    else launch_layout<MODE, EPI, FUSED, 1, true>(stream, p, a, sh, blocks, lds);
   }
   return hipGetLastError();
 }
@@ -338,6 +371,8 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   sh.lane_shift = __builtin_ctz((unsigned)lanes);
   sh.iters = ceil_div(a.rows, (64 / lanes) * rows_per_lane);
   const int steps = ceil_div(chunks, lanes);
+  // Dead lanes exist when the last step is partial (items never hold dead steps).
+  sh.exact = chunks % lanes == 0;
   const int cus = device_cus();
   const bool fused = a.q8_in == nullptr && a.n <= kFusedLimit;
   int blocks = ceil_div(sh.iters, kThreads / 64);

@@ -89,6 +89,13 @@ struct GemmArgs {
 };
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a);
 
+// K-splits of the GEMM for m tokens (its fp32 order: S contiguous group ranges,
+// each an fmaf chain, added in order); 1 = one chain over all groups.
+int gemm_splits(int m, int rows, int n);
+int max_lds_per_block();
+int skinny_splits(int m, int rows, int n, size_t max_lds);  // 0 = does not apply
+hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, int splits);
+
 hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const uint8_t* packed,
                         const uint16_t* scales, float* output, int n, int row_bytes, int groups);
 hipError_t launch_gather(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid);

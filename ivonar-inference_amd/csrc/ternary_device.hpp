@@ -64,25 +64,28 @@ __device__ __forceinline__ int sdot4(unsigned a, int b, int c) {
 }
 
 // Sum over one 64-input chunk of code * q: 16 packed words against 16 q8 words.
+// Each packed word w holds 16 codes as four byte-wise 2-bit fields; instead of
+// shifting every field down (7 ops), the fields are isolated in place with
+// masks (w & 0x03, w & 0x0c, w & 0x30 per byte, and (w >> 2) & 0x30 for the
+// top field: 5 ops), so the dot products see code, 4*code and 16*code.  Three
+// accumulators keep those weights apart and are recombined exactly
+// (a multiple of 4 or 16 shifts right without loss).
+__device__ __forceinline__ int word_code_dot(unsigned w, int4 q, int& a1, int& a4, int& a16) {
+  a1 = sdot4(w & 0x03030303u, q.x, a1);
+  a4 = sdot4(w & 0x0c0c0c0cu, q.y, a4);
+  a16 = sdot4(w & 0x30303030u, q.z, a16);
+  a16 = sdot4((w >> 2) & 0x30303030u, q.w, a16);
+  return 0;
+}
+
 __device__ __forceinline__ int chunk_code_dot(const uint4 w, const int4 q0, const int4 q1, const int4 q2,
                                               const int4 q3, int acc) {
-  acc = sdot4(w.x & kLow2, q0.x, acc);
-  acc = sdot4((w.x >> 2) & kLow2, q0.y, acc);
-  acc = sdot4((w.x >> 4) & kLow2, q0.z, acc);
-  acc = sdot4((w.x >> 6) & kLow2, q0.w, acc);
-  acc = sdot4(w.y & kLow2, q1.x, acc);
-  acc = sdot4((w.y >> 2) & kLow2, q1.y, acc);
-  acc = sdot4((w.y >> 4) & kLow2, q1.z, acc);
-  acc = sdot4((w.y >> 6) & kLow2, q1.w, acc);
-  acc = sdot4(w.z & kLow2, q2.x, acc);
-  acc = sdot4((w.z >> 2) & kLow2, q2.y, acc);
-  acc = sdot4((w.z >> 4) & kLow2, q2.z, acc);
-  acc = sdot4((w.z >> 6) & kLow2, q2.w, acc);
-  acc = sdot4(w.w & kLow2, q3.x, acc);
-  acc = sdot4((w.w >> 2) & kLow2, q3.y, acc);
-  acc = sdot4((w.w >> 4) & kLow2, q3.z, acc);
-  acc = sdot4((w.w >> 6) & kLow2, q3.w, acc);
-  return acc;
+  int a1 = acc, a4 = 0, a16 = 0;
+  word_code_dot(w.x, q0, a1, a4, a16);
+  word_code_dot(w.y, q1, a1, a4, a16);
+  word_code_dot(w.z, q2, a1, a4, a16);
+  word_code_dot(w.w, q3, a1, a4, a16);
+  return a1 + (a4 >> 2) + (a16 >> 4);
 }
 
 // Lane value of the partner in the same lane pair (quad_perm [1,0,3,2]).

@@ -98,6 +98,8 @@ def library() -> ctypes.CDLL:
             lib.ivonar_define.restype = c_int
             lib.ivonar_gemv_plan.argtypes = [c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]
             lib.ivonar_gemv_plan.restype = None
+            lib.ivonar_gemm_plan.argtypes = [c_int, c_int, c_int]
+            lib.ivonar_gemm_plan.restype = c_int
             for name, argtypes in SIGNATURES.items():
                 function = getattr(lib, name)
                 function.argtypes = [c_void_p, *argtypes]
@@ -117,6 +119,11 @@ def gemv_plan(rows: int, n: int) -> tuple[int, int]:
     lanes, per_lane = c_int(), c_int()
     library().ivonar_gemv_plan(int(rows), int(n), ctypes.byref(lanes), ctypes.byref(per_lane))
     return int(lanes.value), int(per_lane.value)
+
+
+def gemm_plan(m: int, rows: int, n: int) -> int:
+    """K-splits of the token GEMM for m tokens (fixes its fp32 summation order)."""
+    return int(library().ivonar_gemm_plan(int(m), int(rows), int(n)))
 
 
 def initialise(device_index: int) -> None:

@@ -260,24 +260,33 @@ void orc_gemv_pairs(int epi, const int8_t* q8, const int32_t* xsum, float sx, co
   free(y);
 }
 
-/* MFMA GEMM order: one fmaf chain over groups per (token, row). */
-void orc_gemm_seq(int epi, const int8_t* q8, const int32_t* xsum, const float* scale_in, const uint8_t* packed,
-                  const uint16_t* scales, const float* bias, float* out, int rows, int n, int row_bytes, int groups,
-                  int out_stride, int m) {
+/* MFMA GEMM order with K split S ways: groups in S contiguous ranges of
+ * ceil(G/S), each range an fmaf chain from zero in ascending order, the S
+ * partial sums then added in range order (S = 1: one chain over all groups). */
+void orc_gemm_split(int epi, const int8_t* q8, const int32_t* xsum, const float* scale_in, const uint8_t* packed,
+                    const uint16_t* scales, const float* bias, float* out, int rows, int n, int row_bytes,
+                    int groups, int out_stride, int m, int splits) {
   const int chunks = (n + 63) >> 6, ngroups = (n + 127) >> 7;
+  const int per = (ngroups + splits - 1) / splits;
   float* y = (float*)malloc(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
   for (int t = 0; t < m; ++t) {
     const int8_t* qrow = q8 + (size_t)t * chunks * 64;
     const int32_t* xrow = xsum + (size_t)t * chunks;
     for (int r = 0; r < rows; ++r) {
       const uint8_t* wrow = packed + (size_t)r * row_bytes;
-      float acc = 0.0f;
-      for (int g = 0; g < ngroups; ++g) {
-        int total = chunk_partial(wrow, qrow, xrow, 2 * g);
-        if (2 * g + 1 < chunks) total += chunk_partial(wrow, qrow, xrow, 2 * g + 1);
-        acc = fmaf((float)total, orc_h2f(scales[(size_t)r * groups + g]), acc);
+      float total = 0.0f;
+      for (int s = 0; s < splits; ++s) {
+        const int begin = s * per < ngroups ? s * per : ngroups;
+        const int end = begin + per < ngroups ? begin + per : ngroups;
+        float acc = 0.0f;
+        for (int g = begin; g < end; ++g) {
+          int p = chunk_partial(wrow, qrow, xrow, 2 * g);
+          if (2 * g + 1 < chunks) p += chunk_partial(wrow, qrow, xrow, 2 * g + 1);
+          acc = fmaf((float)p, orc_h2f(scales[(size_t)r * groups + g]), acc);
+        }
+        total = s == 0 ? acc : total + acc;
       }
-      float v = acc * scale_in[t];
+      float v = total * scale_in[t];
       if (bias) v = v + bias[r];
       y[r] = v;
     }
@@ -291,6 +300,13 @@ void orc_gemm_seq(int epi, const int8_t* q8, const int32_t* xsum, const float* s
     }
   }
   free(y);
+}
+
+/* One fmaf chain over groups per (token, row): the split order with S = 1. */
+void orc_gemm_seq(int epi, const int8_t* q8, const int32_t* xsum, const float* scale_in, const uint8_t* packed,
+                  const uint16_t* scales, const float* bias, float* out, int rows, int n, int row_bytes, int groups,
+                  int out_stride, int m) {
+  orc_gemm_split(epi, q8, xsum, scale_in, packed, scales, bias, out, rows, n, row_bytes, groups, out_stride, m, 1);
 }
 
 /* The reference kernel's own fp32 order (ternary.cu:330-347 for the GEMV,

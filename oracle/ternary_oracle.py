@@ -166,6 +166,8 @@ class Oracle:
                                        c_int, c_int, c_int, c_int, c_int]
         lib.orc_gemm_seq.argtypes = [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_int, c_int, c_int, c_int, c_int, c_int]
+        lib.orc_gemm_split.argtypes = [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_int, c_int, c_int, c_int, c_int, c_int, c_int]
         lib.orc_reforder.argtypes = [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int]
         lib.orc_embed.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int]
@@ -231,6 +233,16 @@ class Oracle:
                               _ptr(np.ascontiguousarray(scale_in, dtype=np.float32)), _ptr(packed), _ptr(scales_bits),
                               _ptr(bias), _ptr(out), packed.shape[0], n, packed.shape[1], scales_bits.shape[1],
                               out_stride, m)
+        return out
+
+    def gemm_split(self, epi: int, q8, xsum, scale_in, packed, scales_bits, bias, out: np.ndarray, n: int,
+                   out_stride: int, m: int, splits: int) -> np.ndarray:
+        packed = np.ascontiguousarray(packed)
+        scales_bits = np.ascontiguousarray(scales_bits, dtype=np.uint16)
+        self.lib.orc_gemm_split(epi, _ptr(np.ascontiguousarray(q8)), _ptr(np.ascontiguousarray(xsum)),
+                                _ptr(np.ascontiguousarray(scale_in, dtype=np.float32)), _ptr(packed), _ptr(scales_bits),
+                                _ptr(bias), _ptr(out), packed.shape[0], n, packed.shape[1], scales_bits.shape[1],
+                                out_stride, m, splits)
         return out
 
     def reforder(self, epi: int, tile: bool, q8, xsum, scale_in, packed, scales_bits, bias, out: np.ndarray, n: int,

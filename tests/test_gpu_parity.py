@@ -250,7 +250,7 @@ def test_gemv_attn_residual(cuda, oracle, head_dim, heads, splits):
 @pytest.mark.parametrize("m", [1, 5, 16, 32, 33, 70])
 @pytest.mark.parametrize("k,rows", [(24, 16), (96, 64), (1024, 256), (4096, 96), (1100, 48)])
 def test_gemm_tile_store(cuda, oracle, m, k, rows):
-    from ivonar_amd import ops
+    from ivonar_amd import ops, runtime
 
     rng = np.random.default_rng(m * 7919 + k + rows)
     codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=(m == 5))
@@ -261,9 +261,10 @@ def test_gemm_tile_store(cuda, oracle, m, k, rows):
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
     assert_bits_equal(to_np(q8), eq8, "tile q8")
-    expected = oracle.gemm_seq(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b, np.zeros((m, rows), np.float32),
-                               k, rows, m)
-    assert_bits_equal(y, expected, "gemm vs oracle (kernel order)")
+    splits = runtime.gemm_plan(m, rows, k)
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                 np.zeros((m, rows), np.float32), k, rows, m, splits)
+    assert_bits_equal(y, expected, f"gemm vs oracle (kernel order, {splits} splits)")
     ref = oracle.reforder(T.EPI_STORE, True, eq8, exsum, esx, packed, scale_bits, b, np.zeros((m, rows), np.float32),
                           k, reference_lanes(k, rows), rows, m)
     assert_within(y, ref, what="gemm vs reference-kernel order")
@@ -272,7 +273,7 @@ def test_gemm_tile_store(cuda, oracle, m, k, rows):
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
 def test_gemm_tile_epilogues(cuda, oracle, epilogue):
     import torch
-    from ivonar_amd import ops
+    from ivonar_amd import ops, runtime
 
     rng = np.random.default_rng(99 if epilogue == "residual" else 98)
     m, k, rows = 32, 1024, 128
@@ -287,7 +288,8 @@ def test_gemm_tile_epilogues(cuda, oracle, epilogue):
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
     epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
-    expected = oracle.gemm_seq(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m)
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m,
+                                 runtime.gemm_plan(m, rows, k))
     assert_bits_equal(to_np(out), expected, epilogue)
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
@@ -390,3 +392,46 @@ def test_invalid_arguments_raise(cuda):
                                   runtime.pointer(torch.empty(7, device=cuda)), 7, 64, 8, matrix.groups, 2, 1,
                                   runtime.float32(1e-6), None, 0)
     assert status != 0  # row_bytes below 16 * chunks
+
+
+@pytest.mark.parametrize("m,k,rows", [(2048, 1024, 4096), (2048, 4096, 1024), (512, 1100, 4096), (300, 4096, 2048)])
+def test_gemm_large_tiles_on_sampled_tokens(cuda, oracle, m, k, rows):
+    """The large block shapes are chosen only at big M: check every row of a sample of tokens bit for bit
+    (each output depends only on its own token row), and the whole output against the fp64 truth."""
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(m + k + rows)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=(m == 300))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    sample = np.unique(np.array([0, 1, 63, 64, 127, 128, 255, 256, m // 2, m - 1]) % m)
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    assert runtime.gemm_plan(m, rows, k) == 1
+    expected = oracle.gemm_seq(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                               np.zeros((len(sample), rows), np.float32), k, rows, len(sample))
+    assert_bits_equal(y[sample], expected, "sampled tokens")
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("m", [1, 3, 16, 32])
+@pytest.mark.parametrize("k,rows", [(8192, 512), (28672, 128), (4096, 1024), (1024, 4096)])
+def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
+    """Few tokens run the K-split MFMA kernel: bit-exact against the oracle's split order."""
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(m * 31 + k + rows)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    splits = runtime.gemm_plan(m, rows, k)
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, None,
+                                 np.zeros((m, rows), np.float32), k, rows, m, splits)
+    assert_bits_equal(y, expected, f"skinny gemm ({splits} splits)")
+    q, s = T.quantize_closed_form(x[0])
+    truth = T.truth_fp64(T.group_partials_int64(codes, q), T.half_bits_to_float(scale_bits), s)
+    assert_within(y[0], truth, what="skinny gemm vs fp64 truth")

@@ -64,6 +64,8 @@ def test_host_only_calls():
     assert lib.ivonar_define(b"TILE", 0) != 0
     assert lib.ivonar_define(b"TILE", 32) == 0
     assert lib.ivonar_error_string(1)
+    assert runtime.gemm_plan(2048, 4096, 1024) == 1
+    assert runtime.gemm_plan(1, 4096, 1024) >= 1
     for n, expected in [(8, 2), (64, 2), (100, 2), (1024, 16), (4096, 64), (8192, 64), (28672, 64)]:
         lanes, per_lane = runtime.gemv_plan(100, n)
         assert lanes == expected and per_lane == 2

@@ -223,3 +223,20 @@ def test_cpu_baseline_agrees_with_the_oracle():
     bias = GOLDEN[case + "bias"]
     out = cb.gemv(np.ascontiguousarray(x), planes, scales, bias, np.zeros(rows, np.float32))
     assert_within(out, GOLDEN[case + "y64"], rtol=1e-5, atol=1e-5, what="cpu baseline")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8])
+def test_split_order_agrees_with_fp64_truth(oracle, splits):
+    case = "plain6_"
+    codes, x = GOLDEN[case + "codes"], GOLDEN[case + "x"]
+    rows, k = codes.shape
+    packed = T.pad_rows16(GOLDEN[case + "packed"])
+    scales = GOLDEN[case + "scales"]
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    got = oracle.gemm_split(T.EPI_STORE, q8, xsum, sx, packed, scales, None, np.zeros((1, rows), np.float32), k, rows,
+                            1, splits)
+    assert_within(got[0], GOLDEN[case + "y64"] - 0.0, what=f"{splits} splits")
+    if splits == 1:
+        seq = oracle.gemm_seq(T.EPI_STORE, q8, xsum, sx, packed, scales, None, np.zeros((1, rows), np.float32), k,
+                              rows, 1)
+        assert_bits_equal(got, seq, "one split is the sequential chain")
