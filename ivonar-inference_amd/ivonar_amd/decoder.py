@@ -1,0 +1,296 @@
+"""Decode and prefill driver for a stack of ternary linear layers (mirrors the reference's kernel_decoder.py).
+
+The reference's ``KernelDecoder`` (``kernel_decoder.py:179-283``, ``:303-368``)
+builds one ``Launch`` per op and replays the list per token (decode) and per
+32-token tile (prefill).  ``StackDecoder`` builds the same launch pattern for
+the ternary linear path, with the same entry points and argument lists, through
+this package's ``runtime`` (the C ABI of the MI355X library):
+
+decode step (``kernel_decoder.py:233-269``)::
+
+    embed_token                                   token -> residual
+    per layer:
+      gemv_norm_store       entry (fused QKV)     residual -> mixer_in   (RMSNorm prologue)
+      gemv_plain_residual   out                   V third of mixer_in -> residual +=
+      gemv_norm_silu_pair   gate/up (interleaved) residual -> ffn_mid    (RMSNorm prologue)
+      gemv_plain_residual   down                  ffn_mid -> residual +=
+    quantize_norm + gemv_prequant_store           residual -> logits (tied token matrix)
+    ivonar_argmax                                 logits -> next token (greedy, top_k = 1)
+
+prefill tile (``kernel_decoder.py:303-368``): ``embed_tile``, per layer
+``quantize_tile_norm`` + ``gemm_tile_store``, ``quantize_tile_plain`` +
+``gemm_tile_residual``, ``quantize_tile_norm`` + ``gemm_tile_silu_pair``,
+``quantize_tile_plain`` + ``gemm_tile_residual``, then ``gather_token`` and
+the head.
+
+The mixers (recurrent scan, latent attention) are not part of this path: the
+output projection reads the V third of the entry projection's output instead
+of a mixer's output.  Greedy tokens are written on the device into a ring of
+``burst`` slots, so a burst of decode steps runs as one HIP graph replay with
+a single read-back, as the reference's burst graphs do (``kernel_decoder.py:694-735``).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import runtime
+from .matrix import Matrix, _lanes_for
+from .quantization import TernaryLinear
+from .runtime import KernelError, Launch, float32, int32, pointer
+from .synthetic import LinearStackWeights
+
+TILE = 32
+THREADS = 256
+HEAD_LANES = 4
+CHUNK = 64
+BURST = 16
+
+
+def _linear(layer) -> TernaryLinear:
+    return TernaryLinear(torch.from_numpy(np.ascontiguousarray(layer.packed)),
+                         torch.from_numpy(np.ascontiguousarray(layer.scales)), layer.in_features,
+                         None if layer.bias is None else torch.from_numpy(layer.bias))
+
+
+@dataclass
+class _LayerOps:
+    entry: Matrix
+    out: Matrix
+    gate_up: Matrix
+    down: Matrix
+    mixer_norm: torch.Tensor
+    ffn_norm: torch.Tensor
+
+
+class StackDecoder:
+    def __init__(self, weights: LinearStackWeights, device: str | torch.device = "cuda", burst: int = BURST) -> None:
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise KernelError("the ternary decoder needs a ROCm device")
+        config = weights.config
+        self.config = config
+        self.device = device
+        self.burst = int(burst)
+        hidden, dense, vocab = config.hidden, config.dense, config.vocab
+        max_chunks = (max(hidden, dense) + CHUNK - 1) // CHUNK
+        self.module = runtime.compile_module(None, {"HEAD_DIM": 64, "MAX_CHUNKS": max_chunks, "TILE": TILE}, device)
+        self.token_matrix = Matrix([_linear(weights.token)], device, lanes=HEAD_LANES)
+        self.layers: list[_LayerOps] = []
+        for layer in weights.layers:
+            self.layers.append(_LayerOps(
+                entry=Matrix([_linear(layer.qkv)], device),
+                out=Matrix([_linear(layer.out)], device),
+                gate_up=Matrix([_linear(layer.gate), _linear(layer.up)], device, interleave=True, max_lanes=16),
+                down=Matrix([_linear(layer.down)], device),
+                mixer_norm=torch.from_numpy(layer.mixer_norm).to(device),
+                ffn_norm=torch.from_numpy(layer.ffn_norm).to(device),
+            ))
+        self.final_norm = torch.from_numpy(weights.final_norm).to(device)
+        f32 = dict(dtype=torch.float32, device=device)
+        self.residual = torch.zeros(hidden, **f32)
+        self.mixer_in = torch.zeros(config.qkv, **f32)
+        self.ffn_mid = torch.zeros(dense, **f32)
+        self.logits = torch.zeros(vocab, **f32)
+        self.q8 = torch.zeros(max_chunks * CHUNK, dtype=torch.int8, device=device)
+        self.q8sum = torch.zeros(max_chunks, dtype=torch.int32, device=device)
+        self.q8scale = torch.zeros(1, **f32)
+        self.history = torch.zeros(self.burst, dtype=torch.int64, device=device)
+        # prefill tile buffers (kernel_decoder.py:308-319)
+        self.tile_tokens = torch.zeros(TILE, dtype=torch.int64, device=device)
+        self.tile_valid = torch.zeros(1, dtype=torch.int64, device=device)
+        self.residual_tile = torch.zeros(TILE, hidden, **f32)
+        self.mixer_in_tile = torch.zeros(TILE, config.qkv, **f32)
+        self.ffn_tile = torch.zeros(TILE, dense, **f32)
+        self.q8_tile = torch.zeros(TILE, max_chunks * CHUNK, dtype=torch.int8, device=device)
+        self.xsum_tile = torch.zeros(TILE, max_chunks, dtype=torch.int32, device=device)
+        self.scale_tile = torch.zeros(TILE, **f32)
+        self._head = [
+            self._quantize("quantize_norm", self.residual, self.final_norm, hidden, eps=config.eps),
+            self._gemv("gemv_prequant_store", self.token_matrix, None, None, self.logits, prequant=True),
+        ]
+        self._steps = [self._build_step(slot) for slot in range(self.burst)]
+        self._tile = self._build_tile()
+        self._graph: torch.cuda.CUDAGraph | None = None
+        self.position = 0
+
+    # ------------------------------------------------------------------ launch builders
+
+    def _gemv(self, name: str, matrix: Matrix, source, aux, output, eps: float = 1e-6, splits: int = 1,
+              prequant: bool = False) -> Launch:
+        """kernel_decoder.py:562-584 (the prefetch slots are passed empty)."""
+        args = [
+            pointer(source), pointer(aux),
+            pointer(self.q8 if prequant else None), pointer(self.q8sum if prequant else None),
+            pointer(self.q8scale if prequant else None),
+            pointer(matrix.packed), pointer(matrix.scales), pointer(matrix.bias), pointer(output),
+            int32(matrix.rows), int32(matrix.in_features), int32(matrix.row_bytes), int32(matrix.groups),
+            int32(matrix.lanes), int32(splits), float32(eps), pointer(None), int32(0),
+        ]
+        if matrix.wide and not prequant:
+            name += "_wide"
+        return Launch(self.module.kernel(name), (matrix.grid, 1, 1), (THREADS, 1, 1), args)
+
+    def _quantize(self, name: str, source, aux, width: int, eps: float = 1e-6) -> Launch:
+        """kernel_decoder.py:611-618."""
+        args = [pointer(source), pointer(aux), int32(width), float32(eps), int32(1),
+                pointer(self.q8), pointer(self.q8sum), pointer(self.q8scale)]
+        if width > 4 * THREADS:
+            name += "_wide"
+        return Launch(self.module.kernel(name), (1, 1, 1), (THREADS, 1, 1), args)
+
+    def _quantize_tile(self, name: str, source, width: int, in_stride: int, aux=None, eps: float = 1e-6) -> Launch:
+        """kernel_decoder.py:370-386."""
+        args = [pointer(source), int32(in_stride), pointer(aux), int32(width), float32(eps), int32(1),
+                pointer(self.q8_tile), pointer(self.xsum_tile), pointer(self.scale_tile)]
+        if width > 4 * THREADS:
+            name += "_wide"
+        return Launch(self.module.kernel(name), (TILE, 1, 1), (THREADS, 1, 1), args)
+
+    def _gemm_tile(self, name: str, matrix: Matrix, output, out_stride: int) -> Launch:
+        """kernel_decoder.py:388-397."""
+        args = [pointer(self.q8_tile), pointer(self.xsum_tile), pointer(self.scale_tile),
+                pointer(matrix.packed), pointer(matrix.scales), pointer(matrix.bias), pointer(output),
+                int32(matrix.rows), int32(matrix.in_features), int32(matrix.row_bytes), int32(matrix.groups),
+                int32(matrix.lanes), int32(out_stride), int32(TILE)]
+        if matrix.wide:
+            name += "_wide"
+        return Launch(self.module.kernel(name), (matrix.grid, 1, 1), (THREADS, 1, 1), args)
+
+    def _argmax(self, slot: int) -> Launch:
+        args = [pointer(self.logits), int32(self.config.vocab), pointer(self.history[slot:slot + 1])]
+        return Launch(self.module.kernel("ivonar_argmax"), (1, 1, 1), (1024, 1, 1), args)
+
+    def _build_step(self, slot: int) -> list[Launch]:
+        """One greedy decode step reading the token in slot-1 of the ring and writing slot."""
+        config = self.config
+        hidden = config.hidden
+        previous = self.history[(slot - 1) % self.burst:(slot - 1) % self.burst + 1]
+        token = self.token_matrix
+        launches = [Launch(self.module.kernel("embed_token"), ((hidden + THREADS - 1) // THREADS, 1, 1), (THREADS, 1, 1),
+                           [pointer(previous), pointer(token.packed), pointer(token.scales), pointer(self.residual),
+                            int32(hidden), int32(token.row_bytes), int32(token.groups)])]
+        values = self.mixer_in.narrow(0, 2 * hidden, hidden)
+        for ops in self.layers:
+            launches.append(self._gemv("gemv_norm_store", ops.entry, self.residual, ops.mixer_norm, self.mixer_in,
+                                       eps=config.eps))
+            launches.append(self._gemv("gemv_plain_residual", ops.out, values, None, self.residual))
+            launches.append(self._gemv("gemv_norm_silu_pair", ops.gate_up, self.residual, ops.ffn_norm,
+                                       self.ffn_mid, eps=config.eps))
+            launches.append(self._gemv("gemv_plain_residual", ops.down, self.ffn_mid, None, self.residual))
+        launches.extend(self._head)
+        launches.append(self._argmax(slot))
+        return launches
+
+    def _build_tile(self) -> list[Launch]:
+        """One 32-token prefill tile ending in the head and the first greedy token (slot burst-1)."""
+        config = self.config
+        hidden, dense, qkv = config.hidden, config.dense, config.qkv
+        token = self.token_matrix
+        launches = [Launch(self.module.kernel("embed_tile"), ((hidden + THREADS - 1) // THREADS, TILE, 1),
+                           (THREADS, 1, 1),
+                           [pointer(self.tile_tokens), pointer(token.packed), pointer(token.scales),
+                            pointer(self.residual_tile), int32(hidden), int32(token.row_bytes), int32(token.groups),
+                            int32(TILE)])]
+        values = self.mixer_in_tile.narrow(1, 2 * hidden, hidden)
+        for ops in self.layers:
+            launches.append(self._quantize_tile("quantize_tile_norm", self.residual_tile, hidden, hidden,
+                                                ops.mixer_norm, eps=config.eps))
+            launches.append(self._gemm_tile("gemm_tile_store", ops.entry, self.mixer_in_tile, qkv))
+            launches.append(self._quantize_tile("quantize_tile_plain", values, hidden, qkv))
+            launches.append(self._gemm_tile("gemm_tile_residual", ops.out, self.residual_tile, hidden))
+            launches.append(self._quantize_tile("quantize_tile_norm", self.residual_tile, hidden, hidden,
+                                                ops.ffn_norm, eps=config.eps))
+            launches.append(self._gemm_tile("gemm_tile_silu_pair", ops.gate_up, self.ffn_tile, dense))
+            launches.append(self._quantize_tile("quantize_tile_plain", self.ffn_tile, dense, dense))
+            launches.append(self._gemm_tile("gemm_tile_residual", ops.down, self.residual_tile, hidden))
+        launches.append(Launch(self.module.kernel("gather_token"), ((hidden + THREADS - 1) // THREADS, 1, 1),
+                               (THREADS, 1, 1),
+                               [pointer(self.residual_tile), pointer(self.residual), int32(hidden),
+                                pointer(self.tile_valid)]))
+        launches.extend(self._head)
+        launches.append(self._argmax(self.burst - 1))
+        return launches
+
+    # ------------------------------------------------------------------ running
+
+    def _run(self, launches: list[Launch]) -> None:
+        stream = runtime.current_stream(self.device)
+        for launch in launches:
+            launch(stream)
+
+    @torch.no_grad()
+    def prefill(self, input_ids) -> torch.Tensor:
+        """Runs the prompt in 32-token tiles (kernel_decoder.py:456-479); the first greedy token is left in
+        the ring's last slot and the logits of the prompt's last token in ``self.logits``."""
+        ids = torch.as_tensor(input_ids, dtype=torch.int64).reshape(-1)
+        length = int(ids.numel())
+        if length == 0:
+            raise ValueError("the prompt must not be empty")
+        if int(ids.min()) < 0 or int(ids.max()) >= self.config.vocab:
+            raise IndexError(f"token id is out of range for vocab_size={self.config.vocab}")
+        ids = ids.to(self.device)
+        for start in range(0, length, TILE):
+            chunk = ids[start:start + TILE]
+            count = int(chunk.numel())
+            self.tile_tokens.zero_()
+            self.tile_tokens[:count].copy_(chunk)
+            self.tile_valid.fill_(count)
+            self._run(self._tile)
+        self.position = 0
+        return self.logits
+
+    @torch.no_grad()
+    def step(self) -> None:
+        """One eager greedy step: consumes the last token, appends the next one to the ring."""
+        self._run(self._steps[self.position % self.burst])
+        self.position += 1
+
+    @torch.no_grad()
+    def capture(self) -> bool:
+        """Records one burst of decode steps into a HIP graph (kernel_decoder.py:694-719)."""
+        if self.position % self.burst != 0:
+            raise KernelError("capture at a burst boundary")
+        saved = self.history.clone()
+        stream = torch.cuda.Stream(device=self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            for slot in range(self.burst):
+                self._run(self._steps[slot])
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        torch.cuda.synchronize(self.device)
+        self.history.copy_(saved)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for slot in range(self.burst):
+                self._run(self._steps[slot])
+        torch.cuda.synchronize(self.device)
+        self.history.copy_(saved)
+        self._graph = graph
+        return True
+
+    @torch.no_grad()
+    def advance_many(self, count: int) -> list[int]:
+        """``count`` greedy tokens after the last one produced: whole bursts replay the graph with one
+        read-back each (kernel_decoder.py:722-735); the rest run eagerly."""
+        tokens: list[int] = []
+        while count - len(tokens) >= self.burst and self._graph is not None and self.position % self.burst == 0:
+            self._graph.replay()
+            self.position += self.burst
+            tokens.extend(self.history.tolist())
+        while len(tokens) < count:
+            slot = self.position % self.burst
+            self.step()
+            tokens.append(int(self.history[slot]))
+        return tokens
+
+    @torch.no_grad()
+    def generate(self, prompt_ids, count: int) -> list[int]:
+        """Greedy decoding: the first token from the prompt's last position, then count-1 steps."""
+        self.prefill(prompt_ids)
+        first = int(self.history[self.burst - 1])
+        return [first] + self.advance_many(count - 1)

@@ -131,3 +131,85 @@ def sweep_layer(seed: int = 4):
 
 def student_t(rng: np.random.Generator, shape, dof: float = 3.0) -> np.ndarray:
     return rng.standard_t(dof, size=shape).astype(np.float32)
+
+
+# Decoder-shaped stack -------------------------------------------------------
+
+
+@dataclass
+class StackConfig:
+    """A decoder's ternary linear path: per layer a fused QKV entry (norm prologue), an output
+    projection fed by the V third of the entry's output (the mixer is not part of this path), a
+    gated MLP (gate and up interleaved, silu pair) and a down projection; a tied ternary
+    embedding / LM head over the vocabulary."""
+
+    vocab: int = 32000
+    hidden: int = 1024
+    layers: int = 24
+    dense: int = 4096
+    eps: float = 1e-6
+
+    @property
+    def qkv(self) -> int:
+        return 3 * self.hidden
+
+
+@dataclass
+class StackLayer:
+    qkv: Layer
+    out: Layer
+    gate: Layer
+    up: Layer
+    down: Layer
+    mixer_norm: np.ndarray
+    ffn_norm: np.ndarray
+
+
+@dataclass
+class LinearStackWeights:
+    config: StackConfig
+    token: Layer
+    layers: list
+    final_norm: np.ndarray
+    codes: dict | None = None  # name -> uint8 codes [rows, K] when kept
+
+    def named_layers(self):
+        yield "token", self.token
+        for index, layer in enumerate(self.layers):
+            for name in ("qkv", "out", "gate", "up", "down"):
+                yield f"{index}.{name}", getattr(layer, name)
+
+
+def decoder_stack(config: StackConfig | None = None, seed: int = 1, keep_codes: bool = False) -> LinearStackWeights:
+    """Random-init weights: codes p=(0.3,0.4,0.3), scales |N(0,0.02)|+1e-4, norm weights 1+0.1*N(0,1)."""
+    config = config or StackConfig()
+    rng = np.random.default_rng(seed)
+    codes: dict | None = {} if keep_codes else None
+
+    def make(name: str, rows: int, k: int) -> Layer:
+        layer, c = ternary_layer(rng, rows, k, sigma=0.02, offset=1e-4, with_codes=True)
+        if codes is not None:
+            codes[name] = c
+        return layer
+
+    def norm() -> np.ndarray:
+        return (1.0 + 0.1 * rng.standard_normal(config.hidden)).astype(np.float32)
+
+    token = make("token", config.vocab, config.hidden)
+    layers = []
+    for index in range(config.layers):
+        layers.append(StackLayer(
+            qkv=make(f"{index}.qkv", config.qkv, config.hidden),
+            out=make(f"{index}.out", config.hidden, config.hidden),
+            gate=make(f"{index}.gate", config.dense, config.hidden),
+            up=make(f"{index}.up", config.dense, config.hidden),
+            down=make(f"{index}.down", config.hidden, config.dense),
+            mixer_norm=norm(),
+            ffn_norm=norm(),
+        ))
+    return LinearStackWeights(config, token, layers, norm(), codes)
+
+
+def prompt_ids(vocab: int, length: int = 36, seed: int = 1) -> list[int]:
+    """Random prompt ids in [2, vocab)."""
+    return [int(v) for v in np.random.default_rng(10_000 + seed).integers(2, vocab, size=length)]

@@ -371,6 +371,80 @@ void orc_embed(const int64_t* tokens, int m, const uint8_t* packed, const uint16
   }
 }
 
+/* ---------------------------------------------------------------------------
+ * Fast paths for whole decoder stacks.  The per-group partials are integers,
+ * so they are the same whatever order they are summed in; only the fp32
+ * finishing step below follows a kernel's order.  Rows run in parallel
+ * (OpenMP), which changes nothing inside a row.
+ * ------------------------------------------------------------------------- */
+
+/* w: int8 ternary values [rows, K] (-1, 0, +1); q: int8 activations in input
+ * order [K]; out: int32 partials [rows, ceil(K/128)]. */
+void orc_partials_i8(const int8_t* w, int rows, int k, const int8_t* q, int32_t* out) {
+  const int groups = (k + 127) / 128;
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) {
+    const int8_t* wr = w + (size_t)r * k;
+    for (int g = 0; g < groups; ++g) {
+      const int begin = g * 128, end = begin + 128 < k ? begin + 128 : k;
+      int total = 0;
+      for (int i = begin; i < end; ++i) total += (int)wr[i] * (int)q[i];
+      out[(size_t)r * groups + g] = total;
+    }
+  }
+}
+
+/* fp32 outputs of m x rows from int32 partials [m][rows][G], in one of the
+ * kernels' orders: order 0 = GEMV lane pairs (param = lanes), order 1 = GEMM
+ * K-split (param = splits).  scale_in: per-token scale; epilogue as above. */
+void orc_finish(int order, int param, int epi, const int32_t* partials, const uint16_t* scales, int groups_stride,
+                const float* scale_in, const float* bias, float* out, int rows, int k, int out_stride, int m) {
+  const int groups = (k + 127) / 128;
+  float* y = (float*)malloc(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
+  float* acc = (float*)malloc(sizeof(float) * (size_t)(param > 0 ? param : 1));
+  float* next = (float*)malloc(sizeof(float) * (size_t)(param > 0 ? param : 1));
+  for (int t = 0; t < m; ++t) {
+    for (int r = 0; r < rows; ++r) {
+      const int32_t* p = partials + ((size_t)t * rows + r) * groups;
+      const uint16_t* s = scales + (size_t)r * groups_stride;
+      float total = 0.0f;
+      if (order == 0) {
+        const int pairs = param / 2;
+        for (int i = 0; i < pairs; ++i) acc[i] = 0.0f;
+        for (int g = 0; g < groups; ++g) acc[g % pairs] = fmaf((float)p[g], orc_h2f(s[g]), acc[g % pairs]);
+        for (int offset = 1; offset < pairs; offset <<= 1) {
+          for (int i = 0; i < pairs; ++i) next[i] = acc[i] + acc[i ^ offset];
+          memcpy(acc, next, sizeof(float) * (size_t)pairs);
+        }
+        total = acc[0];
+      } else {
+        const int per = (groups + param - 1) / param;
+        for (int sp = 0; sp < param; ++sp) {
+          const int begin = sp * per < groups ? sp * per : groups;
+          const int end = begin + per < groups ? begin + per : groups;
+          float a = 0.0f;
+          for (int g = begin; g < end; ++g) a = fmaf((float)p[g], orc_h2f(s[g]), a);
+          total = sp == 0 ? a : total + a;
+        }
+      }
+      float v = total * scale_in[t];
+      if (bias) v = v + bias[r];
+      y[r] = v;
+    }
+    float* orow = out + (size_t)t * out_stride;
+    for (int r = 0; r < rows; ++r) {
+      if (epi == EPI_SILU_PAIR) {
+        if ((r & 1) == 0 && r + 1 < rows) epilogue(epi, orow, r >> 1, r, y[r], y[r + 1]);
+      } else {
+        epilogue(epi, orow, r, r, y[r], 0.0f);
+      }
+    }
+  }
+  free(next);
+  free(acc);
+  free(y);
+}
+
 /* First index of the maximum (greedy decoding). */
 int64_t orc_argmax(const float* x, int n) {
   int64_t best = 0;

@@ -82,6 +82,11 @@ def q8_index(n: int) -> np.ndarray:
     return (i >> 6) * 64 + ((i >> 4) & 3) * 16 + (i & 3) * 4 + ((i >> 2) & 3)
 
 
+def q8_linear(q8: np.ndarray, n: int) -> np.ndarray:
+    """Inverse of the q8 layout: int8 activations in input order [..., n]."""
+    return np.ascontiguousarray(np.asarray(q8)[..., q8_index(n)])
+
+
 def q8_layout(q: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Linear-order int q [K] -> (q8 int8 [C*64] in the q8 layout, xsum int32 [C])."""
     n = q.shape[-1]
@@ -171,6 +176,9 @@ class Oracle:
         lib.orc_reforder.argtypes = [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int]
         lib.orc_embed.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int]
+        lib.orc_partials_i8.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p]
+        lib.orc_finish.argtypes = [c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                   c_int, c_int, c_int, c_int]
         lib.orc_argmax.argtypes = [c_void_p, c_int]
         lib.orc_argmax.restype = c_int64
         self.lib = lib
@@ -253,6 +261,28 @@ class Oracle:
                               _ptr(np.ascontiguousarray(scale_in, dtype=np.float32)), _ptr(packed), _ptr(scales_bits),
                               _ptr(bias), _ptr(out), packed.shape[0], n, packed.shape[1], scales_bits.shape[1],
                               lanes, out_stride, m)
+        return out
+
+    def partials_i8(self, w: np.ndarray, q_lin: np.ndarray) -> np.ndarray:
+        """Exact int32 partials [rows, G] of int8 ternary values w [rows, K] against q [K] (input order)."""
+        w = np.ascontiguousarray(w, dtype=np.int8)
+        q_lin = np.ascontiguousarray(q_lin, dtype=np.int8)
+        rows, k = w.shape
+        out = np.zeros((rows, (k + 127) // 128), dtype=np.int32)
+        self.lib.orc_partials_i8(_ptr(w), rows, k, _ptr(q_lin), _ptr(out))
+        return out
+
+    def finish(self, order: int, param: int, epi: int, partials: np.ndarray, scales_bits: np.ndarray, scale_in,
+               bias, out: np.ndarray, k: int, out_stride: int) -> np.ndarray:
+        """fp32 outputs from partials [m, rows, G]: order 0 = GEMV pairs (param = lanes), 1 = GEMM split."""
+        partials = np.ascontiguousarray(partials, dtype=np.int32)
+        if partials.ndim == 2:
+            partials = partials[None]
+        m, rows, _ = partials.shape
+        scales_bits = np.ascontiguousarray(scales_bits, dtype=np.uint16)
+        self.lib.orc_finish(order, param, epi, _ptr(partials), _ptr(scales_bits), scales_bits.shape[1],
+                            _ptr(np.ascontiguousarray(scale_in, dtype=np.float32)), _ptr(bias), _ptr(out), rows, k,
+                            out_stride, m)
         return out
 
     def embed(self, tokens: np.ndarray, packed, scales_bits, n: int) -> np.ndarray:

@@ -150,3 +150,13 @@ def test_synthetic_layers_follow_the_stated_statistics():
     assert np.allclose(freq, (0.3, 0.4, 0.3), atol=0.01)
     assert (layer.scales > 0).all() and not (codes == 3).any()
     assert layer.packed.shape == (512, 256) and layer.scales.shape == (512, 8)
+
+
+def test_decoder_refuses_a_cpu_device():
+    from ivonar_amd.decoder import StackDecoder
+    from ivonar_amd.runtime import KernelError
+    from ivonar_amd.synthetic import StackConfig, decoder_stack
+
+    weights = decoder_stack(StackConfig(vocab=64, hidden=128, layers=1, dense=256), seed=0)
+    with pytest.raises(KernelError):
+        StackDecoder(weights, "cpu")

@@ -240,3 +240,46 @@ def test_split_order_agrees_with_fp64_truth(oracle, splits):
         seq = oracle.gemm_seq(T.EPI_STORE, q8, xsum, sx, packed, scales, None, np.zeros((1, rows), np.float32), k,
                               rows, 1)
         assert_bits_equal(got, seq, "one split is the sequential chain")
+
+
+# ------------------------------------------------------- stack fast paths
+
+
+def test_q8_linear_inverts_the_layout(rng):
+    q = rng.integers(-127, 128, size=200)
+    q8, _ = T.q8_layout(q)
+    np.testing.assert_array_equal(T.q8_linear(q8, 200), q.astype(np.int8))
+
+
+@pytest.mark.parametrize("case", ["plain3_", "plain6_", "plain7_"])
+def test_int8_partials_match_the_packed_core(oracle, case):
+    codes, x = GOLDEN[case + "codes"], GOLDEN[case + "x"]
+    rows, k = codes.shape
+    q8, xsum, _ = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    got = oracle.partials_i8(codes.astype(np.int8) - 1, T.q8_linear(q8[0], k))
+    packed = oracle.group_partials(q8[0], xsum[0], T.pad_rows16(GOLDEN[case + "packed"]), rows, k)
+    np.testing.assert_array_equal(got, packed)
+    q, _ = T.quantize_closed_form(x)
+    np.testing.assert_array_equal(got, T.group_partials_int64(codes, q))
+
+
+@pytest.mark.parametrize("epi", [T.EPI_STORE, T.EPI_RESIDUAL, T.EPI_SILU_PAIR])
+def test_finish_restates_the_kernel_orders(oracle, epi, rng):
+    """orc_finish (partials -> fp32) gives the bits of orc_gemv_pairs and orc_gemm_split."""
+    rows, k, m = 48, 1000, 3
+    codes = rng.integers(0, 3, size=(rows, k)).astype(np.uint8)
+    packed = T.pad_rows16(T.pack_codes(codes))
+    scales = (np.abs(rng.normal(0, 0.02, (rows, 8))) + 1e-4).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    partials = np.stack([oracle.partials_i8(codes.astype(np.int8) - 1, T.q8_linear(q8[t], k)) for t in range(m)])
+    width = rows // 2 if epi == T.EPI_SILU_PAIR else rows
+    base = np.linspace(-1, 1, m * width).astype(np.float32).reshape(m, width)
+    for lanes in (2, 4, 16, 64):
+        expected = oracle.gemv_pairs(epi, q8[1], xsum[1], sx[1], packed, scales, None, base[1].copy(), k, lanes)
+        got = oracle.finish(0, lanes, epi, partials[1], scales, sx[1:2], None, base[1].copy(), k, width)
+        assert_bits_equal(got, expected, f"lanes {lanes}")
+    for splits in (1, 2, 3, 8):
+        expected = oracle.gemm_split(epi, q8, xsum, sx, packed, scales, None, base.copy(), k, width, m, splits)
+        got = oracle.finish(1, splits, epi, partials, scales, sx, None, base.copy(), k, width)
+        assert_bits_equal(got, expected, f"{splits} splits")
