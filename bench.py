@@ -49,6 +49,7 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--probe", choices=["gemv-stress", "gemm-prefill"], default=None,
                         help="profiling mode: only the named kernel workload, no JSON line")
     parser.add_argument("--probe-calls", type=int, default=16)
+    parser.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     return parser.parse_args()
 
 
@@ -151,6 +152,93 @@ def device_copies(layer, device, copies: int):
     return mats
 
 
+def measure_traffic(calls: int = 8) -> dict:
+    """HBM bytes per GEMV dispatch from two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over
+    the GEMV probe, each scaled by what the counter reads for the probe's 512 MiB device copy.
+    Runs as child processes before this process touches the GPU."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    tool = shutil.which("rocprofv3")
+    if tool is None:
+        return {"error": "rocprofv3 not found"}
+    readings: dict[str, dict] = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="ivonar_pmc_", dir="/tmp")
+        command = [tool, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "pmc", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--probe", "gemv-stress", "--probe-calls", str(calls)]
+        print(f"bench: counter pass {counter}", file=sys.stderr, flush=True)
+        try:
+            done = subprocess.run(command, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, timeout=240,
+                                  stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        except subprocess.TimeoutExpired:
+            return {"error": f"{counter} pass timed out"}
+        files = sorted(Path(out).rglob("*counter_collection.csv"))
+        if done.returncode != 0 and not files:
+            return {"error": f"{counter} pass exited {done.returncode}: {done.stdout[-300:]}"}
+        if not files:
+            return {"error": f"{counter} pass wrote no counter file"}
+        gemv, other = {}, []
+        with open(files[0]) as handle:
+            for row in csv.DictReader(handle):
+                if row["Counter_Name"] != counter:
+                    continue
+                value = float(row["Counter_Value"])
+                if "gemv_kernel" in row["Kernel_Name"]:
+                    gemv.setdefault(int(row["Grid_Size"]), []).append(value)
+                else:
+                    other.append(value)
+        shutil.rmtree(out, ignore_errors=True)
+        if not gemv or not other:
+            return {"error": f"{counter} pass found no GEMV or copy dispatch"}
+        copy_kib = max(other)
+        readings[counter] = {"factor": (512 * 1024) / copy_kib,
+                             "per_grid": {grid: sum(v) / len(v) for grid, v in gemv.items()}}
+    fetch, write = readings["FETCH_SIZE"], readings["WRITE_SIZE"]
+    per_launch = [fetch["per_grid"][grid] * fetch["factor"] * 1024 + write["per_grid"].get(grid, 0.0) * write["factor"] * 1024
+                  for grid in fetch["per_grid"]]
+    return {"bytes_per_launch": sum(per_launch) / len(per_launch),
+            "fetch_factor": round(fetch["factor"], 4), "write_factor": round(write["factor"], 4),
+            "per_launch": [round(v) for v in per_launch]}
+
+
+def m_sweep(device, stream) -> dict:
+    """K=4096 -> N=14336 with p(0)=0.6, lognormal(-4, 0.5) scales and Student-t(3) activations: the GEMV
+    (one launch per token) against the token GEMM for M in 1..2048, weights warm in the caches."""
+    import torch
+
+    from ivonar_amd import ops, synthetic
+
+    layer, rng = synthetic.sweep_layer(seed=4)
+    mat = device_copies(layer, device, 1)[0]
+    k, n = layer.in_features, layer.rows
+    table = {}
+    crossover = None
+    for m in synthetic.SWEEP_M:
+        x = torch.from_numpy(synthetic.student_t(rng, (m, k))).to(device)
+        q8, xsum, sx = ops.quantize_rows(x)
+        out = torch.empty((m, n), dtype=torch.float32, device=device)
+        g = graph_of(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream)
+        t_gemm = time_graph(g, 20 if m >= 512 else 50, 3)
+        entry = {"gemm_us": round(t_gemm * 1e6, 3), "gemm_TOPS": round(2 * m * n * k / t_gemm / 1e12, 2)}
+        if m <= 16:
+            rows = [(q8[i], xsum[i], sx[i:i + 1], out[i]) for i in range(m)]
+
+            def per_token(rows=rows):
+                for q, xs, s, o in rows:
+                    ops.gemv_prequant(mat, q, xs, s, out=o)
+
+            g2 = graph_of(per_token, stream)
+            t_gemv = time_graph(g2, 50, 3)
+            entry["gemv_us"] = round(t_gemv * 1e6, 3)
+            if crossover is None and t_gemm < t_gemv:
+                crossover = m
+        table[str(m)] = entry
+    return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover}
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -168,6 +256,7 @@ def main() -> None:
 
     from ivonar_amd import ops, runtime, synthetic
 
+    traffic = None if args.no_traffic else measure_traffic()
     device = torch.device("cuda", 0)
     runtime.initialise(0)
     stream = torch.cuda.Stream()
@@ -255,6 +344,7 @@ def main() -> None:
 
     # ---- decoder-shaped stack: greedy decode tok/s -------------------------------------------
     results["decode_stack"] = decode_stack(device)
+    results["m_sweep"] = m_sweep(device, stream)
 
     # ---- CPU baseline on a bounded sample -------------------------------------------------------
     cpu = None
@@ -285,7 +375,9 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if not traffic or "error" in traffic else round(traffic["bytes_per_launch"]),
+            "traffic_detail": traffic,
+            "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
             "kernel": "gemv_kernel (pre-quantized activations)",
             "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)} for k, v in kernel.items()},
         },

@@ -71,55 +71,72 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
 
   // Staging: A in 64-byte pieces (two per token), B in 16-byte packed pieces
   // (two per weight row, each expanding to 64 bytes), one scale per row.
+  // Two register sets hold the next two groups while the MFMAs consume the
+  // third from LDS, so a group's loads have two group-steps to arrive.
   constexpr int kThreadsN = T::kThreadsPerBlock;
   constexpr int kPiecesA = (2 * T::kTokens + kThreadsN - 1) / kThreadsN;
   constexpr int kPiecesB = (2 * T::kRowsPerBlock + kThreadsN - 1) / kThreadsN;
-  uint4 ra[kPiecesA][4];
-  uint4 rb[kPiecesB];
-  uint16_t rs = 0;
+  struct Regs {
+    uint4 a[kPiecesA][4];
+    uint4 b[kPiecesB];
+    uint16_t s;
+    int g;
+  };
   const bool s_thread = tid < T::kRowsPerBlock;
   const uint16_t* s_src = scales + (size_t)min(row0 + tid % T::kRowsPerBlock, a.rows - 1) * a.groups;
 
-  auto fetch = [&](int g) {
-    const bool second_live = 2 * g + 1 < chunks;  // does chunk 2g+1 exist?
+  // Loads are unconditional, with the group clamped into the matrix (a
+  // predicated load would make the compiler wait for every outstanding load
+  // at its first use).  A missing second chunk reads the group's first chunk;
+  // its activations are replaced by zeros when staged, which also cancels
+  // whatever its weight bytes hold.
+  auto fetch = [&](Regs& r, int g_raw) {
+    const int g = min(g_raw, groups - 1);
+    r.g = g;
+    const bool second_live = 2 * g + 1 < chunks;
 #pragma unroll
     for (int k = 0; k < kPiecesA; ++k) {
       const int piece = tid + k * kThreadsN;
-      const int token = min(token0 + piece % T::kTokens, a.m - 1), half = piece / T::kTokens;
-      const bool live = piece < 2 * T::kTokens && (half == 0 || second_live);
-      const int8_t* src = q8 + (size_t)token * q8_stride + (size_t)g * kGroup + half * 64;
+      const int token = min(token0 + piece % T::kTokens, a.m - 1), half = (piece / T::kTokens) & 1;
+      const bool live = half == 0 || second_live;
+      const int8_t* src = q8 + (size_t)token * q8_stride + (size_t)g * kGroup + (live ? half * 64 : 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ra[k][i] = live ? *reinterpret_cast<const uint4*>(src + i * 16) : make_uint4(0u, 0u, 0u, 0u);
+      for (int i = 0; i < 4; ++i) r.a[k][i] = *reinterpret_cast<const uint4*>(src + i * 16);
     }
 #pragma unroll
     for (int k = 0; k < kPiecesB; ++k) {
       const int piece = tid + k * kThreadsN;
-      const int row = min(row0 + piece % T::kRowsPerBlock, a.rows - 1), half = piece / T::kRowsPerBlock;
-      const bool live = piece < 2 * T::kRowsPerBlock && (half == 0 || second_live);
-      rb[k] = live ? *reinterpret_cast<const uint4*>(packed + (size_t)row * a.row_bytes + (size_t)g * 32 + half * 16)
-                   : make_uint4(0u, 0u, 0u, 0u);
+      const int row = min(row0 + piece % T::kRowsPerBlock, a.rows - 1), half = (piece / T::kRowsPerBlock) & 1;
+      const bool live = half == 0 || second_live;
+      r.b[k] = *reinterpret_cast<const uint4*>(packed + (size_t)row * a.row_bytes + (size_t)g * 32 + (live ? half * 16 : 0));
     }
-    if (s_thread) rs = s_src[g];
+    r.s = s_src[g];  // clamped row: valid for every thread
   };
-  auto stage = [&](int g, int buffer) {
+  auto stage = [&](const Regs& r, int buffer) {
     unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
+    const bool second_live = 2 * r.g + 1 < chunks;  // wave-uniform
 #pragma unroll
     for (int k = 0; k < kPiecesA; ++k) {
       const int piece = tid + k * kThreadsN;
       if (piece < 2 * T::kTokens) {
-        unsigned char* dst = base + (piece % T::kTokens) * kRowPitch + (piece / T::kTokens) * 64;
+        const int half = piece / T::kTokens;
+        unsigned char* dst = base + (piece % T::kTokens) * kRowPitch + half * 64;
+        if (second_live) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(dst + i * 16) = ra[k][i];
+          for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(dst + i * 16) = r.a[k][i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(dst + i * 16) = half == 0 ? r.a[k][i] : make_uint4(0u, 0u, 0u, 0u);
+        }
       }
     }
 #pragma unroll
     for (int k = 0; k < kPiecesB; ++k) {
       const int piece = tid + k * kThreadsN;
       if (piece < 2 * T::kRowsPerBlock) {
-        // A dead second chunk stages zero activations, so its weight bytes need no masking.
         unsigned char* dst = base + (T::kTokens + piece % T::kRowsPerBlock) * kRowPitch + (piece / T::kRowsPerBlock) * 64;
-        const unsigned words[4] = {rb[k].x, rb[k].y, rb[k].z, rb[k].w};
+        const unsigned words[4] = {r.b[k].x, r.b[k].y, r.b[k].z, r.b[k].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           uint4 e;
@@ -131,7 +148,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
         }
       }
     }
-    if (s_thread) reinterpret_cast<float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch)[tid] = h2f(rs);
+    if (s_thread) reinterpret_cast<float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch)[tid] = h2f(r.s);
   };
 
   float acc[4][4][4];
@@ -142,44 +159,57 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
 
-  fetch(0);
-  stage(0, 0);
-  __syncthreads();
-  for (int g = 0; g < groups; ++g) {
-    const int buffer = g & 1;
-    if (g + 1 < groups) fetch(g + 1);
+  // One group from LDS.  The weight fragments of both MFMA halves stay in
+  // registers; per 16-token row of tiles the two halves accumulate the exact
+  // int32 partials, which are folded into fp32 with one fmaf per output and
+  // the row's group scale while the next row of tiles runs on the MFMA unit.
+  auto compute = [&](int buffer) {
     const unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
     const unsigned char* a_lds = base + (wm * 64 + col) * kRowPitch;
     const unsigned char* b_lds = base + (T::kTokens + wn * 64 + col) * kRowPitch;
-    v4i p[4][4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      v4i af[4], bf[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        af[mt] = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb + h) * 16);
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        bf[nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb + h) * 16);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const v4i zero = {0, 0, 0, 0};
-          p[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bf[nt], h == 0 ? zero : p[mt][nt], 0, 0, 0);
-        }
-    }
     const float* s_lds = reinterpret_cast<const float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch);
+    v4i bf[2][4];
+    float sc[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      const float s = s_lds[wn * 64 + nt * 16 + col];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][nt][i] = __builtin_fmaf((float)p[mt][nt][i], s, acc[mt][nt][i]);
+      bf[0][nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb) * 16);
+      bf[1][nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb + 1) * 16);
+      sc[nt] = s_lds[wn * 64 + nt * 16 + col];
     }
-    if (g + 1 < groups) stage(g + 1, buffer ^ 1);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const v4i a0 = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb) * 16);
+      const v4i a1 = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb + 1) * 16);
+      v4i p[4];
+      const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bf[0][nt], zero, 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bf[1][nt], p[nt], 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][nt][i] = __builtin_fmaf((float)p[nt][i], sc[nt], acc[mt][nt][i]);
+    }
+  };
+
+  // LDS buffer g & 1 holds group g; register sets r0 / r1 alternate.
+  Regs r0, r1;
+  fetch(r0, 0);
+  fetch(r1, 1);
+  stage(r0, 0);
+  __syncthreads();
+  fetch(r0, 2);
+  for (int g = 0; g < groups; g += 2) {
+    compute(0);
+    if (g + 1 < groups) stage(r1, 1);
     __syncthreads();
+    fetch(r1, g + 3);
+    if (g + 1 >= groups) break;
+    compute(1);
+    if (g + 2 < groups) stage(r0, 0);
+    __syncthreads();
+    fetch(r0, g + 4);
   }
 
   // Epilogue: lane holds rows row0 + wn*64 + nt*16 + col, tokens token0 + wm*64 + mt*16 + 4*kb + i.

@@ -22,13 +22,15 @@
 // per lane the next row step's weights are prefetched while the current one
 // is computed (double buffering), so each wave keeps 2-4 KB in flight.
 //
-// Activations.  The block holds the token's q8 row in LDS, quad-planar (quad
-// w of chunk u at int4 index w*C + u: the 16-byte reads of a slot's lanes are
-// contiguous).  With at most two steps per lane the lane's q8 words stay in
-// registers for the whole kernel.  For rows up to kFusedLimit inputs the
-// block quantizes the fp32 input itself (the fused prologue of gemv_plain_*,
-// gemv_norm_*, gemv_attn_*); longer rows are quantized once by the quantizer
-// into the device scratch and each block copies the result to LDS.
+// Activations.  For rows up to kFusedLimit inputs the block quantizes the
+// fp32 input itself into LDS (the fused prologue of gemv_plain_*,
+// gemv_norm_*, gemv_attn_*), quad-planar (quad w of chunk u at int4 index
+// w*C + u), and each lane then keeps its chunks' quads in registers.  Longer
+// rows are quantized once by the quantizer into the device scratch, and
+// pre-quantized activations are read by each lane straight from global
+// memory: once for the whole kernel when a row needs at most two steps per
+// lane, else with every step's weights.  That path has no LDS and no
+// barrier: the q8 row is small and stays in the caches for every block.
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -55,10 +57,12 @@ struct GemvPtrs {
   const float* scale_in;
 };
 
+// One pipeline item's loads: weights of NJ steps for kRows rows, and per
+// step the group scale of the lane's own row (row0 + (sub & 1)).
 template <int NJ>
 struct Step {
   uint4 w[NJ][kRows];
-  uint16_t s[NJ][kRows];
+  uint16_t s[NJ];
 };
 
 __device__ __forceinline__ uint4 load16(const uint8_t* __restrict__ p) {
@@ -70,6 +74,7 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
                                           const uint16_t* __restrict__ scales, const GemvShape& sh, int row0,
                                           int j0, int sub, int chunks) {
   const int lanes = LANES ? LANES : sh.lanes;
+  const int own_row = min(row0 + (sub & 1), sh.rows - 1);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int u = min((j0 + j) * lanes + sub, chunks - 1);
@@ -77,18 +82,25 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
     for (int r = 0; r < kRows; ++r) {
       const int row = min(row0 + r, sh.rows - 1);
       st.w[j][r] = load16(packed + (size_t)row * sh.row_bytes + (size_t)u * 16);
-      st.s[j][r] = SCALES ? scales[(size_t)row * sh.groups + (u >> 1)] : (uint16_t)0;
     }
+    st.s[j] = SCALES ? scales[(size_t)own_row * sh.groups + (u >> 1)] : (uint16_t)0;
   }
 }
 
+// Lane pair (sub, sub ^ 1) covers the two chunks of a group for rows row0 and
+// row0 + 1; each lane keeps the accumulator of its own row (sub & 1).  A lane
+// forms both rows' chunk sums, sends the partner's row across the pair (one
+// DPP swap) and adds the partner's sum for its own row: the exact group
+// partial P[own row, g].
 template <int EPI, int NJ, bool QREG, int LANES, bool EXACT>
 __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr)[QREG ? NJ : 1][4],
                                              const int (&xr)[QREG ? NJ : 1], const int4* __restrict__ lds_q,
-                                             const int* __restrict__ lds_x, float (&acc)[kRows],
+                                             const int* __restrict__ lds_x, float& acc,
                                              int32_t* __restrict__ partials, const GemvShape& sh, int row0, int j0,
                                              int sub, int chunks) {
+  static_assert(kRows == 2, "a lane pair holds two rows");
   const int lanes = LANES ? LANES : sh.lanes;
+  const bool odd = (sub & 1) != 0;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int u_raw = (j0 + j) * lanes + sub;
@@ -111,18 +123,19 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
       q3 = lds_q[3 * chunks + u];
       xs = lds_x[u];
     }
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      int d = chunk_code_dot(st.w[j][r], q0, q1, q2, q3, -xs);
-      if constexpr (!EXACT) d = live ? d : 0;
-      d += pair_swap(d);
-      const int row = row0 + r;
-      if constexpr (EPI == kPartials) {
-        if (group_live && (sub & 1) == 0 && row < sh.rows) partials[(size_t)row * sh.groups + g] = d;
-      } else {
-        const float contribution = EXACT || group_live ? (float)d : 0.0f;
-        acc[r] = __builtin_fmaf(contribution, h2f(st.s[j][r]), acc[r]);
-      }
+    int d0 = chunk_code_dot(st.w[j][0], q0, q1, q2, q3, -xs);
+    int d1 = chunk_code_dot(st.w[j][1], q0, q1, q2, q3, -xs);
+    if constexpr (!EXACT) {
+      d0 = live ? d0 : 0;
+      d1 = live ? d1 : 0;
+    }
+    const int d = (odd ? d1 : d0) + pair_swap(odd ? d0 : d1);
+    if constexpr (EPI == kPartials) {
+      const int row = row0 + (sub & 1);
+      if (group_live && row < sh.rows) partials[(size_t)row * sh.groups + g] = d;
+    } else {
+      const float contribution = EXACT || group_live ? (float)d : 0.0f;
+      acc = __builtin_fmaf(contribution, h2f(st.s[j]), acc);
     }
   }
 }
@@ -133,13 +146,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
                                                         const float* __restrict__ bias, float* __restrict__ output,
                                                         int32_t* __restrict__ partials, GemvShape sh) {
   // One block of steps per row (no rolling over steps) keeps the lane's q8
-  // words in registers; rows of several blocks read them from LDS.
+  // words in registers for the whole kernel; a rolling pipeline reads them
+  // from the block's LDS copy at every step.
   constexpr bool QREG = !ROLL;
+  static_assert(!(FUSED && ROLL), "the fused prologue keeps q8 in registers");
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ float slots[64];
   const int chunks = (sh.n + kChunk - 1) / kChunk;
-  int4* lds_q = reinterpret_cast<int4*>(lds_raw);
+  int4* lds_q = reinterpret_cast<int4*>(lds_raw);  // quad w of chunk u at w*C + u
   int* lds_x = reinterpret_cast<int*>(lds_raw + (size_t)chunks * kChunk);
+  const int4* gq = reinterpret_cast<const int4*>(in.q8_in);  // chunk u, quad w at u*4 + w
 
   const int lane = threadIdx.x & 63;
   const int lanes = LANES ? LANES : sh.lanes;
@@ -159,7 +175,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
   load_step<NJ, EPI != kPartials, LANES>(a, packed, scales, sh, it * rows_per_iter + slot * kRows, 0, sub, chunks);
 
   float sx;
+  int4 qr[QREG ? NJ : 1][4];
+  int xr[QREG ? NJ : 1];
   if constexpr (FUSED) {
+    // The block quantizes the token into LDS, then each lane takes its chunks' quads.
     const RowSource src{in.input, in.aux, sh.n, sh.eps, sh.splits, sh.head_dim};
     float inv_rms;
     sx = row_scale<MODE>(src, inv_rms, slots);
@@ -170,17 +189,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
       const int total = chunk_lane_sum(word_sum(value));
       if ((d & 15) == 0) lds_x[u] = total;
     }
-  } else {
-    const int4* gq = reinterpret_cast<const int4*>(in.q8_in);
-    for (int e = threadIdx.x; e < chunks * 4; e += kThreads) lds_q[(e & 3) * chunks + (e >> 2)] = gq[e];
-    for (int u = threadIdx.x; u < chunks; u += kThreads) lds_x[u] = in.xsum_in[u];
-    sx = *in.scale_in;
-  }
-  __syncthreads();
-
-  int4 qr[QREG ? NJ : 1][4];
-  int xr[QREG ? NJ : 1];
-  if constexpr (QREG) {
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int u = min(j * lanes + sub, chunks - 1);
@@ -188,33 +197,50 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
       for (int w = 0; w < 4; ++w) qr[j][w] = lds_q[w * chunks + u];
       xr[j] = lds_x[u];
     }
+  } else if constexpr (QREG) {
+    // Pre-quantized and at most two steps per lane: the lane's quads straight from global memory.
+    sx = *in.scale_in;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int u = min(j * lanes + sub, chunks - 1);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) qr[j][w] = gq[u * 4 + w];
+      xr[j] = in.xsum_in[u];
+    }
+  } else {
+    // Rolling over a long row: the block copies the q8 row to LDS.  All of a
+    // thread's loads go out before its LDS stores.
+    constexpr int kCopyBatch = 8;
+    const int words = chunks * 4;
+    for (int base = 0; base < words; base += kThreads * kCopyBatch) {
+      int4 v[kCopyBatch];
+#pragma unroll
+      for (int k = 0; k < kCopyBatch; ++k) v[k] = gq[min(base + k * kThreads + (int)threadIdx.x, words - 1)];
+#pragma unroll
+      for (int k = 0; k < kCopyBatch; ++k) {
+        const int e = base + k * kThreads + threadIdx.x;
+        if (e < words) lds_q[(e & 3) * chunks + (e >> 2)] = v[k];
+      }
+    }
+    for (int u = threadIdx.x; u < chunks; u += kThreads) lds_x[u] = in.xsum_in[u];
+    sx = *in.scale_in;
+    __syncthreads();
   }
 
-  auto finish = [&](float (&acc)[kRows], int row0) {
+  // Butterfly over the pairs (offsets 2 .. lanes/2 keep each lane's row),
+  // then lane sub = r finishes row row0 + r.
+  auto finish = [&](float acc, int row0) {
     if constexpr (EPI != kPartials) {
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) {
-        for (int offset = 2; offset < lanes; offset <<= 1) acc[r] = acc[r] + __shfl_xor(acc[r], offset);
-      }
-      if (sub == 0) {
-        float y[kRows];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-          const int row = row0 + r;
-          y[r] = acc[r] * sx;
-          if (bias != nullptr && row < sh.rows) y[r] = y[r] + bias[row];
-        }
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-          const int row = row0 + r;
-          if constexpr (EPI == kStore) {
-            if (row < sh.rows) output[row] = y[r];
-          } else if constexpr (EPI == kResidual) {
-            if (row < sh.rows) output[row] = output[row] + y[r];
-          } else if constexpr (EPI == kSiluPair) {
-            if ((r & 1) == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y[r]) * y[r + 1];
-          }
-        }
+      for (int offset = 2; offset < lanes; offset <<= 1) acc = acc + __shfl_xor(acc, offset);
+      const int row = row0 + (sub & 1);
+      float y = acc * sx;
+      if (bias != nullptr && row < sh.rows) y = y + bias[row];
+      if constexpr (EPI == kSiluPair) {
+        const float up = __int_as_float(pair_swap(__float_as_int(y)));
+        if (sub == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y) * up;
+      } else if (sub < 2 && row < sh.rows) {
+        if constexpr (EPI == kStore) output[row] = y;
+        else output[row] = output[row] + y;
       }
     }
   };
@@ -223,9 +249,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
   // item's weights are in flight while the current one is computed.
   const int blocks_per_row = (steps + NJ - 1) / NJ;
   int jb = 0;
-  float acc[kRows];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+  float acc = 0.0f;
   while (it < sh.iters) {
     {
       int it_next = it, jb_next = jb + 1;
@@ -240,8 +264,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
                                                 chunks);
       if (jb == blocks_per_row - 1) {
         finish(acc, row0);
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+        acc = 0.0f;
       }
       it = it_next;
       jb = jb_next;
@@ -260,8 +283,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
                                                 chunks);
       if (jb == blocks_per_row - 1) {
         finish(acc, row0);
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+        acc = 0.0f;
       }
       it = it_next;
       jb = jb_next;
@@ -355,7 +377,8 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   if (in.rows <= 0) return hipSuccess;
   GemvArgs a = in;
   const int chunks = ceil_div(a.n, kChunk);
-  const size_t lds = (size_t)chunks * (kChunk + 4);
+  const bool fused = a.q8_in == nullptr && a.n <= kFusedLimit;
+  const size_t lds = (size_t)chunks * (kChunk + 4);  // unused by the non-rolling pre-quantized layouts
   if (lds > (size_t)kMaxLdsBytes) return hipErrorInvalidValue;
   int lanes, rows_per_lane;
   gemv_plan(a.rows, a.n, &lanes, &rows_per_lane);
@@ -374,7 +397,6 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   // Dead lanes exist when the last step is partial (items never hold dead steps).
   sh.exact = chunks % lanes == 0;
   const int cus = device_cus();
-  const bool fused = a.q8_in == nullptr && a.n <= kFusedLimit;
   int blocks = ceil_div(sh.iters, kThreads / 64);
   const int cap = (fused ? 2 : kBlocksPerCu) * cus;
   if (blocks > cap) blocks = cap;

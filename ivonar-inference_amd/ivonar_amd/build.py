@@ -9,7 +9,10 @@ valid inside it and its launches can be recorded into torch's HIP graphs.
 Flags: ``-ffp-contract=off`` (every fused multiply-add in the kernels is an
 explicit ``fmaf``, which keeps the fp32 order reproducible on the CPU) and
 ``-Xclang -target-feature -Xclang -packed-fp32-ops`` (no packed fp32 VALU
-instructions).
+instructions) and ``-mllvm -amdgpu-mfma-vgpr-form`` (MFMA results in ordinary
+VGPRs: the kernels convert every int32 MFMA tile with VALU instructions, which
+would otherwise first copy it out of the accumulation registers, and the
+smaller register footprint keeps two waves per SIMD).
 """
 
 from __future__ import annotations
@@ -38,6 +41,8 @@ HIP_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
 )
