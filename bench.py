@@ -79,7 +79,8 @@ def probe_gemv_stress(calls: int) -> None:
 
 
 def probe_gemm_prefill(calls: int) -> None:
-    """Prefill GEMM alone at M=2048 and M=32 on both prefill shapes (pre-quantized activations)."""
+    """Token GEMM alone at M=2048 and M=32 on both prefill shapes and on K=4096 -> N=14336
+    (pre-quantized activations)."""
     import numpy as np
     import torch
 
@@ -91,7 +92,8 @@ def probe_gemm_prefill(calls: int) -> None:
     print(f"probe: {props.name} CUs={props.multi_processor_count} "
           f"lds_per_block={getattr(props, 'shared_memory_per_block', '?')}", flush=True)
     rng = np.random.default_rng(2)
-    for layer, k in synthetic.prefill_layers(seed=2):
+    sweep, _ = synthetic.sweep_layer(seed=4)
+    for layer, k in [*synthetic.prefill_layers(seed=2), (sweep, sweep.in_features)]:
         mat = device_copies(layer, device, 1)[0]
         for m in (2048, 32):
             xs = torch.from_numpy(synthetic.prefill_activations(rng, m, k)).to(device)
@@ -133,6 +135,13 @@ def time_graph(graph, replays: int, warmup: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3 / replays
+
+
+def time_calls(call, stream, calls_per_graph: int, replays: int, warmup: int = 2) -> float:
+    """Seconds per call: `calls_per_graph` back-to-back calls recorded in one HIP graph, so that the time of
+    a short kernel is not the host's graph-launch time."""
+    graph = graph_of(lambda: [call() for _ in range(calls_per_graph)], stream)
+    return time_graph(graph, replays, warmup) / calls_per_graph
 
 
 def device_copies(layer, device, copies: int):
@@ -220,8 +229,7 @@ def m_sweep(device, stream) -> dict:
         x = torch.from_numpy(synthetic.student_t(rng, (m, k))).to(device)
         q8, xsum, sx = ops.quantize_rows(x)
         out = torch.empty((m, n), dtype=torch.float32, device=device)
-        g = graph_of(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream)
-        t_gemm = time_graph(g, 20 if m >= 512 else 50, 3)
+        t_gemm = time_calls(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream, 20 if m <= 128 else 4, 10)
         entry = {"gemm_us": round(t_gemm * 1e6, 3), "gemm_TOPS": round(2 * m * n * k / t_gemm / 1e12, 2)}
         if m <= 16:
             rows = [(q8[i], xsum[i], sx[i:i + 1], out[i]) for i in range(m)]
@@ -230,13 +238,13 @@ def m_sweep(device, stream) -> dict:
                 for q, xs, s, o in rows:
                     ops.gemv_prequant(mat, q, xs, s, out=o)
 
-            g2 = graph_of(per_token, stream)
-            t_gemv = time_graph(g2, 50, 3)
+            t_gemv = time_calls(per_token, stream, 10, 10)
             entry["gemv_us"] = round(t_gemv * 1e6, 3)
             if crossover is None and t_gemm < t_gemv:
                 crossover = m
         table[str(m)] = entry
-    return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover}
+    return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover,
+            "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph"}
 
 
 def main() -> None:
@@ -328,18 +336,29 @@ def main() -> None:
     t0 = time_graph(g0, 20, 2) / 64
     results["single_linear_1024x4096_us"] = round(t0 * 1e6, 3)
 
-    # ---- prefill tile GEMM at M=32 -----------------------------------------------------------
+    # ---- prefill GEMM: prompts of L tokens as 32-token tiles and as one launch ----------------------
     rng = np.random.default_rng(2)
     prefill = {}
     for layer, k in synthetic.prefill_layers(seed=2):
         mat = device_copies(layer, device, 1)[0]
-        for m in (32, 2048):
-            xs = torch.from_numpy(synthetic.prefill_activations(rng, m, k)).to(device)
+        shape = {}
+        for length in (32, 128, 512, 2048):
+            xs = torch.from_numpy(synthetic.prefill_activations(rng, length, k)).to(device)
             q8, xsum, sx = ops.quantize_rows(xs)
-            out = torch.empty((m, layer.rows), dtype=torch.float32, device=device)
-            g = graph_of(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream)
-            t = time_graph(g, 50, 5)
-            prefill[f"{k}x{layer.rows}_m{m}"] = {"us": round(t * 1e6, 3), "TOPS": round(2 * m * layer.rows * k / t / 1e12, 3)}
+            out = torch.empty((length, layer.rows), dtype=torch.float32, device=device)
+            tiles = [(q8[t:t + 32], xsum[t:t + 32], sx[t:t + 32], out[t:t + 32]) for t in range(0, length, 32)]
+
+            def tiled(tiles=tiles):
+                for q, x, s_, o in tiles:
+                    ops.gemm(mat, q, x, s_, out=o)
+
+            t_tiles = time_calls(tiled, stream, max(1, 64 // len(tiles)), 10)
+            t_one = time_calls(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream, 20 if length <= 128 else 4, 10)
+            ops_count = 2 * length * layer.rows * k
+            shape[str(length)] = {"tiles_us": round(t_tiles * 1e6, 3), "tiles_TOPS": round(ops_count / t_tiles / 1e12, 2),
+                                  "one_launch_us": round(t_one * 1e6, 3),
+                                  "one_launch_TOPS": round(ops_count / t_one / 1e12, 2)}
+        prefill[f"{k}x{layer.rows}"] = shape
     results["prefill_gemm"] = prefill
 
     # ---- decoder-shaped stack: greedy decode tok/s -------------------------------------------

@@ -9,14 +9,16 @@
 // loop walks the 128-input groups.  For each group the block stages, double
 // buffered in LDS:
 //   * the q8 bytes of its tokens (128 per token, the q8 layout's two chunks);
-//   * its weight rows' 32 packed bytes, expanded once per block to signed
-//     int8 (code - 1) with one v_perm_b32 table lookup per 4 codes, so the
-//     MFMA produces P directly (no activation-sum correction);
+//   * its weight rows' 32 packed bytes, expanded once per block to the codes
+//     0, 1, 2 as int8 (two VALU operations per 4 codes);
+//   * minus each token's activation sum over the group, which seeds the
+//     MFMA accumulator, so sum (code * q) - sum q = P comes out exact with no
+//     per-output correction;
 //   * the fp16 group scales of its rows.
 // LDS rows are padded from 128 to 144 bytes, which spreads the 16 lanes of
-// each 16-byte operand read over distinct banks.  The global loads of group
-// g+1 are issued before the MFMAs of group g and written to the other buffer
-// after them, with one barrier per group.
+// each 16-byte operand read over distinct banks.  Each group's global loads
+// are issued two group-steps before they are staged, from two register sets,
+// and there is one barrier per group.
 //
 // Operand pairing: MFMA half h of a group takes, in lane (c = lane % 16,
 // kb = lane / 16), the 16 bytes of word 2*kb + h of the group (inputs
@@ -24,7 +26,8 @@
 // order the expansion (w >> 2k) & 0x03030303 produces, so both operands see
 // the same input in the same byte slot.  Each group's int32 tile is folded
 // into fp32 with one fmaf per output in ascending group order (the order the
-// CPU oracle restates as orc_gemm_seq).
+// CPU oracle restates as orc_gemm_seq); the fold of one 16-token row of tiles
+// is independent of the next row's MFMAs, so the two overlap.
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -33,20 +36,21 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kRowPitch = 144;        // bytes per staged LDS row (128 + 16 padding)
-constexpr unsigned kSignedLut = 0x000100FFu;  // v_perm table: code 0 -> -1, 1 -> 0, 2 -> +1
+constexpr int kRowPitch = 144;  // bytes per staged LDS row (128 + 16 padding)
 
-__device__ __forceinline__ unsigned signed_codes(unsigned w, int k) {
-  return __builtin_amdgcn_perm(0u, kSignedLut, (w >> (2 * k)) & kLow2);
-}
+// Codes of field k of four packed bytes, one per byte (0, 1, 2).
+__device__ __forceinline__ unsigned field_codes(unsigned w, int k) { return (w >> (2 * k)) & kLow2; }
 
+// LDS stage: A rows, B rows, then fp32 row scales and minus the token sums.
 template <int WM, int WN>
 struct Tile {
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreadsPerBlock = 64 * kWaves;
   static constexpr int kTokens = 64 * WM;
   static constexpr int kRowsPerBlock = 64 * WN;
-  static constexpr int kStageBytes = (kTokens + kRowsPerBlock) * kRowPitch + kRowsPerBlock * 4;
+  static constexpr int kScaleOffset = (kTokens + kRowsPerBlock) * kRowPitch;
+  static constexpr int kSumOffset = kScaleOffset + kRowsPerBlock * 4;
+  static constexpr int kStageBytes = kSumOffset + kTokens * 4;
 };
 
 template <int EPI, int WM, int WN>
@@ -69,86 +73,83 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
   const int token0 = blockIdx.y * T::kTokens;
   const int row0 = blockIdx.x * T::kRowsPerBlock;
 
-  // Staging: A in 64-byte pieces (two per token), B in 16-byte packed pieces
-  // (two per weight row, each expanding to 64 bytes), one scale per row.
-  // Two register sets hold the next two groups while the MFMAs consume the
-  // third from LDS, so a group's loads have two group-steps to arrive.
+  // Staging: A in 16-byte pieces, eight per token and group (consecutive
+  // threads read consecutive pieces of a token, so each load instruction
+  // covers whole 128-byte lines); B in 16-byte packed pieces, two per weight
+  // row (each expanding to 64 bytes); one scale per row and the two chunk
+  // sums per token.  Two register sets hold the next two groups while the
+  // MFMAs consume the third from LDS.
   constexpr int kThreadsN = T::kThreadsPerBlock;
-  constexpr int kPiecesA = (2 * T::kTokens + kThreadsN - 1) / kThreadsN;
-  constexpr int kPiecesB = (2 * T::kRowsPerBlock + kThreadsN - 1) / kThreadsN;
+  constexpr int kLoadsA = T::kTokens * 8 / kThreadsN;
+  constexpr int kLoadsB = T::kRowsPerBlock * 2 / kThreadsN;
+  static_assert(T::kTokens * 8 % kThreadsN == 0 && T::kRowsPerBlock * 2 % kThreadsN == 0, "whole pieces");
+  static_assert(T::kTokens <= kThreadsN && T::kRowsPerBlock <= kThreadsN, "one thread per token sum and scale");
   struct Regs {
-    uint4 a[kPiecesA][4];
-    uint4 b[kPiecesB];
+    uint4 a[kLoadsA];
+    uint4 b[kLoadsB];
     uint16_t s;
+    int x0, x1;
     int g;
   };
   const bool s_thread = tid < T::kRowsPerBlock;
+  const bool x_thread = tid < T::kTokens;
   const uint16_t* s_src = scales + (size_t)min(row0 + tid % T::kRowsPerBlock, a.rows - 1) * a.groups;
+  const int32_t* x_src = a.xsum_in + (size_t)min(token0 + tid % T::kTokens, a.m - 1) * chunks;
 
   // Loads are unconditional, with the group clamped into the matrix (a
   // predicated load would make the compiler wait for every outstanding load
   // at its first use).  A missing second chunk reads the group's first chunk;
-  // its activations are replaced by zeros when staged, which also cancels
-  // whatever its weight bytes hold.
+  // its activations and chunk sum are replaced by zeros when staged, which
+  // also cancels whatever its weight bytes hold.
   auto fetch = [&](Regs& r, int g_raw) {
     const int g = min(g_raw, groups - 1);
     r.g = g;
     const bool second_live = 2 * g + 1 < chunks;
 #pragma unroll
-    for (int k = 0; k < kPiecesA; ++k) {
-      const int piece = tid + k * kThreadsN;
-      const int token = min(token0 + piece % T::kTokens, a.m - 1), half = (piece / T::kTokens) & 1;
-      const bool live = half == 0 || second_live;
-      const int8_t* src = q8 + (size_t)token * q8_stride + (size_t)g * kGroup + (live ? half * 64 : 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r.a[k][i] = *reinterpret_cast<const uint4*>(src + i * 16);
+    for (int k = 0; k < kLoadsA; ++k) {
+      const int f = k * kThreadsN + tid;
+      const int token = min(token0 + (f >> 3), a.m - 1), piece = f & 7;
+      const int offset = (second_live ? piece : (piece & 3)) * 16;
+      r.a[k] = *reinterpret_cast<const uint4*>(q8 + (size_t)token * q8_stride + (size_t)g * kGroup + offset);
     }
 #pragma unroll
-    for (int k = 0; k < kPiecesB; ++k) {
-      const int piece = tid + k * kThreadsN;
-      const int row = min(row0 + piece % T::kRowsPerBlock, a.rows - 1), half = (piece / T::kRowsPerBlock) & 1;
-      const bool live = half == 0 || second_live;
-      r.b[k] = *reinterpret_cast<const uint4*>(packed + (size_t)row * a.row_bytes + (size_t)g * 32 + (live ? half * 16 : 0));
+    for (int k = 0; k < kLoadsB; ++k) {
+      const int f = k * kThreadsN + tid;
+      const int row = min(row0 + (f >> 1), a.rows - 1), half = f & 1;
+      const int offset = (second_live ? half : 0) * 16;
+      r.b[k] = *reinterpret_cast<const uint4*>(packed + (size_t)row * a.row_bytes + (size_t)g * 32 + offset);
     }
     r.s = s_src[g];  // clamped row: valid for every thread
+    r.x0 = x_src[2 * g];
+    r.x1 = x_src[min(2 * g + 1, chunks - 1)];
   };
   auto stage = [&](const Regs& r, int buffer) {
     unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
     const bool second_live = 2 * r.g + 1 < chunks;  // wave-uniform
 #pragma unroll
-    for (int k = 0; k < kPiecesA; ++k) {
-      const int piece = tid + k * kThreadsN;
-      if (piece < 2 * T::kTokens) {
-        const int half = piece / T::kTokens;
-        unsigned char* dst = base + (piece % T::kTokens) * kRowPitch + half * 64;
-        if (second_live) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(dst + i * 16) = r.a[k][i];
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<uint4*>(dst + i * 16) = half == 0 ? r.a[k][i] : make_uint4(0u, 0u, 0u, 0u);
-        }
-      }
+    for (int k = 0; k < kLoadsA; ++k) {
+      const int f = k * kThreadsN + tid;
+      const int piece = f & 7;
+      uint4* dst = reinterpret_cast<uint4*>(base + (f >> 3) * kRowPitch + piece * 16);
+      *dst = (second_live || piece < 4) ? r.a[k] : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
-    for (int k = 0; k < kPiecesB; ++k) {
-      const int piece = tid + k * kThreadsN;
-      if (piece < 2 * T::kRowsPerBlock) {
-        unsigned char* dst = base + (T::kTokens + piece % T::kRowsPerBlock) * kRowPitch + (piece / T::kRowsPerBlock) * 64;
-        const unsigned words[4] = {r.b[k].x, r.b[k].y, r.b[k].z, r.b[k].w};
+    for (int k = 0; k < kLoadsB; ++k) {
+      const int f = k * kThreadsN + tid;
+      unsigned char* dst = base + (T::kTokens + (f >> 1)) * kRowPitch + (f & 1) * 64;
+      const unsigned words[4] = {r.b[k].x, r.b[k].y, r.b[k].z, r.b[k].w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint4 e;
-          e.x = signed_codes(words[j], 0);
-          e.y = signed_codes(words[j], 1);
-          e.z = signed_codes(words[j], 2);
-          e.w = signed_codes(words[j], 3);
-          *reinterpret_cast<uint4*>(dst + j * 16) = e;
-        }
+      for (int j = 0; j < 4; ++j) {
+        uint4 e;
+        e.x = field_codes(words[j], 0);
+        e.y = field_codes(words[j], 1);
+        e.z = field_codes(words[j], 2);
+        e.w = field_codes(words[j], 3);
+        *reinterpret_cast<uint4*>(dst + j * 16) = e;
       }
     }
-    if (s_thread) reinterpret_cast<float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch)[tid] = h2f(r.s);
+    if (s_thread) reinterpret_cast<float*>(base + T::kScaleOffset)[tid] = h2f(r.s);
+    if (x_thread) reinterpret_cast<int*>(base + T::kSumOffset)[tid] = -(r.x0 + (second_live ? r.x1 : 0));
   };
 
   float acc[4][4][4];
@@ -160,14 +161,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
       for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
 
   // One group from LDS.  The weight fragments of both MFMA halves stay in
-  // registers; per 16-token row of tiles the two halves accumulate the exact
-  // int32 partials, which are folded into fp32 with one fmaf per output and
-  // the row's group scale while the next row of tiles runs on the MFMA unit.
+  // registers; per 16-token row of tiles the accumulators start at minus the
+  // tokens' group sums and the two halves add sum(code * q), giving P; the
+  // previous row's P is folded into fp32 (one fmaf per output with the row's
+  // group scale) while this row's MFMAs run.
   auto compute = [&](int buffer) {
     const unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
     const unsigned char* a_lds = base + (wm * 64 + col) * kRowPitch;
     const unsigned char* b_lds = base + (T::kTokens + wn * 64 + col) * kRowPitch;
-    const float* s_lds = reinterpret_cast<const float*>(base + (T::kTokens + T::kRowsPerBlock) * kRowPitch);
+    const float* s_lds = reinterpret_cast<const float*>(base + T::kScaleOffset);
+    const int* x_lds = reinterpret_cast<const int*>(base + T::kSumOffset) + wm * 64 + 4 * kb;
     v4i bf[2][4];
     float sc[4];
 #pragma unroll
@@ -176,21 +179,37 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
       bf[1][nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb + 1) * 16);
       sc[nt] = s_lds[wn * 64 + nt * 16 + col];
     }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const v4i a0 = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb) * 16);
-      const v4i a1 = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb + 1) * 16);
-      v4i p[4];
-      const v4i zero = {0, 0, 0, 0};
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bf[0][nt], zero, 0, 0, 0);
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bf[1][nt], p[nt], 0, 0, 0);
+    auto fold = [&](const v4i (&p)[4], int mt) {
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[mt][nt][i] = __builtin_fmaf((float)p[nt][i], sc[nt], acc[mt][nt][i]);
+    };
+    v4i prev[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const v4i a0 = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb) * 16);
+      const v4i a1 = *reinterpret_cast<const v4i*>(a_lds + mt * 16 * kRowPitch + (2 * kb + 1) * 16);
+      const v4i seed = *reinterpret_cast<const v4i*>(x_lds + mt * 16);
+      v4i p[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bf[0][nt], seed, 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bf[1][nt], p[nt], 0, 0, 0);
+      if (mt > 0) fold(prev, mt - 1);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) prev[nt] = p[nt];
+      if (mt > 0) {
+        // Issue order hint: each of this row's MFMAs followed by four VALU
+        // instructions of the previous row's fold.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+      }
     }
+    fold(prev, 3);
   };
 
   // LDS buffer g & 1 holds group g; register sets r0 / r1 alternate.
@@ -212,34 +231,70 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
     fetch(r0, g + 4);
   }
 
-  // Epilogue: lane holds rows row0 + wn*64 + nt*16 + col, tokens token0 + wm*64 + mt*16 + 4*kb + i.
-  const bool full = token0 + T::kTokens <= a.m && row0 + T::kRowsPerBlock <= a.rows;
+  // Epilogue.  y = acc * s_x[t] (+ bias[r]) in the MFMA layout (lane holds
+  // row nt*16 + col of tokens mt*16 + 4*kb + i), transposed through LDS (the
+  // stage buffers are free by now) so that each lane then owns four
+  // consecutive rows of one token and the stores are 16-byte vectors over
+  // whole rows of the output.
   float sx[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) sx[mt][i] = scale_in[min(token0 + wm * 64 + mt * 16 + 4 * kb + i, a.m - 1)];
+  constexpr int kPitch = 68;  // floats per LDS tile row: conflict-free column writes
+  static_assert(T::kWaves * 64 * kPitch * 4 <= 2 * T::kStageBytes, "the transpose fits the stage buffers");
+  float* tile = reinterpret_cast<float*>(smem) + wave * 64 * kPitch;
+  __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int row = row0 + wn * 64 + nt * 16 + col;
-    const bool row_live = row < a.rows;
-    const float b = (bias != nullptr && row_live) ? bias[row] : 0.0f;
+    const float b = (bias != nullptr && row < a.rows) ? bias[row] : 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = token0 + wm * 64 + mt * 16 + 4 * kb + i;
-        const bool live = full || (row_live && t < a.m);
         float y = acc[mt][nt][i] * sx[mt][i];
         if (bias != nullptr) y = y + b;
-        float* orow = output + (size_t)min(t, a.m - 1) * a.out_stride;
-        if constexpr (EPI == kSiluPair) {
-          const float partner = __shfl_xor(y, 1);
-          if (live && (row & 1) == 0 && row + 1 < a.rows) orow[row >> 1] = ivo_silu(y) * partner;
-        } else if constexpr (EPI == kResidual) {
-          if (live) orow[row] = orow[row] + y;
-        } else {
-          if (live) orow[row] = y;
+        tile[(mt * 16 + 4 * kb + i) * kPitch + nt * 16 + col] = y;
+      }
+  }
+  __syncthreads();
+  const int r4 = (lane & 15) * 4;
+  const int row = row0 + wn * 64 + r4;  // first of the lane's four rows (a multiple of 4)
+  const bool rows_whole = row + 3 < a.rows;
+  const uintptr_t base_addr = reinterpret_cast<uintptr_t>(output);
+  const bool vec4 = (a.out_stride & 3) == 0 && (base_addr & 15) == 0;
+  const bool vec2 = (a.out_stride & 1) == 0 && (base_addr & 7) == 0;
+#pragma unroll 4
+  for (int j = 0; j < 16; ++j) {
+    const int tl = j * 4 + (lane >> 4);
+    const int t = token0 + wm * 64 + tl;
+    if (t >= a.m) continue;
+    const float4 v = *reinterpret_cast<const float4*>(tile + tl * kPitch + r4);
+    float* orow = output + (size_t)t * a.out_stride;
+    if constexpr (EPI == kSiluPair) {
+      const float p0 = ivo_silu(v.x) * v.y, p1 = ivo_silu(v.z) * v.w;
+      if (rows_whole && vec2) {
+        *reinterpret_cast<float2*>(orow + (row >> 1)) = make_float2(p0, p1);
+      } else {
+        if (row + 1 < a.rows) orow[row >> 1] = p0;
+        if (row + 3 < a.rows) orow[(row >> 1) + 1] = p1;
+      }
+    } else if (rows_whole && vec4) {
+      float4* dst = reinterpret_cast<float4*>(orow + row);
+      if constexpr (EPI == kResidual) {
+        const float4 o = *dst;
+        *dst = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+      } else {
+        *dst = v;
+      }
+    } else {
+      const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (row + k < a.rows) {
+          if constexpr (EPI == kResidual) orow[row + k] = orow[row + k] + vs[k];
+          else orow[row + k] = vs[k];
         }
       }
     }
