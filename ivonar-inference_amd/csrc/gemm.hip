@@ -9,16 +9,18 @@
 // loop walks the 128-input groups.  For each group the block stages, double
 // buffered in LDS:
 //   * the q8 bytes of its tokens (128 per token, the q8 layout's two chunks);
-//   * its weight rows' 32 packed bytes, expanded once per block to the codes
-//     0, 1, 2 as int8 (two VALU operations per 4 codes);
+//   * its weight rows' 32 packed bytes, which each wave reads as 8 bytes per
+//     lane and expands in registers to the codes 0, 1, 2 as int8 (two VALU
+//     operations per 4 codes) - a quarter of the LDS traffic of staging the
+//     expanded codes;
 //   * minus each token's activation sum over the group, which seeds the
 //     MFMA accumulator, so sum (code * q) - sum q = P comes out exact with no
 //     per-output correction;
 //   * the fp16 group scales of its rows.
-// LDS rows are padded from 128 to 144 bytes, which spreads the 16 lanes of
-// each 16-byte operand read over distinct banks.  Each group's global loads
-// are issued two group-steps before they are staged, from two register sets,
-// and there is one barrier per group.
+// LDS rows are padded (q8 rows from 128 to 144 bytes, packed rows from 32 to
+// 48), which spreads the lanes of each operand read over distinct banks.
+// Each group's global loads are issued two group-steps before they are
+// staged, from two register sets, and there is one barrier per group.
 //
 // Operand pairing: MFMA half h of a group takes, in lane (c = lane % 16,
 // kb = lane / 16), the 16 bytes of word 2*kb + h of the group (inputs
@@ -38,19 +40,32 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kRowPitch = 144;  // bytes per staged LDS row (128 + 16 padding)
 
+// Raw buffer resource over `bytes` bytes of an operand (the launcher keeps
+// every operand below 2 GiB).  Offsets at or past the size read zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t operand_buffer(const void* base, long long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // Codes of field k of four packed bytes, one per byte (0, 1, 2).
 __device__ __forceinline__ unsigned field_codes(unsigned w, int k) { return (w >> (2 * k)) & kLow2; }
 
-// LDS stage: A rows, B rows, then fp32 row scales and minus the token sums.
+constexpr int kPackedPitch = 48;  // bytes per staged packed weight row (32 + 16 padding)
+constexpr int kOutPitch = 68;     // floats per row of the epilogue's transpose tile
+
+// LDS stage: A rows (q8), packed B rows, fp32 row scales, minus the token
+// sums.  Two stages, and afterwards the epilogue's transpose tiles.
 template <int WM, int WN>
 struct Tile {
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreadsPerBlock = 64 * kWaves;
   static constexpr int kTokens = 64 * WM;
   static constexpr int kRowsPerBlock = 64 * WN;
-  static constexpr int kScaleOffset = (kTokens + kRowsPerBlock) * kRowPitch;
+  static constexpr int kPackedOffset = kTokens * kRowPitch;
+  static constexpr int kScaleOffset = kPackedOffset + kRowsPerBlock * kPackedPitch;
   static constexpr int kSumOffset = kScaleOffset + kRowsPerBlock * 4;
   static constexpr int kStageBytes = kSumOffset + kTokens * 4;
+  static constexpr int kOutBytes = kWaves * 64 * kOutPitch * 4;
+  static constexpr int kLdsBytes = 2 * kStageBytes > kOutBytes ? 2 * kStageBytes : kOutBytes;
 };
 
 template <int EPI, int WM, int WN>
@@ -93,35 +108,49 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
   };
   const bool s_thread = tid < T::kRowsPerBlock;
   const bool x_thread = tid < T::kTokens;
-  const uint16_t* s_src = scales + (size_t)min(row0 + tid % T::kRowsPerBlock, a.rows - 1) * a.groups;
-  const int32_t* x_src = a.xsum_in + (size_t)min(token0 + tid % T::kTokens, a.m - 1) * chunks;
 
-  // Loads are unconditional, with the group clamped into the matrix (a
-  // predicated load would make the compiler wait for every outstanding load
-  // at its first use).  A missing second chunk reads the group's first chunk;
-  // its activations and chunk sum are replaced by zeros when staged, which
-  // also cancels whatever its weight bytes hold.
+  // Buffer loads: each operand is a buffer resource whose size the hardware
+  // checks, returning zeros past it (tokens past m, rows past the matrix),
+  // so no address is clamped.  A thread's offsets into the operands are
+  // fixed for the whole kernel; the group advances a scalar offset.  A
+  // missing second chunk (odd chunk count, last group) is read at an offset
+  // past the operand, and its chunk sum is dropped when staged.  Loads are
+  // never predicated (a predicated load would make the compiler wait for
+  // every outstanding load at its first use).
+  constexpr int kPast = 0x7FFFFFF0;
+  const __amdgpu_buffer_rsrc_t q8_buf = operand_buffer(q8, (long long)a.m * (long long)q8_stride);
+  const __amdgpu_buffer_rsrc_t w_buf = operand_buffer(packed, (long long)a.rows * a.row_bytes);
+  const __amdgpu_buffer_rsrc_t s_buf = operand_buffer(scales, (long long)a.rows * a.groups * 2);
+  const __amdgpu_buffer_rsrc_t x_buf = operand_buffer(a.xsum_in, (long long)a.m * chunks * 4);
+  int a_off[kLoadsA], a_dead[kLoadsA], b_off[kLoadsB], b_dead[kLoadsB];
+#pragma unroll
+  for (int k = 0; k < kLoadsA; ++k) {
+    const int f = k * kThreadsN + tid;
+    a_off[k] = (token0 + (f >> 3)) * (int)q8_stride + (f & 7) * 16;
+    a_dead[k] = (f & 7) < 4 ? a_off[k] : kPast;
+  }
+#pragma unroll
+  for (int k = 0; k < kLoadsB; ++k) {
+    const int f = k * kThreadsN + tid;
+    b_off[k] = (row0 + (f >> 1)) * a.row_bytes + (f & 1) * 16;
+    b_dead[k] = (f & 1) == 0 ? b_off[k] : kPast;
+  }
+  const int s_off = (row0 + tid % T::kRowsPerBlock) * a.groups * 2;
+  const int x_off = (token0 + tid % T::kTokens) * chunks * 4;
+
   auto fetch = [&](Regs& r, int g_raw) {
     const int g = min(g_raw, groups - 1);
     r.g = g;
     const bool second_live = 2 * g + 1 < chunks;
 #pragma unroll
-    for (int k = 0; k < kLoadsA; ++k) {
-      const int f = k * kThreadsN + tid;
-      const int token = min(token0 + (f >> 3), a.m - 1), piece = f & 7;
-      const int offset = (second_live ? piece : (piece & 3)) * 16;
-      r.a[k] = *reinterpret_cast<const uint4*>(q8 + (size_t)token * q8_stride + (size_t)g * kGroup + offset);
-    }
+    for (int k = 0; k < kLoadsA; ++k)
+      r.a[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(q8_buf, second_live ? a_off[k] : a_dead[k], g * kGroup, 0));
 #pragma unroll
-    for (int k = 0; k < kLoadsB; ++k) {
-      const int f = k * kThreadsN + tid;
-      const int row = min(row0 + (f >> 1), a.rows - 1), half = f & 1;
-      const int offset = (second_live ? half : 0) * 16;
-      r.b[k] = *reinterpret_cast<const uint4*>(packed + (size_t)row * a.row_bytes + (size_t)g * 32 + offset);
-    }
-    r.s = s_src[g];  // clamped row: valid for every thread
-    r.x0 = x_src[2 * g];
-    r.x1 = x_src[min(2 * g + 1, chunks - 1)];
+    for (int k = 0; k < kLoadsB; ++k)
+      r.b[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_buf, second_live ? b_off[k] : b_dead[k], g * 32, 0));
+    r.s = __builtin_amdgcn_raw_buffer_load_b16(s_buf, s_off, g * 2, 0);
+    r.x0 = (int)__builtin_amdgcn_raw_buffer_load_b32(x_buf, x_off, g * 8, 0);
+    r.x1 = (int)__builtin_amdgcn_raw_buffer_load_b32(x_buf, second_live ? x_off + 4 : kPast, g * 8, 0);
   };
   auto stage = [&](const Regs& r, int buffer) {
     unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
@@ -136,17 +165,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
 #pragma unroll
     for (int k = 0; k < kLoadsB; ++k) {
       const int f = k * kThreadsN + tid;
-      unsigned char* dst = base + (T::kTokens + (f >> 1)) * kRowPitch + (f & 1) * 64;
-      const unsigned words[4] = {r.b[k].x, r.b[k].y, r.b[k].z, r.b[k].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint4 e;
-        e.x = field_codes(words[j], 0);
-        e.y = field_codes(words[j], 1);
-        e.z = field_codes(words[j], 2);
-        e.w = field_codes(words[j], 3);
-        *reinterpret_cast<uint4*>(dst + j * 16) = e;
-      }
+      *reinterpret_cast<uint4*>(base + T::kPackedOffset + (f >> 1) * kPackedPitch + (f & 1) * 16) = r.b[k];
     }
     if (s_thread) reinterpret_cast<float*>(base + T::kScaleOffset)[tid] = h2f(r.s);
     if (x_thread) reinterpret_cast<int*>(base + T::kSumOffset)[tid] = -(r.x0 + (second_live ? r.x1 : 0));
@@ -168,15 +187,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
   auto compute = [&](int buffer) {
     const unsigned char* base = smem + (size_t)buffer * T::kStageBytes;
     const unsigned char* a_lds = base + (wm * 64 + col) * kRowPitch;
-    const unsigned char* b_lds = base + (T::kTokens + wn * 64 + col) * kRowPitch;
+    const unsigned char* b_lds = base + T::kPackedOffset + (wn * 64 + col) * kPackedPitch + kb * 8;
     const float* s_lds = reinterpret_cast<const float*>(base + T::kScaleOffset);
     const int* x_lds = reinterpret_cast<const int*>(base + T::kSumOffset) + wm * 64 + 4 * kb;
     v4i bf[2][4];
     float sc[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      bf[0][nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb) * 16);
-      bf[1][nt] = *reinterpret_cast<const v4i*>(b_lds + nt * 16 * kRowPitch + (2 * kb + 1) * 16);
+      // Words 2kb and 2kb+1 of the row's group, expanded to one code per byte.
+      const uint2 w = *reinterpret_cast<const uint2*>(b_lds + nt * 16 * kPackedPitch);
+      bf[0][nt] = v4i{(int)field_codes(w.x, 0), (int)field_codes(w.x, 1), (int)field_codes(w.x, 2),
+                      (int)field_codes(w.x, 3)};
+      bf[1][nt] = v4i{(int)field_codes(w.y, 0), (int)field_codes(w.y, 1), (int)field_codes(w.y, 2),
+                      (int)field_codes(w.y, 3)};
       sc[nt] = s_lds[wn * 64 + nt * 16 + col];
     }
     auto fold = [&](const v4i (&p)[4], int mt) {
@@ -219,14 +242,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
   stage(r0, 0);
   __syncthreads();
   fetch(r0, 2);
+  // Staging is unconditional (past the last group it rewrites the idle
+  // buffer with the last group's data), so each group step is one straight
+  // block the scheduler can interleave.
   for (int g = 0; g < groups; g += 2) {
     compute(0);
-    if (g + 1 < groups) stage(r1, 1);
+    stage(r1, 1);
     __syncthreads();
     fetch(r1, g + 3);
     if (g + 1 >= groups) break;
     compute(1);
-    if (g + 2 < groups) stage(r0, 0);
+    stage(r0, 0);
     __syncthreads();
     fetch(r0, g + 4);
   }
@@ -241,8 +267,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const int8_t* __rest
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) sx[mt][i] = scale_in[min(token0 + wm * 64 + mt * 16 + 4 * kb + i, a.m - 1)];
-  constexpr int kPitch = 68;  // floats per LDS tile row: conflict-free column writes
-  static_assert(T::kWaves * 64 * kPitch * 4 <= 2 * T::kStageBytes, "the transpose fits the stage buffers");
+  constexpr int kPitch = kOutPitch;  // conflict-free column writes
   float* tile = reinterpret_cast<float*>(smem) + wave * 64 * kPitch;
   __syncthreads();
 #pragma unroll
@@ -305,7 +330,7 @@ template <int EPI, int WM, int WN>
 hipError_t launch_shape(hipStream_t stream, const GemmArgs& a) {
   using T = Tile<WM, WN>;
   const dim3 grid(ceil_div(a.rows, T::kRowsPerBlock), ceil_div(a.m, T::kTokens));
-  const size_t lds = 2 * (size_t)T::kStageBytes;
+  const size_t lds = (size_t)T::kLdsBytes;
   hipLaunchKernelGGL((gemm_kernel<EPI, WM, WN>), grid, dim3(T::kThreadsPerBlock), lds, stream, a.q8_in, a.scale_in,
                      a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
@@ -330,7 +355,7 @@ namespace {
 
 template <int WM, int WN>
 bool fits() {
-  return 2 * Tile<WM, WN>::kStageBytes <= max_lds_per_block();
+  return Tile<WM, WN>::kLdsBytes <= max_lds_per_block();
 }
 
 // Block shape: the largest tile that still gives about one block per CU and
@@ -354,6 +379,11 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (a.rows <= 0 || a.m <= 0) return hipSuccess;
   const int splits = skinny_splits(a.m, a.rows, a.n, (size_t)max_lds_per_block());
   if (splits > 0) return launch_skinny(stream, a, splits);
+  // Buffer offsets are 32-bit: every operand (with a tile of slack) stays below 2 GiB.
+  const long long limit = 0x7FFFFFF0LL;
+  if (((long long)a.m + 256) * ceil_div(a.n, kChunk) * kChunk >= limit ||
+      ((long long)a.rows + 256) * a.row_bytes >= limit || ((long long)a.rows + 256) * a.groups * 2 >= limit)
+    return hipErrorInvalidValue;
   switch (a.epi) {
     case kStore: return launch_epi<kStore>(stream, a);
     case kResidual: return launch_epi<kResidual>(stream, a);
