@@ -37,13 +37,48 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
                                                                  int64_t* __restrict__ out) {
   __shared__ float best_value[kArgmaxThreads / 64];
   __shared__ int best_index[kArgmaxThreads / 64];
+  // (value, index) pairs are compared by value, then by smaller index, so
+  // the result does not depend on the order the elements are visited in.
+  // Loads go out in batches (a 16-byte vector per element group when the
+  // row allows it), clamped to the row and masked after.
   float value = -__builtin_inff();
   int index = n;
-  for (int i = threadIdx.x; i < n; i += kArgmaxThreads) {
-    const float v = values[i];
+  auto consider = [&](float v, int i) {
     if (v > value || (v == value && i < index)) {
       value = v;
       index = i;
+    }
+  };
+  constexpr int kBatch = 8;
+  int scalar_from = 0;
+  if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(values) & 15) == 0) {
+    const float4* v4 = reinterpret_cast<const float4*>(values);
+    const int n4 = n >> 2;
+    for (int base = 0; base < n4; base += kArgmaxThreads * kBatch) {
+      float4 b[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) b[k] = v4[min(base + k * kArgmaxThreads + (int)threadIdx.x, n4 - 1)];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int j = base + k * kArgmaxThreads + threadIdx.x;
+        if (j < n4) {
+          consider(b[k].x, 4 * j);
+          consider(b[k].y, 4 * j + 1);
+          consider(b[k].z, 4 * j + 2);
+          consider(b[k].w, 4 * j + 3);
+        }
+      }
+    }
+    scalar_from = n;
+  }
+  for (int base = scalar_from; base < n; base += kArgmaxThreads * kBatch) {
+    float b[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) b[k] = values[min(base + k * kArgmaxThreads + (int)threadIdx.x, n - 1)];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int i = base + k * kArgmaxThreads + threadIdx.x;
+      if (i < n) consider(b[k], i);
     }
   }
   for (int offset = 32; offset > 0; offset >>= 1) {

@@ -39,6 +39,7 @@ namespace {
 
 constexpr int kRows = 2;  // rows per lane; even, so a silu pair stays in one lane
 constexpr int kFusedLimit = 4096;
+static_assert(kFusedLimit <= kThreads * kBatch, "the fused prologue holds a row in registers");
 constexpr int kMaxLdsBytes = 64 * 1024;
 constexpr int kBlocksPerCu = 4;
 
@@ -178,24 +179,32 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
   int4 qr[QREG ? NJ : 1][4];
   int xr[QREG ? NJ : 1];
   if constexpr (FUSED) {
-    // The block quantizes the token into LDS, then each lane takes its chunks' quads.
+    // The block quantizes the token into LDS, then each lane takes its
+    // chunks' quads.  PLAIN and NORM rows are read once into registers; the
+    // lane forms its chunks' sums from the quads it holds.
     const RowSource src{in.input, in.aux, sh.n, sh.eps, sh.splits, sh.head_dim};
-    float inv_rms;
-    sx = row_scale<MODE>(src, inv_rms, slots);
-    for (int d = threadIdx.x; d < chunks * 16; d += kThreads) {
-      const int u = d >> 4, w = (d >> 2) & 3, k = d & 3;
-      const int value = quantize_word<MODE>(src, u, w, k, inv_rms, sx);
-      reinterpret_cast<int*>(lds_q)[(w * chunks + u) * 4 + k] = value;
-      const int total = chunk_lane_sum(word_sum(value));
-      if ((d & 15) == 0) lds_x[u] = total;
+    if constexpr (MODE == kAttn) {
+      float inv_rms;
+      sx = row_scale<MODE>(src, inv_rms, slots);
+      for (int d = threadIdx.x; d < chunks * 16; d += kThreads) {
+        const int u = d >> 4, w = (d >> 2) & 3, k = d & 3;
+        const int value = quantize_word<MODE>(src, u, w, k, inv_rms, sx);
+        reinterpret_cast<int*>(lds_q)[(w * chunks + u) * 4 + k] = value;
+      }
+    } else {
+      sx = quantize_row_to_lds<MODE>(src, chunks, reinterpret_cast<unsigned char*>(lds_q), slots);
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int u = min(j * lanes + sub, chunks - 1);
+      int total = 0;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) qr[j][w] = lds_q[w * chunks + u];
-      xr[j] = lds_x[u];
+      for (int w = 0; w < 4; ++w) {
+        qr[j][w] = lds_q[w * chunks + u];
+        total = word_sum(qr[j][w].x) + word_sum(qr[j][w].y) + word_sum(qr[j][w].z) + word_sum(qr[j][w].w) + total;
+      }
+      xr[j] = total;
     }
   } else if constexpr (QREG) {
     // Pre-quantized and at most two steps per lane: the lane's quads straight from global memory.

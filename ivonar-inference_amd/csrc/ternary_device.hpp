@@ -114,6 +114,18 @@ __device__ __forceinline__ float block_max(float v, float* slots) {
 // the row masked to zero, which leaves a non-negative fma chain unchanged).
 constexpr int kBatch = 16;
 
+// The block part of that tree, from each thread's fma partial.
+__device__ __forceinline__ float tree_reduce(float s, float* slots) {
+  const int tid = threadIdx.x;
+  for (int offset = 16; offset > 0; offset >>= 1) s = s + __shfl_xor(s, offset);
+  if ((tid & 31) == 0) slots[tid >> 5] = s;
+  __syncthreads();
+  float total = 0.0f;
+  for (int w = 0; w < kThreads / 32; ++w) total = total + slots[w];
+  __syncthreads();
+  return total;
+}
+
 __device__ __forceinline__ float tree_sum_squares(const float* __restrict__ x, int n, float* slots) {
   const int tid = threadIdx.x;
   float s = 0.0f;
@@ -127,13 +139,7 @@ __device__ __forceinline__ float tree_sum_squares(const float* __restrict__ x, i
       s = __builtin_fmaf(value, value, s);
     }
   }
-  for (int offset = 16; offset > 0; offset >>= 1) s = s + __shfl_xor(s, offset);
-  if ((tid & 31) == 0) slots[tid >> 5] = s;
-  __syncthreads();
-  float total = 0.0f;
-  for (int w = 0; w < kThreads / 32; ++w) total = total + slots[w];
-  __syncthreads();
-  return total;
+  return tree_reduce(s, slots);
 }
 
 // Source value of input i (ternary.cu:128-146 for the split-softmax merge).
@@ -242,6 +248,57 @@ __device__ __forceinline__ int word_sum(int word) { return sdot4((unsigned)word,
 __device__ __forceinline__ int chunk_lane_sum(int v) {
   for (int offset = 1; offset < 16; offset <<= 1) v += __shfl_xor(v, offset);
   return v;
+}
+
+// Whole-block quantizer for one PLAIN or NORM token row of at most
+// kThreads * kBatch inputs that reads the row once: thread t holds inputs
+// t + 256*b in registers, which is also the reference's order for the
+// sum-of-squares partials (so the fp32 result is the same as row_scale's).
+// The q8 bytes go to LDS in the quad-planar layout (quad w of chunk u at
+// 16-byte slot w*C + u; word k of a quad holds inputs 16w + k + 4b' at byte
+// b'), zero past n up to C*64.  Returns the token scale.  All threads of the
+// block call it; it ends with the block's writes not yet fenced.
+template <int MODE>
+__device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int chunks, unsigned char* lds_q,
+                                                     float* slots) {
+  static_assert(MODE == kPlain || MODE == kNorm, "register path for PLAIN and NORM rows");
+  const int tid = threadIdx.x;
+  const int n = src.n;
+  float v[kBatch], w[kBatch];
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    const int i = min(b * kThreads + tid, n - 1);
+    v[b] = src.input[i];
+    w[b] = MODE == kNorm ? src.aux[i] : 1.0f;
+  }
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b)
+    if (b * kThreads + tid >= n) v[b] = 0.0f;
+  float inv_rms = 1.0f;
+  if constexpr (MODE == kNorm) {
+    float s = 0.0f;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) s = __builtin_fmaf(v[b], v[b], s);
+    inv_rms = 1.0f / __builtin_sqrtf(tree_reduce(s, slots) / (float)n + src.eps);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    if constexpr (MODE == kNorm) v[b] = fminf(fmaxf(v[b] * inv_rms, -8.0f), 8.0f) * w[b];
+    amax = fmaxf(amax, fabsf(v[b]));
+  }
+  amax = block_max(amax, slots + 32);
+  const float scale = fmaxf(amax / 127.0f, 1e-5f);
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    const int i = b * kThreads + tid;
+    if (i < chunks * kChunk) {
+      const int q = i < n ? (int)__builtin_rintf(v[b] / scale) : 0;
+      const int u = i >> 6, r = i & 63;
+      lds_q[((((r >> 4) & 3) * chunks + u) << 4) + ((r & 3) << 2) + ((r >> 2) & 3)] = (unsigned char)(q & 0xff);
+    }
+  }
+  return scale;
 }
 
 }  // namespace ivo

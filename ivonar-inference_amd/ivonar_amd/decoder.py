@@ -14,7 +14,7 @@ decode step (``kernel_decoder.py:233-269``)::
       gemv_plain_residual   out                   V third of mixer_in -> residual +=
       gemv_norm_silu_pair   gate/up (interleaved) residual -> ffn_mid    (RMSNorm prologue)
       gemv_plain_residual   down                  ffn_mid -> residual +=
-    quantize_norm + gemv_prequant_store           residual -> logits (tied token matrix)
+    gemv_norm_store                               residual -> logits (tied token matrix, RMSNorm fused)
     ivonar_argmax                                 logits -> next token (greedy, top_k = 1)
 
 prefill tile (``kernel_decoder.py:303-368``): ``embed_tile``, per layer
@@ -109,10 +109,10 @@ class StackDecoder:
         self.q8_tile = torch.zeros(TILE, max_chunks * CHUNK, dtype=torch.int8, device=device)
         self.xsum_tile = torch.zeros(TILE, max_chunks, dtype=torch.int32, device=device)
         self.scale_tile = torch.zeros(TILE, **f32)
-        self._head = [
-            self._quantize("quantize_norm", self.residual, self.final_norm, hidden, eps=config.eps),
-            self._gemv("gemv_prequant_store", self.token_matrix, None, None, self.logits, prequant=True),
-        ]
+        # The head is one GEMV with the RMSNorm prologue fused (the reference runs quantize_norm and
+        # gemv_prequant_store, kernel_decoder.py:265-267; the logits are the same bits either way).
+        self._head = [self._gemv("gemv_norm_store", self.token_matrix, self.residual, self.final_norm, self.logits,
+                                 eps=config.eps)]
         self._steps = [self._build_step(slot) for slot in range(self.burst)]
         self._tile = self._build_tile()
         self._graph: torch.cuda.CUDAGraph | None = None

@@ -329,6 +329,23 @@ def test_embed_gather_and_argmax(cuda, oracle):
     assert int(to_np(ops.argmax(_t(values, cuda)))[0]) == oracle.argmax(values) == 123
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 1023, 32000, 32001, 100003])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_argmax_first_maximum(cuda, oracle, n, offset):
+    """Vector and scalar load paths (offset 1 breaks 16-byte alignment), ties, all-negative rows."""
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(n + offset)
+    values = (rng.standard_normal(n + offset).astype(np.float32) - 10.0)
+    values[offset + rng.integers(0, n, size=min(n, 5))] = -np.inf
+    top = values[offset:].max()
+    ties = np.sort(rng.integers(0, n, size=min(n, 3)))
+    values[offset + ties] = top + 1.0
+    device_values = _t(values, cuda)[offset:]
+    got = int(to_np(ops.argmax(device_values))[0])
+    assert got == oracle.argmax(values[offset:]) == int(ties[0])
+
+
 # ----------------------------------------------------------- graph capture
 
 
