@@ -137,6 +137,30 @@ def time_graph(graph, replays: int, warmup: int) -> float:
     return start.elapsed_time(end) / 1e3 / replays
 
 
+def read_ceiling(matrices, stream) -> dict:
+    """Streaming-read bandwidth over the packed weights the GEMV streams (8 rotating copies of both stress
+    matrices, 58.7 MB each), one launch per matrix, timed like the GEMV: the best a kernel that only reads
+    achieves per launch at this size."""
+    import torch
+
+    from ivonar_amd import runtime
+
+    lib = runtime.library()
+    sink = torch.empty(lib.ivonar_stream_read_sink_words(), dtype=torch.int32, device=matrices[0][0].packed.device)
+    buffers = [(m.packed, m.packed.numel()) for shape in matrices for m in shape]
+    total = sum(size for _, size in buffers)
+
+    def run():
+        stream_id = runtime.current_stream()
+        for tensor, size in buffers:
+            runtime.check(lib.ivonar_stream_read(stream_id, runtime.pointer(tensor), size, runtime.pointer(sink)),
+                          "ivonar_stream_read")
+
+    seconds = time_graph(graph_of(run, stream), 10, 2)
+    return {"GBps": round(total / seconds / 1e9, 1), "bytes": total,
+            "kernel": "ivonar_stream_read (16-byte loads, 4 in flight per thread, 1024 blocks)"}
+
+
 def time_calls(call, stream, calls_per_graph: int, replays: int, warmup: int = 2) -> float:
     """Seconds per call: `calls_per_graph` back-to-back calls recorded in one HIP graph, so that the time of
     a short kernel is not the host's graph-launch time."""
@@ -326,6 +350,7 @@ def main() -> None:
     kernel_bytes = sum(v["bytes"] for v in kernel.values())
     kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
     achieved = kernel_bytes / kernel_seconds / 1e9
+    ceiling = read_ceiling(matrices, stream)
 
     # ---- single linear K=1024 -> N=4096 (launch-latency bound) ------------------------------
     layer0, x0 = synthetic.single_linear(seed=0)
@@ -398,6 +423,8 @@ def main() -> None:
             "traffic_detail": traffic,
             "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
             "kernel": "gemv_kernel (pre-quantized activations)",
+            "read_ceiling": ceiling,
+            "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 4),
             "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)} for k, v in kernel.items()},
         },
         "cpu_baseline": cpu,

@@ -162,6 +162,14 @@ hipError_t gather_token(hipStream_t stream, const float* tile, float* output, in
  * sample_token, ternary.cu:1099-1337). */
 hipError_t ivonar_argmax(hipStream_t stream, const float* values, int n, int64_t* out);
 
+/* Measurement export (no reference counterpart): reads `bytes` (a multiple of
+ * 16, 16-byte aligned) of `data` with 16-byte loads at full occupancy and
+ * writes nothing in practice; `sink` must hold ivonar_stream_read_sink_words()
+ * uint32.  Its bandwidth is the streaming-read ceiling the GEMV is compared
+ * with. */
+int ivonar_stream_read_sink_words(void);
+hipError_t ivonar_stream_read(hipStream_t stream, const void* data, long long bytes, unsigned* sink);
+
 #ifdef __cplusplus
 }
 #endif

@@ -342,4 +342,12 @@ hipError_t ivonar_argmax(hipStream_t stream, const float* values, int n, int64_t
   return launch_argmax(stream, values, n, out);
 }
 
+int ivonar_stream_read_sink_words(void) { return stream_read_sink_words(); }
+
+hipError_t ivonar_stream_read(hipStream_t stream, const void* data, long long bytes, unsigned* sink) {
+  if (data == nullptr || sink == nullptr || bytes < 0 || (bytes & 15) != 0 || !aligned16(data))
+    return hipErrorInvalidValue;
+  return launch_stream_read(stream, data, bytes, sink);
+}
+
 }  // extern "C"

@@ -100,6 +100,10 @@ hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const 
                         const uint16_t* scales, float* output, int n, int row_bytes, int groups);
 hipError_t launch_gather(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid);
 hipError_t launch_argmax(hipStream_t stream, const float* values, int n, int64_t* out);
+// Streaming-read reference (measurement): reads bytes/16 16-byte words of data;
+// sink holds stream_read_sink_words() uint32 and is written only in theory.
+int stream_read_sink_words();
+hipError_t launch_stream_read(hipStream_t stream, const void* data, long long bytes, unsigned* sink);
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -68,6 +68,7 @@ SIGNATURES: dict[str, list] = {
     "gemv_group_partials": [_P, _P, _P, _I, _I, _I, _I, _P],
     "ivonar_quantize_rows": [_I, _P, _I, _P, _I, _F, _I, _I, _P, _P, _P],
     "ivonar_argmax": [_P, _I, _P],
+    "ivonar_stream_read": [_P, ctypes.c_longlong, _P],
 }
 
 _lock = threading.Lock()
@@ -100,6 +101,8 @@ def library() -> ctypes.CDLL:
             lib.ivonar_gemv_plan.restype = None
             lib.ivonar_gemm_plan.argtypes = [c_int, c_int, c_int]
             lib.ivonar_gemm_plan.restype = c_int
+            lib.ivonar_stream_read_sink_words.argtypes = []
+            lib.ivonar_stream_read_sink_words.restype = c_int
             for name, argtypes in SIGNATURES.items():
                 function = getattr(lib, name)
                 function.argtypes = [c_void_p, *argtypes]

@@ -425,10 +425,10 @@ def test_gemm_large_tiles_on_sampled_tokens(cuda, oracle, m, k, rows):
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     sample = np.unique(np.array([0, 1, 63, 64, 127, 128, 255, 256, m // 2, m - 1]) % m)
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
-    assert runtime.gemm_plan(m, rows, k) == 1
-    expected = oracle.gemm_seq(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                               np.zeros((len(sample), rows), np.float32), k, rows, len(sample))
-    assert_bits_equal(y[sample], expected, "sampled tokens")
+    splits = runtime.gemm_plan(m, rows, k)
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), splits)
+    assert_bits_equal(y[sample], expected, f"sampled tokens ({splits} splits)")
     assert np.isfinite(y).all()
 
 

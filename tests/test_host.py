@@ -25,7 +25,7 @@ def test_library_exports_every_declared_entry_point():
 
     lib = runtime.library()
     declared = _declared_functions()
-    assert len(declared) >= 36
+    assert len(declared) >= 38
     missing = [name for name in declared if not hasattr(lib, name)]
     assert not missing, missing
 
