@@ -141,8 +141,16 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
   }
 }
 
+// Threads per block: the rolling layout (long rows, q8 copied to LDS) runs
+// one 1024-thread block per CU, so each CU copies the q8 row once and the
+// copy takes one load round trip; the others run four 256-thread blocks.
+template <bool ROLL>
+constexpr int block_threads() {
+  return ROLL ? 1024 : kThreads;
+}
+
 template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
+__global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
                                                         const float* __restrict__ bias, float* __restrict__ output,
                                                         int32_t* __restrict__ partials, GemvShape sh) {
@@ -164,8 +172,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
   const int sub = lane & (lanes - 1);
   const int slot = lane >> lane_shift;
   const int rows_per_iter = (64 >> lane_shift) * kRows;
-  const int waves = gridDim.x * (kThreads / 64);
-  const int first = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  constexpr int kBlock = block_threads<ROLL>();
+  const int waves = gridDim.x * (kBlock / 64);
+  const int first = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   const int steps = (chunks + lanes - 1) / lanes;
 
   // Weights of the first row step go out before the activation prologue.
@@ -221,17 +230,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvPtrs in, const uint8
     // thread's loads go out before its LDS stores.
     constexpr int kCopyBatch = 8;
     const int words = chunks * 4;
-    for (int base = 0; base < words; base += kThreads * kCopyBatch) {
+    for (int base = 0; base < words; base += kBlock * kCopyBatch) {
       int4 v[kCopyBatch];
 #pragma unroll
-      for (int k = 0; k < kCopyBatch; ++k) v[k] = gq[min(base + k * kThreads + (int)threadIdx.x, words - 1)];
+      for (int k = 0; k < kCopyBatch; ++k) v[k] = gq[min(base + k * kBlock + (int)threadIdx.x, words - 1)];
 #pragma unroll
       for (int k = 0; k < kCopyBatch; ++k) {
-        const int e = base + k * kThreads + threadIdx.x;
+        const int e = base + k * kBlock + threadIdx.x;
         if (e < words) lds_q[(e & 3) * chunks + (e >> 2)] = v[k];
       }
     }
-    for (int u = threadIdx.x; u < chunks; u += kThreads) lds_x[u] = in.xsum_in[u];
+    for (int u = threadIdx.x; u < chunks; u += kBlock) lds_x[u] = in.xsum_in[u];
     sx = *in.scale_in;
     __syncthreads();
   }
@@ -316,22 +325,27 @@ int device_cus() {
 template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
 void launch_one(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                 size_t lds) {
-  hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, NJ, LANES, EXACT, ROLL>), dim3(blocks), dim3(kThreads), lds,
+  hipLaunchKernelGGL((gemv_kernel<MODE, EPI, FUSED, NJ, LANES, EXACT, ROLL>), dim3(blocks),
+                     dim3(block_threads<ROLL>()), lds,
                      stream, p, a.packed, a.scales, a.bias, a.output, a.partials, sh);
 }
 
 // Compiled layouts: 64 lanes per row (rows of more than 32 chunks) with or
 // without dead lanes, and any narrower power of two (one step) likewise.
+// Returns false when the plan asks for a layout that is not compiled.
 template <int MODE, int EPI, bool FUSED, int NJ, bool ROLL>
-void launch_layout(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
+bool launch_layout(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                    size_t lds) {
   if (sh.lanes == 64) {
     if (sh.exact) launch_one<MODE, EPI, FUSED, NJ, 64, true, ROLL>(stream, p, a, sh, blocks, lds);
     else launch_one<MODE, EPI, FUSED, NJ, 64, false, ROLL>(stream, p, a, sh, blocks, lds);
+    return true;
   } else if constexpr (NJ == 1 && !ROLL) {
     if (sh.exact) launch_one<MODE, EPI, FUSED, 1, 0, true, false>(stream, p, a, sh, blocks, lds);
     else launch_one<MODE, EPI, FUSED, 1, 0, false, false>(stream, p, a, sh, blocks, lds);
+    return true;
   }
+  return false;
 }
 
 // Steps per pipeline item: a whole row of up to two steps (q8 in registers),
@@ -347,14 +361,16 @@ template <int MODE, int EPI, bool FUSED>
 hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                      size_t lds, int steps) {
   const int nj = steps_per_item(steps);
+  bool launched = false;
   if (steps <= 2) {
-    if (nj == 1) launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
-    else launch_layout<MODE, EPI, FUSED, 2, false>(stream, p, a, sh, blocks, lds);
+    if (nj == 1) launched = launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
+    else launched = launch_layout<MODE, EPI, FUSED, 2, false>(stream, p, a, sh, blocks, lds);
   } else if constexpr (!FUSED) {
-    if (nj == 4) launch_layout<MODE, EPI, FUSED, 4, true>(stream, p, a, sh, blocks, lds);
-    else if (nj == 2) launch_layout<MODE, EPI, FUSED, 2, true>(stream, p, a, sh, blocks, lds);
-    else launch_layout<MODE, EPI, FUSED, 1, true>(stream, p, a, sh, blocks, lds);
+    if (nj == 4) launched = launch_layout<MODE, EPI, FUSED, 4, true>(stream, p, a, sh, blocks, lds);
+    else if (nj == 2) launched = launch_layout<MODE, EPI, FUSED, 2, true>(stream, p, a, sh, blocks, lds);
+    else launched = launch_layout<MODE, EPI, FUSED, 1, true>(stream, p, a, sh, blocks, lds);
   }
+  if (!launched) return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -406,8 +422,9 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   // Dead lanes exist when the last step is partial (items never hold dead steps).
   sh.exact = chunks % lanes == 0;
   const int cus = device_cus();
-  int blocks = ceil_div(sh.iters, kThreads / 64);
-  const int cap = (fused ? 2 : kBlocksPerCu) * cus;
+  const bool roll = !fused && steps > 2;  // the layouts launch_nj picks
+  int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);
+  const int cap = (fused ? 2 : roll ? 1 : kBlocksPerCu) * cus;
   if (blocks > cap) blocks = cap;
 
   if (fused) {
