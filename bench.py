@@ -33,6 +33,8 @@ sys.path.insert(0, str(ROOT / "ivonar-inference_amd"))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 ROTATING_COPIES = 8
+PROBE_GEMM_SHAPES = [(1024, 4096), (4096, 1024), (4096, 14336)]  # (K, N) of the GEMM probe, in order
+PROBE_GEMM_M = (2048, 32)
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
@@ -49,7 +51,7 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--probe", choices=["gemv-stress", "gemm-prefill"], default=None,
                         help="profiling mode: only the named kernel workload, no JSON line")
     parser.add_argument("--probe-calls", type=int, default=16)
-    parser.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    parser.add_argument("--no-traffic", action="store_true", help="skip the three rocprofv3 counter passes")
     return parser.parse_args()
 
 
@@ -93,9 +95,12 @@ def probe_gemm_prefill(calls: int) -> None:
           f"lds_per_block={getattr(props, 'shared_memory_per_block', '?')}", flush=True)
     rng = np.random.default_rng(2)
     sweep, _ = synthetic.sweep_layer(seed=4)
-    for layer, k in [*synthetic.prefill_layers(seed=2), (sweep, sweep.in_features)]:
+    layers = [*synthetic.prefill_layers(seed=2), (sweep, sweep.in_features)]
+    if [(k, layer.rows) for layer, k in layers] != PROBE_GEMM_SHAPES:
+        raise RuntimeError("GEMM probe shapes changed")
+    for layer, k in layers:
         mat = device_copies(layer, device, 1)[0]
-        for m in (2048, 32):
+        for m in PROBE_GEMM_M:
             xs = torch.from_numpy(synthetic.prefill_activations(rng, m, k)).to(device)
             q8, xsum, sx = ops.quantize_rows(xs)
             out = torch.empty((m, layer.rows), dtype=torch.float32, device=device)
@@ -121,13 +126,23 @@ def graph_of(step, stream):
     return graph
 
 
-def time_graph(graph, replays: int, warmup: int) -> float:
-    """Seconds per replay, HIP events around `replays` replays on the current stream."""
+def time_graph(graph, replays: int, warmup: int, median: bool = False) -> float:
+    """Seconds per replay on the current stream: HIP events around all `replays` replays (the mean), or
+    with `median`, around each replay and the median of those."""
     import torch
 
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
+    if median:
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+        marks[0].record()
+        for index in range(replays):
+            graph.replay()
+            marks[index + 1].record()
+        torch.cuda.synchronize()
+        times = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(replays))
+        return times[len(times) // 2] / 1e3
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(replays):
@@ -135,6 +150,20 @@ def time_graph(graph, replays: int, warmup: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3 / replays
+
+
+def copy_bandwidth(device, stream, size: int = 1 << 30) -> dict:
+    """Device-to-device copy of `size` bytes (torch's copy kernel), 4 copies per HIP graph, median of 20
+    replays; bandwidth counts the bytes read plus the bytes written."""
+    import torch
+
+    src = torch.empty(size, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    graph = graph_of(lambda: [dst.copy_(src) for _ in range(4)], stream)
+    seconds = time_graph(graph, 20, 2, median=True) / 4
+    del src, dst
+    return {"GBps": round(2 * size / seconds / 1e9, 1), "bytes_moved": 2 * size, "us": round(seconds * 1e6, 2)}
 
 
 def read_ceiling(matrices, stream) -> dict:
@@ -156,7 +185,7 @@ def read_ceiling(matrices, stream) -> dict:
             runtime.check(lib.ivonar_stream_read(stream_id, runtime.pointer(tensor), size, runtime.pointer(sink)),
                           "ivonar_stream_read")
 
-    seconds = time_graph(graph_of(run, stream), 10, 2)
+    seconds = time_graph(graph_of(run, stream), 20, 2, median=True)
     return {"GBps": round(total / seconds / 1e9, 1), "bytes": total,
             "kernel": "ivonar_stream_read (16-byte loads, 4 in flight per thread, 1024 blocks)"}
 
@@ -185,10 +214,9 @@ def device_copies(layer, device, copies: int):
     return mats
 
 
-def measure_traffic(calls: int = 8) -> dict:
-    """HBM bytes per GEMV dispatch from two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over
-    the GEMV probe, each scaled by what the counter reads for the probe's 512 MiB device copy.
-    Runs as child processes before this process touches the GPU."""
+def counter_pass(counters: list[str], probe: str, calls: int) -> list[dict] | str:
+    """One rocprofv3 counter pass over `bench.py --probe <probe>` as a child process (this process has not
+    touched the GPU yet): the per-dispatch rows of its counter CSV, or an error string."""
     import csv
     import shutil
     import subprocess
@@ -196,38 +224,50 @@ def measure_traffic(calls: int = 8) -> dict:
 
     tool = shutil.which("rocprofv3")
     if tool is None:
-        return {"error": "rocprofv3 not found"}
+        return "rocprofv3 not found"
+    out = tempfile.mkdtemp(prefix="ivonar_pmc_", dir="/tmp")
+    command = [tool, "--pmc", *counters, "--output-format", "csv", "-d", out, "-o", "pmc", "--",
+               sys.executable, str(ROOT / "bench.py"), "--probe", probe, "--probe-calls", str(calls)]
+    print(f"bench: counter pass {' '.join(counters)} over {probe}", file=sys.stderr, flush=True)
+    try:
+        done = subprocess.run(command, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, timeout=240,
+                              stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    except subprocess.TimeoutExpired:
+        shutil.rmtree(out, ignore_errors=True)
+        return f"{counters} pass timed out"
+    files = sorted(Path(out).rglob("*counter_collection.csv"))
+    if not files:
+        shutil.rmtree(out, ignore_errors=True)
+        return f"{counters} pass exited {done.returncode} without a counter file: {done.stdout[-300:]}"
+    dispatches: dict[int, dict] = {}
+    with open(files[0]) as handle:
+        for row in csv.DictReader(handle):
+            entry = dispatches.setdefault(int(row["Dispatch_Id"]), {"kernel": row["Kernel_Name"],
+                                                                   "grid": int(row["Grid_Size"])})
+            entry[row["Counter_Name"]] = entry.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    shutil.rmtree(out, ignore_errors=True)
+    return [dispatches[key] for key in sorted(dispatches)]
+
+
+def measure_traffic(calls: int = 8) -> dict:
+    """HBM bytes per GEMV dispatch from two counter passes (FETCH_SIZE, then WRITE_SIZE) over the GEMV
+    probe, each scaled by what the counter reads for the probe's 512 MiB device copy."""
     readings: dict[str, dict] = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        out = tempfile.mkdtemp(prefix="ivonar_pmc_", dir="/tmp")
-        command = [tool, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "pmc", "--",
-                   sys.executable, str(ROOT / "bench.py"), "--probe", "gemv-stress", "--probe-calls", str(calls)]
-        print(f"bench: counter pass {counter}", file=sys.stderr, flush=True)
-        try:
-            done = subprocess.run(command, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, timeout=240,
-                                  stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-        except subprocess.TimeoutExpired:
-            return {"error": f"{counter} pass timed out"}
-        files = sorted(Path(out).rglob("*counter_collection.csv"))
-        if done.returncode != 0 and not files:
-            return {"error": f"{counter} pass exited {done.returncode}: {done.stdout[-300:]}"}
-        if not files:
-            return {"error": f"{counter} pass wrote no counter file"}
+        rows = counter_pass([counter], "gemv-stress", calls)
+        if isinstance(rows, str):
+            return {"error": rows}
         gemv, other = {}, []
-        with open(files[0]) as handle:
-            for row in csv.DictReader(handle):
-                if row["Counter_Name"] != counter:
-                    continue
-                value = float(row["Counter_Value"])
-                if "gemv_kernel" in row["Kernel_Name"]:
-                    gemv.setdefault(int(row["Grid_Size"]), []).append(value)
-                else:
-                    other.append(value)
-        shutil.rmtree(out, ignore_errors=True)
+        for row in rows:
+            if counter not in row:
+                continue
+            if "gemv_kernel" in row["kernel"]:
+                gemv.setdefault(row["grid"], []).append(row[counter])
+            else:
+                other.append(row[counter])
         if not gemv or not other:
             return {"error": f"{counter} pass found no GEMV or copy dispatch"}
-        copy_kib = max(other)
-        readings[counter] = {"factor": (512 * 1024) / copy_kib,
+        readings[counter] = {"factor": (512 * 1024) / max(other),
                              "per_grid": {grid: sum(v) / len(v) for grid, v in gemv.items()}}
     fetch, write = readings["FETCH_SIZE"], readings["WRITE_SIZE"]
     per_launch = [fetch["per_grid"][grid] * fetch["factor"] * 1024 + write["per_grid"].get(grid, 0.0) * write["factor"] * 1024
@@ -235,6 +275,32 @@ def measure_traffic(calls: int = 8) -> dict:
     return {"bytes_per_launch": sum(per_launch) / len(per_launch),
             "fetch_factor": round(fetch["factor"], 4), "write_factor": round(write["factor"], 4),
             "per_launch": [round(v) for v in per_launch]}
+
+
+def measure_mfma(calls: int = 16, cus: int = 256) -> dict:
+    """MFMA-busy share of the token GEMM from one counter pass over the GEMM probe: per dispatch,
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the expression of rocprofv3's MfmaUtil, and the
+    int8 ops the MFMA unit counted (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512) against 2*M*N*K."""
+    counters = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_I8", "GRBM_GUI_ACTIVE"]
+    rows = counter_pass(counters, "gemm-prefill", calls)
+    if isinstance(rows, str):
+        return {"error": rows}
+    gemm = [row for row in rows if ("gemm_kernel" in row["kernel"] or "skinny_kernel" in row["kernel"])
+            and all(c in row for c in counters)]
+    cases = [(k, n, m) for k, n in PROBE_GEMM_SHAPES for m in PROBE_GEMM_M]
+    if len(gemm) != len(cases) * calls:
+        return {"error": f"expected {len(cases) * calls} GEMM dispatches, found {len(gemm)}"}
+    table = {}
+    for index, (k, n, m) in enumerate(cases):
+        chunk = gemm[index * calls:(index + 1) * calls]
+        busy = sum(r["SQ_VALU_MFMA_BUSY_CYCLES"] for r in chunk) / calls
+        active = sum(r["GRBM_GUI_ACTIVE"] for r in chunk) / calls
+        mops = sum(r["SQ_INSTS_VALU_MFMA_MOPS_I8"] for r in chunk) / calls
+        table[f"{k}x{n}_M{m}"] = {"mfma_busy_share": round(busy / (active * 4 * cus), 4),
+                                  "mfma_ops_counted": int(mops * 512), "ops_algorithmic": 2 * m * n * k,
+                                  "kernel": chunk[0]["kernel"].split("(")[0]}
+    return {"by_case": table, "simds": 4 * cus,
+            "note": "GRBM_GUI_ACTIVE counts the whole dispatch, launch and drain included"}
 
 
 def m_sweep(device, stream) -> dict:
@@ -289,6 +355,7 @@ def main() -> None:
     from ivonar_amd import ops, runtime, synthetic
 
     traffic = None if args.no_traffic else measure_traffic()
+    mfma = None if args.no_traffic else measure_mfma()
     device = torch.device("cuda", 0)
     runtime.initialise(0)
     stream = torch.cuda.Stream()
@@ -329,7 +396,7 @@ def main() -> None:
                 ops.gemv_prequant(matrices[shape][copy], q8, xsum, sx, out=outputs[shape])
 
         g = graph_of(prequant, stream)
-        t = time_graph(g, max(1, args.steps // ROTATING_COPIES), 2) / ROTATING_COPIES
+        t = time_graph(g, max(20, args.steps // ROTATING_COPIES), 2, median=True) / ROTATING_COPIES
         b = gemv_bytes(1, layer.rows, layer.in_features)
         kernel[f"{layer.in_features}x{layer.rows}"] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
     # the same shapes through the K-split MFMA kernel (gemm_tile_store with one token)
@@ -351,6 +418,7 @@ def main() -> None:
     kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
     achieved = kernel_bytes / kernel_seconds / 1e9
     ceiling = read_ceiling(matrices, stream)
+    copy = copy_bandwidth(device, stream)
 
     # ---- single linear K=1024 -> N=4096 (launch-latency bound) ------------------------------
     layer0, x0 = synthetic.single_linear(seed=0)
@@ -385,9 +453,12 @@ def main() -> None:
                                   "one_launch_TOPS": round(ops_count / t_one / 1e12, 2)}
         prefill[f"{k}x{layer.rows}"] = shape
     results["prefill_gemm"] = prefill
+    results["prefill_gemm_counters"] = mfma
 
-    # ---- decoder-shaped stack: greedy decode tok/s -------------------------------------------
+    # ---- decoder-shaped stack: greedy decode tok/s, and the device sampler -------------------------
     results["decode_stack"] = decode_stack(device)
+    results["decode_stack_sampled"] = decode_stack(device, sampling=(0.8, 40, 1.1))
+    results["sampler"] = sampler_timing(device, stream)
     results["m_sweep"] = m_sweep(device, stream)
 
     # ---- CPU baseline on a bounded sample -------------------------------------------------------
@@ -425,6 +496,10 @@ def main() -> None:
             "kernel": "gemv_kernel (pre-quantized activations)",
             "read_ceiling": ceiling,
             "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 4),
+            "copy_bandwidth": copy,
+            "frac_of_copy_bandwidth": round(achieved / copy["GBps"], 4),
+            "timing": "median of >= 20 HIP-graph replays of 8 calls (one per rotating copy), events on the "
+                      "launch stream",
             "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)} for k, v in kernel.items()},
         },
         "cpu_baseline": cpu,
@@ -433,10 +508,11 @@ def main() -> None:
     print(json.dumps(line))
 
 
-def decode_stack(device, generated: int = 256, repeats: int = 3):
-    """Greedy decode on the 24-layer d=1024 stack (vocab 32000, 36-token prompt): prefill in 32-token
-    tiles, then `generated` tokens in 16-step HIP-graph bursts with one token read-back per burst.
-    tok/s counts the decode steps only; the wall clock includes the read-backs."""
+def decode_stack(device, generated: int = 256, repeats: int = 3, sampling=None):
+    """Decode on the 24-layer d=1024 stack (vocab 32000, 36-token prompt): prefill in 32-token tiles,
+    then `generated` tokens in 16-step HIP-graph bursts with one token read-back per burst.  Greedy, or
+    with `sampling` = (temperature, top_k, repetition penalty) drawn by the device sampler.  tok/s counts
+    the decode steps only; the wall clock includes the read-backs."""
     import hashlib
 
     import torch
@@ -445,13 +521,17 @@ def decode_stack(device, generated: int = 256, repeats: int = 3):
     from ivonar_amd.synthetic import StackConfig, decoder_stack, prompt_ids
 
     config = StackConfig()
-    decoder = StackDecoder(decoder_stack(config, seed=1), device, burst=16)
+    decoder = StackDecoder(decoder_stack(config, seed=1), device, burst=16, sampling=sampling is not None)
     prompt = prompt_ids(config.vocab, 36, seed=1)
+    if sampling is not None:
+        decoder.configure_sampling(*sampling)
     decoder.prefill(prompt)
     decoder.capture()
     tokens = decoder.generate(prompt, generated)  # warm-up, and the tokens reported
     prefill_times, decode_times = [], []
     for _ in range(repeats):
+        if sampling is not None:
+            decoder.configure_sampling(*sampling)
         torch.cuda.synchronize()
         start = time.perf_counter()
         decoder.prefill(prompt)
@@ -462,9 +542,13 @@ def decode_stack(device, generated: int = 256, repeats: int = 3):
         end = time.perf_counter()
         prefill_times.append(middle - start)
         decode_times.append(end - middle)
-        if again[:-1] != tokens[1:]:
+        if sampling is None and again[:-1] != tokens[1:]:
             raise RuntimeError("greedy decoding is not deterministic across runs")
     best = min(decode_times)
+    if sampling is not None:
+        return {"tok_per_s": round(generated / best, 1), "ms_per_token": round(best / generated * 1e3, 4),
+                "rule": {"temperature": sampling[0], "top_k": sampling[1], "repetition_penalty": sampling[2]},
+                "tokens_first8": tokens[:8]}
     return {
         "tok_per_s": round(generated / best, 1),
         "ms_per_token": round(best / generated * 1e3, 4),
@@ -477,6 +561,28 @@ def decode_stack(device, generated: int = 256, repeats: int = 3):
     }
 
 
+def sampler_timing(device, stream, vocab: int = 32000) -> dict:
+    """One draw of the device sampler (uniform_(), logit_bounds, sample_token) over 32000 logits,
+    64 draws per HIP graph, for a few top-k values."""
+    import torch
+
+    from ivonar_amd.sampling import DeviceSampler
+
+    sampler = DeviceSampler(vocab, device, max_top_k=1024)
+    logits = torch.randn(vocab, device=device) * 3
+    table = {}
+    for top_k in (1, 40, 256, 1024):
+        sampler.configure_sampling(temperature=0.8, top_k=top_k, repetition_penalty=1.1)
+
+        def draw():
+            sampler.uniform.uniform_()
+            sampler.launch(logits)
+
+        table[str(top_k)] = round(time_calls(draw, stream, 64, 10) * 1e6, 3)
+    return {"us_per_draw_by_top_k": table, "vocab": vocab,
+            "note": "uniform_ + logit_bounds + sample_token, seen cleared per top_k only"}
+
+
 def decoder_bytes(config) -> int:
     """Packed weights and fp16 scales streamed per decode step (all layers and the head)."""
     h, d = config.hidden, config.dense
@@ -485,38 +591,75 @@ def decoder_bytes(config) -> int:
     return config.layers * per_layer + config.vocab * ((h + 3) // 4) + 2 * config.vocab * ((h + 127) // 128)
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def physical_cores(allowed: set[int]) -> int:
+    """Distinct (package, core) pairs among the CPUs this process may run on."""
+    cores = set()
+    try:
+        text = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return len(allowed)
+    for block in text.split("\n\n"):
+        fields = dict(line.split(":", 1) for line in block.splitlines() if ":" in line)
+        fields = {k.strip(): v.strip() for k, v in fields.items()}
+        if "processor" in fields and int(fields["processor"]) in allowed:
+            cores.add((fields.get("physical id", "0"), fields.get("core id", fields["processor"])))
+    return len(cores) or len(allowed)
+
+
 def cpu_baseline(stress, budget_seconds: float):
-    """The numba GEMV restated in C++/OpenMP, timed on this host on the stress shapes."""
+    """The numba GEMV restated in C++/OpenMP, timed on this host on the stress shapes: with one thread per
+    physical core of this process's CPU set (at most 16), then with one thread for a quarter of the budget."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
     import ternary_oracle as T
 
     cb = T.CpuBaseline()
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    threads = max(1, min(threads, 16))
-    cb.set_threads(threads)
-    total_bytes, total_seconds, calls = 0, 0.0, 0
+    allowed = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else set(range(os.cpu_count() or 1))
+    threads = max(1, min(physical_cores(allowed), 16))
     prepared = []
     for layer, x in stress:
         planes = cb.planes_of(layer.packed, layer.in_features)
         scales = layer.scales.astype(np.float32)
         prepared.append((planes, scales, np.ascontiguousarray(x[0]), np.zeros(layer.rows, np.float32),
                          cb.workspace(layer.in_features), layer))
-    deadline = time.perf_counter() + budget_seconds
-    while time.perf_counter() < deadline:
-        for planes, scales, x, out, ws, layer in prepared:
-            start = time.perf_counter()
-            cb.gemv(x, planes, scales, None, out, ws=ws)
-            total_seconds += time.perf_counter() - start
-            total_bytes += gemv_bytes(1, layer.rows, layer.in_features)
-            calls += 1
+
+    def timed(count: int, budget: float) -> tuple[float, int]:
+        cb.set_threads(count)
+        total_bytes, total_seconds, calls = 0, 0.0, 0
+        deadline = time.perf_counter() + budget
+        while time.perf_counter() < deadline:
+            for planes, scales, x, out, ws, layer in prepared:
+                start = time.perf_counter()
+                cb.gemv(x, planes, scales, None, out, ws=ws)
+                total_seconds += time.perf_counter() - start
+                total_bytes += gemv_bytes(1, layer.rows, layer.in_features)
+                calls += 1
+        return total_bytes / total_seconds / 1e9, calls
+
+    value, calls = timed(threads, budget_seconds)
+    single, single_calls = timed(1, budget_seconds / 4)
     return {
-        "value": round(total_bytes / total_seconds / 1e9, 3),
+        "value": round(value, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{calls} GEMV calls over both stress shapes (~{budget_seconds:.0f} s), planes layout, OpenMP",
+        "sample": f"{calls} GEMV calls over both stress shapes (~{budget_seconds:.0f} s), planes layout, OpenMP "
+                  f"with {threads} threads",
+        "value_1_thread": round(single, 3),
+        "sample_1_thread": f"{single_calls} calls (~{budget_seconds / 4:.0f} s)",
+        "cpu_model": cpu_model(),
+        "cpus_allowed": len(allowed),
     }
 
 

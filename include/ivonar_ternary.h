@@ -48,8 +48,9 @@ hipError_t ivonar_init(int device);
 /* Process-wide values the reference passes as -D defines to NVRTC
  * (kernel_decoder.py:215, ternary.cu:1-46): "HEAD_DIM" (ATTN prologue head
  * width, default 64), "TILE" (token rows of quantize_tile_*, default 32),
- * "MAX_CHUNKS" (caller q8 capacity, default 70).  Unknown names return
- * hipErrorInvalidValue. */
+ * "MAX_CHUNKS" (caller q8 capacity, default 70), "MAX_TOPK" (largest top-k
+ * of sample_token, 1..1024, default 256).  Unknown names and out-of-range
+ * values return hipErrorInvalidValue. */
 hipError_t ivonar_define(const char* name, int value);
 
 const char* ivonar_error_string(hipError_t status);
@@ -161,6 +162,24 @@ hipError_t gather_token(hipStream_t stream, const float* tile, float* output, in
  * counterpart as a kernel; the reference's greedy sampler is top_k = 1 of
  * sample_token, ternary.cu:1099-1337). */
 hipError_t ivonar_argmax(hipStream_t stream, const float* values, int n, int64_t* out);
+
+/* --------------------------------------------------------------- sampler
+ * The reference's on-device sampler (ternary.cu:1083-1092 and :1098-1337,
+ * launched by kernel_decoder.py:619-634), argument order kept.  Rule:
+ * score = logits[i] * (1 / *temperature), multiplied by *inverse_penalty
+ * (score > 0) or *penalty (score <= 0) where seen[i]; the k = clamp(*top_k,
+ * 1, min(MAX_TOPK, vocab)) largest scores (ties at the cut: lowest index);
+ * softmax over them; inverse-CDF draw with *uniform in [0, 1) over the picks
+ * in ascending index order.  token[0] and history[0] (if not NULL) receive
+ * the draw and seen[token] is set to 1.  vocab <= 262144.  bounds holds
+ * ceil(vocab / 64) floats (the largest score of each 64-entry group) and is
+ * written by logit_bounds, read by sample_token; the two run back to back on
+ * one stream with the same logits, seen and rule. */
+hipError_t logit_bounds(hipStream_t stream, const float* logits, const float* temperature, const float* penalty,
+                        const float* inverse_penalty, const uint8_t* seen, float* bounds, int vocab);
+hipError_t sample_token(hipStream_t stream, const float* logits, const float* bounds, const float* temperature,
+                        const float* penalty, const float* inverse_penalty, uint8_t* seen, const int64_t* top_k,
+                        const float* uniform, int64_t* token, int64_t* history, int vocab);
 
 /* Measurement export (no reference counterpart): reads `bytes` (a multiple of
  * 16, 16-byte aligned) of `data` with 16-byte loads at full occupancy and

@@ -171,6 +171,7 @@ hipError_t ivonar_define(const char* name, int value) {
   if (strcmp(name, "HEAD_DIM") == 0) defines().head_dim = value;
   else if (strcmp(name, "TILE") == 0) defines().tile = value;
   else if (strcmp(name, "MAX_CHUNKS") == 0) defines().max_chunks = value;
+  else if (strcmp(name, "MAX_TOPK") == 0 && value <= kMaxTopK) defines().max_topk = value;
   else return hipErrorInvalidValue;
   return hipSuccess;
 }
@@ -340,6 +341,24 @@ hipError_t gather_token(hipStream_t stream, const float* tile, float* output, in
 hipError_t ivonar_argmax(hipStream_t stream, const float* values, int n, int64_t* out) {
   if (values == nullptr || out == nullptr || n <= 0) return hipErrorInvalidValue;
   return launch_argmax(stream, values, n, out);
+}
+
+hipError_t logit_bounds(hipStream_t stream, const float* logits, const float* temperature, const float* penalty,
+                        const float* inverse_penalty, const uint8_t* seen, float* bounds, int vocab) {
+  if (logits == nullptr || temperature == nullptr || penalty == nullptr || inverse_penalty == nullptr ||
+      seen == nullptr || bounds == nullptr)
+    return hipErrorInvalidValue;
+  return launch_logit_bounds(stream, logits, temperature, penalty, inverse_penalty, seen, bounds, vocab);
+}
+
+hipError_t sample_token(hipStream_t stream, const float* logits, const float* bounds, const float* temperature,
+                        const float* penalty, const float* inverse_penalty, uint8_t* seen, const int64_t* top_k,
+                        const float* uniform, int64_t* token, int64_t* history, int vocab) {
+  if (logits == nullptr || bounds == nullptr || temperature == nullptr || penalty == nullptr ||
+      inverse_penalty == nullptr || seen == nullptr || top_k == nullptr || uniform == nullptr || token == nullptr)
+    return hipErrorInvalidValue;
+  return launch_sample_token(stream, logits, bounds, temperature, penalty, inverse_penalty, seen, top_k, uniform, token,
+                             history, vocab);
 }
 
 int ivonar_stream_read_sink_words(void) { return stream_read_sink_words(); }

@@ -9,11 +9,15 @@ namespace ivo {
 // Process-wide values the reference passes as compile-time defines
 // (kernel_decoder.py:215): HEAD_DIM for the ATTN prologue, TILE for the
 // token count of the quantize_tile_* entry points, MAX_CHUNKS (capacity of
-// the caller's q8 buffers, used only for argument checks).
+// the caller's q8 buffers, used only for argument checks), MAX_TOPK (largest
+// top-k of the sampler, ternary.cu:8).
+constexpr int kMaxTopK = 1024;
+constexpr int kMaxSampleVocab = 1 << 18;
 struct Defines {
   int head_dim = 64;
   int tile = 32;
   int max_chunks = 70;
+  int max_topk = 256;
 };
 Defines& defines();
 
@@ -100,6 +104,13 @@ hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const 
                         const uint16_t* scales, float* output, int n, int row_bytes, int groups);
 hipError_t launch_gather(hipStream_t stream, const float* tile, float* output, int n, const int64_t* valid);
 hipError_t launch_argmax(hipStream_t stream, const float* values, int n, int64_t* out);
+hipError_t launch_logit_bounds(hipStream_t stream, const float* logits, const float* temperature,
+                               const float* penalty, const float* inverse_penalty, const uint8_t* seen,
+                               float* bounds, int vocab);
+hipError_t launch_sample_token(hipStream_t stream, const float* logits, const float* bounds, const float* temperature,
+                               const float* penalty, const float* inverse_penalty, uint8_t* seen,
+                               const int64_t* top_k, const float* uniform, int64_t* token, int64_t* history,
+                               int vocab);
 // Streaming-read reference (measurement): reads bytes/16 16-byte words of data;
 // sink holds stream_read_sink_words() uint32 and is written only in theory.
 int stream_read_sink_words();

@@ -15,13 +15,15 @@ decode step (``kernel_decoder.py:233-269``)::
       gemv_norm_silu_pair   gate/up (interleaved) residual -> ffn_mid    (RMSNorm prologue)
       gemv_plain_residual   down                  ffn_mid -> residual +=
     gemv_norm_store                               residual -> logits (tied token matrix, RMSNorm fused)
-    ivonar_argmax                                 logits -> next token (greedy, top_k = 1)
+    ivonar_argmax                                 logits -> next token (greedy)
+      or, with sampling: uniform_(), logit_bounds, sample_token (kernel_decoder.py:619-681)
 
 prefill tile (``kernel_decoder.py:303-368``): ``embed_tile``, per layer
 ``quantize_tile_norm`` + ``gemm_tile_store``, ``quantize_tile_plain`` +
 ``gemm_tile_residual``, ``quantize_tile_norm`` + ``gemm_tile_silu_pair``,
-``quantize_tile_plain`` + ``gemm_tile_residual``, then ``gather_token`` and
-the head.
+``quantize_tile_plain`` + ``gemm_tile_residual``, then ``gather_token``; the
+head and the first token's selection run once, after the last tile (the
+reference runs its head in every tile and samples after the prompt).
 
 The mixers (recurrent scan, latent attention) are not part of this path: the
 output projection reads the V third of the entry projection's output instead
@@ -42,6 +44,7 @@ from . import runtime
 from .matrix import Matrix, _lanes_for
 from .quantization import TernaryLinear
 from .runtime import KernelError, Launch, float32, int32, pointer
+from .sampling import DeviceSampler
 from .synthetic import LinearStackWeights
 
 TILE = 32
@@ -67,8 +70,22 @@ class _LayerOps:
     ffn_norm: torch.Tensor
 
 
+class _TorchOp:
+    """A torch call in a launch list (runs on torch's current stream, which is the launch stream)."""
+
+    __slots__ = ("function",)
+
+    def __init__(self, function) -> None:
+        self.function = function
+
+    def __call__(self, stream: int) -> None:
+        del stream
+        self.function()
+
+
 class StackDecoder:
-    def __init__(self, weights: LinearStackWeights, device: str | torch.device = "cuda", burst: int = BURST) -> None:
+    def __init__(self, weights: LinearStackWeights, device: str | torch.device = "cuda", burst: int = BURST,
+                 sampling: bool = False, max_top_k: int = 256) -> None:
         device = torch.device(device)
         if device.type != "cuda":
             raise KernelError("the ternary decoder needs a ROCm device")
@@ -100,6 +117,10 @@ class StackDecoder:
         self.q8sum = torch.zeros(max_chunks, dtype=torch.int32, device=device)
         self.q8scale = torch.zeros(1, **f32)
         self.history = torch.zeros(self.burst, dtype=torch.int64, device=device)
+        # sampling state (kernel_decoder.py:213-224): one uniform per ring slot, drawn inside the step
+        self.sampler = DeviceSampler(vocab, device, max_top_k) if sampling else None
+        self.uniforms = torch.zeros(self.burst, **f32)
+        self.drawn_uniforms: list[float] = []  # with sampling: the uniform of every token advance_many returned
         # prefill tile buffers (kernel_decoder.py:308-319)
         self.tile_tokens = torch.zeros(TILE, dtype=torch.int64, device=device)
         self.tile_valid = torch.zeros(1, dtype=torch.int64, device=device)
@@ -115,6 +136,7 @@ class StackDecoder:
                                  eps=config.eps)]
         self._steps = [self._build_step(slot) for slot in range(self.burst)]
         self._tile = self._build_tile()
+        self._first = self._head + self._select(self.burst - 1)  # after the last tile
         self._graph: torch.cuda.CUDAGraph | None = None
         self.position = 0
 
@@ -161,9 +183,32 @@ class StackDecoder:
             name += "_wide"
         return Launch(self.module.kernel(name), (matrix.grid, 1, 1), (THREADS, 1, 1), args)
 
-    def _argmax(self, slot: int) -> Launch:
-        args = [pointer(self.logits), int32(self.config.vocab), pointer(self.history[slot:slot + 1])]
-        return Launch(self.module.kernel("ivonar_argmax"), (1, 1, 1), (1024, 1, 1), args)
+    def _select(self, slot: int) -> list:
+        """The next token into ring slot `slot`: greedy argmax, or a draw of the device sampler with a
+        fresh uniform (kernel_decoder.py:669-681)."""
+        history = self.history[slot:slot + 1]
+        vocab = self.config.vocab
+        sampler = self.sampler
+        if sampler is None:
+            args = [pointer(self.logits), int32(vocab), pointer(history)]
+            return [Launch(self.module.kernel("ivonar_argmax"), (1, 1, 1), (1024, 1, 1), args)]
+        uniform = self.uniforms[slot:slot + 1]
+        groups = (vocab + 63) // 64
+        bounds_args = [pointer(self.logits), pointer(sampler.temperature), pointer(sampler.penalty),
+                       pointer(sampler.inverse_penalty), pointer(sampler.seen), pointer(sampler.bounds), int32(vocab)]
+        sample_args = [pointer(self.logits), pointer(sampler.bounds), pointer(sampler.temperature),
+                       pointer(sampler.penalty), pointer(sampler.inverse_penalty), pointer(sampler.seen),
+                       pointer(sampler.top_k), pointer(uniform), pointer(sampler.token), pointer(history), int32(vocab)]
+        return [_TorchOp(uniform.uniform_),
+                Launch(self.module.kernel("logit_bounds"), (groups, 1, 1), (64, 1, 1), bounds_args),
+                Launch(self.module.kernel("sample_token"), (1, 1, 1), (1024, 1, 1), sample_args)]
+
+    def configure_sampling(self, temperature: float, top_k: int, repetition_penalty: float = 1.0,
+                           penalized_ids=()) -> None:
+        """decoder.py:334-361 (the decoder must have been created with sampling=True)."""
+        if self.sampler is None:
+            raise RuntimeError("this decoder was created without sampling")
+        self.sampler.configure_sampling(temperature, top_k, repetition_penalty, penalized_ids)
 
     def _build_step(self, slot: int) -> list[Launch]:
         """One greedy decode step reading the token in slot-1 of the ring and writing slot."""
@@ -183,11 +228,11 @@ class StackDecoder:
                                        self.ffn_mid, eps=config.eps))
             launches.append(self._gemv("gemv_plain_residual", ops.down, self.ffn_mid, None, self.residual))
         launches.extend(self._head)
-        launches.append(self._argmax(slot))
+        launches.extend(self._select(slot))
         return launches
 
     def _build_tile(self) -> list[Launch]:
-        """One 32-token prefill tile ending in the head and the first greedy token (slot burst-1)."""
+        """One 32-token prefill tile, ending with its last valid token's residual in ``self.residual``."""
         config = self.config
         hidden, dense, qkv = config.hidden, config.dense, config.qkv
         token = self.token_matrix
@@ -212,8 +257,6 @@ class StackDecoder:
                                (THREADS, 1, 1),
                                [pointer(self.residual_tile), pointer(self.residual), int32(hidden),
                                 pointer(self.tile_valid)]))
-        launches.extend(self._head)
-        launches.append(self._argmax(self.burst - 1))
         return launches
 
     # ------------------------------------------------------------------ running
@@ -225,8 +268,9 @@ class StackDecoder:
 
     @torch.no_grad()
     def prefill(self, input_ids) -> torch.Tensor:
-        """Runs the prompt in 32-token tiles (kernel_decoder.py:456-479); the first greedy token is left in
-        the ring's last slot and the logits of the prompt's last token in ``self.logits``."""
+        """Runs the prompt in 32-token tiles (kernel_decoder.py:456-479), then the head on its last token:
+        the logits are left in ``self.logits`` and the first token (greedy, or drawn by the sampler) in
+        the ring's last slot."""
         ids = torch.as_tensor(input_ids, dtype=torch.int64).reshape(-1)
         length = int(ids.numel())
         if length == 0:
@@ -241,6 +285,7 @@ class StackDecoder:
             self.tile_tokens[:count].copy_(chunk)
             self.tile_valid.fill_(count)
             self._run(self._tile)
+        self._run(self._first)
         self.position = 0
         return self.logits
 
@@ -252,10 +297,13 @@ class StackDecoder:
 
     @torch.no_grad()
     def capture(self) -> bool:
-        """Records one burst of decode steps into a HIP graph (kernel_decoder.py:694-719)."""
+        """Records one burst of decode steps into a HIP graph (kernel_decoder.py:694-719).  With sampling,
+        the uniforms are drawn inside the graph, fresh on every replay; the sampler's `seen` is restored
+        after the warm-up and the capture, as the ring is."""
         if self.position % self.burst != 0:
             raise KernelError("capture at a burst boundary")
         saved = self.history.clone()
+        seen = None if self.sampler is None else self.sampler.seen.clone()
         stream = torch.cuda.Stream(device=self.device)
         stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(stream):
@@ -264,12 +312,16 @@ class StackDecoder:
         torch.cuda.current_stream(self.device).wait_stream(stream)
         torch.cuda.synchronize(self.device)
         self.history.copy_(saved)
+        if seen is not None:
+            self.sampler.seen.copy_(seen)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             for slot in range(self.burst):
                 self._run(self._steps[slot])
         torch.cuda.synchronize(self.device)
         self.history.copy_(saved)
+        if seen is not None:
+            self.sampler.seen.copy_(seen)
         self._graph = graph
         return True
 
@@ -278,19 +330,25 @@ class StackDecoder:
         """``count`` greedy tokens after the last one produced: whole bursts replay the graph with one
         read-back each (kernel_decoder.py:722-735); the rest run eagerly."""
         tokens: list[int] = []
+        sampling = self.sampler is not None
         while count - len(tokens) >= self.burst and self._graph is not None and self.position % self.burst == 0:
             self._graph.replay()
             self.position += self.burst
             tokens.extend(self.history.tolist())
+            if sampling:
+                self.drawn_uniforms.extend(self.uniforms.tolist())
         while len(tokens) < count:
             slot = self.position % self.burst
             self.step()
             tokens.append(int(self.history[slot]))
+            if sampling:
+                self.drawn_uniforms.append(float(self.uniforms[slot]))
         return tokens
 
     @torch.no_grad()
     def generate(self, prompt_ids, count: int) -> list[int]:
-        """Greedy decoding: the first token from the prompt's last position, then count-1 steps."""
+        """The first token from the prompt's last position, then count-1 steps (greedy, or drawn by the
+        device sampler as configured)."""
         self.prefill(prompt_ids)
         first = int(self.history[self.burst - 1])
         return [first] + self.advance_many(count - 1)

@@ -68,6 +68,8 @@ SIGNATURES: dict[str, list] = {
     "gemv_group_partials": [_P, _P, _P, _I, _I, _I, _I, _P],
     "ivonar_quantize_rows": [_I, _P, _I, _P, _I, _F, _I, _I, _P, _P, _P],
     "ivonar_argmax": [_P, _I, _P],
+    "logit_bounds": [_P, _P, _P, _P, _P, _P, _I],
+    "sample_token": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I],
     "ivonar_stream_read": [_P, ctypes.c_longlong, _P],
 }
 
@@ -198,7 +200,7 @@ class Module:
         return kernel
 
 
-_DEFINES = ("HEAD_DIM", "TILE", "MAX_CHUNKS")
+_DEFINES = ("HEAD_DIM", "TILE", "MAX_CHUNKS", "MAX_TOPK")
 
 
 def compile_module(
@@ -207,7 +209,7 @@ def compile_module(
     """Bind the prebuilt library for ``device`` and apply the reference's -D defines.
 
     ``source`` is accepted for signature compatibility and ignored.  HEAD_DIM,
-    TILE and MAX_CHUNKS are process-wide in this library (one decoder
+    TILE, MAX_CHUNKS and MAX_TOPK are process-wide in this library (one decoder
     configuration per process, as in the reference's single-flight engine).
     """
     del source, name

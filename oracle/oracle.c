@@ -452,3 +452,118 @@ int64_t orc_argmax(const float* x, int n) {
     if (x[i] > x[best]) best = i;
   return best;
 }
+
+/* ------------------------------------------------------------------ sampler
+ * The sampling rule of the reference's logit_bounds / sample_token
+ * (kernels/ternary.cu:984-1097 scores and bounds, :1098-1337 top-k, softmax
+ * and inverse-CDF draw; torch form decoder.py:324-333), with the picks in
+ * ascending index order and the fp32 CDF order of the HIP sampler:
+ * per 64 picks a Hillis-Steele inclusive scan, wave totals added in wave
+ * order.  Keys order floats as numbers with -NaN lowest and +NaN highest;
+ * equal keys at the top-k cut are taken lowest index first. */
+static inline uint32_t order_key(float v) {
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+static inline float key_value(uint32_t key) {
+  return as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+/* ternary.cu:990-996 */
+static inline float sample_score(const float* logits, const uint8_t* seen, int i, float inv_t, float pen,
+                                 float inv_pen) {
+  float s = logits[i] * inv_t;
+  if (seen[i]) s *= s > 0.0f ? inv_pen : pen;
+  return s;
+}
+
+/* ternary.cu:1083-1092: the largest score of each 64-entry group. */
+void orc_logit_bounds(const float* logits, float temperature, float penalty, float inverse_penalty,
+                      const uint8_t* seen, float* bounds, int vocab) {
+  const float inv_t = 1.0f / temperature;
+  const int groups = (vocab + 63) / 64;
+  for (int g = 0; g < groups; ++g) {
+    uint32_t best = 0u;
+    for (int i = g * 64; i < g * 64 + 64 && i < vocab; ++i) {
+      const uint32_t key = order_key(sample_score(logits, seen, i, inv_t, penalty, inverse_penalty));
+      if (key > best) best = key;
+    }
+    bounds[g] = key_value(best);
+  }
+}
+
+typedef struct {
+  uint32_t key;
+  int index;
+} keyed_t;
+
+static int by_rank(const void* a, const void* b) {
+  const keyed_t* x = (const keyed_t*)a;
+  const keyed_t* y = (const keyed_t*)b;
+  if (x->key != y->key) return x->key > y->key ? -1 : 1;
+  return x->index < y->index ? -1 : (x->index > y->index);
+}
+
+static int by_index(const void* a, const void* b) {
+  const keyed_t* x = (const keyed_t*)a;
+  const keyed_t* y = (const keyed_t*)b;
+  return x->index < y->index ? -1 : (x->index > y->index);
+}
+
+/* ternary.cu:1098-1337.  Returns the token and sets seen[token] = 1; picks
+ * (ascending index) and their CDF go to picks/cdf (k entries each) when not
+ * NULL, k to *count. */
+int64_t orc_sample_token(const float* logits, float temperature, float penalty, float inverse_penalty,
+                         uint8_t* seen, int64_t top_k, int max_topk, float uniform, int vocab, int* picks, float* cdf,
+                         int* count) {
+  const float inv_t = 1.0f / temperature;
+  int64_t limit = max_topk < vocab ? max_topk : vocab;
+  int64_t kk = top_k < limit ? top_k : limit;
+  const int k = (int)(kk < 1 ? 1 : kk);
+  keyed_t* all = (keyed_t*)malloc(sizeof(keyed_t) * (size_t)vocab);
+  for (int i = 0; i < vocab; ++i) {
+    all[i].key = order_key(sample_score(logits, seen, i, inv_t, penalty, inverse_penalty));
+    all[i].index = i;
+  }
+  qsort(all, (size_t)vocab, sizeof(keyed_t), by_rank);
+  const float peak = key_value(all[0].key);
+  qsort(all, (size_t)k, sizeof(keyed_t), by_index);
+  /* 1024 slots as in the one-block kernel; slots past k hold 0. */
+  float run[1024], wave_sum[16], c[1024];
+  for (int j = 0; j < 1024; ++j) run[j] = j < k ? orc_expf(key_value(all[j].key) - peak) : 0.0f;
+  for (int w = 0; w < 16; ++w) {
+    float* r = run + 64 * w;
+    for (int offset = 1; offset < 64; offset <<= 1) {
+      float old[64];
+      memcpy(old, r, sizeof(old));
+      for (int l = offset; l < 64; ++l) r[l] = old[l] + old[l - offset];
+    }
+    wave_sum[w] = r[63];
+  }
+  for (int j = 0; j < 1024; ++j) {
+    float carry = 0.0f;
+    for (int w = 0; w < j / 64; ++w) carry += wave_sum[w];
+    c[j] = carry + run[j];
+  }
+  const float total = c[k - 1];
+  const float target = fminf(uniform, 0.99999994f) * total;
+  int chosen = -1;
+  for (int j = 0; j < k; ++j) {
+    const float lower = j > 0 ? c[j - 1] : 0.0f;
+    if (lower <= target && target < c[j]) {
+      chosen = j;
+      break;
+    }
+  }
+  if (chosen < 0) chosen = k - 1;
+  const int token = all[chosen].index;
+  if (picks != NULL)
+    for (int j = 0; j < k; ++j) picks[j] = all[j].index;
+  if (cdf != NULL) memcpy(cdf, c, sizeof(float) * (size_t)k);
+  if (count != NULL) *count = k;
+  free(all);
+  seen[token] = 1;
+  return token;
+}

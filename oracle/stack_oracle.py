@@ -137,3 +137,25 @@ class StackOracle:
             if history is not None:
                 history.append(logits)
         return (tokens, history) if keep_logits else tokens
+
+    def generate_sampled(self, prompt, uniforms, temperature: float, top_k: int, repetition_penalty: float = 1.0,
+                         penalized_ids=(), max_top_k: int = 256):
+        """Tokens drawn by the sampling rule (decoder.py:324-361): token j uses uniforms[j]; the seen set
+        starts from penalized_ids and gains every drawn token."""
+        vocab = self.config.vocab
+        seen = np.zeros(vocab, dtype=np.uint8)
+        for token in penalized_ids:
+            if 0 <= int(token) < vocab:
+                seen[int(token)] = 1
+        effective = int(top_k) if 0 < int(top_k) <= max_top_k else max_top_k
+        penalty = np.float32(repetition_penalty)
+        inverse = np.float32(1.0 / float(repetition_penalty))
+        tokens = []
+        logits = self.prefill_logits(prompt)
+        for j, u in enumerate(uniforms):
+            if j:
+                logits = self.step_logits(tokens[-1])
+            token, _, _ = self.oracle.sample_token(logits, seen, np.float32(temperature), penalty, inverse,
+                                                   effective, max_top_k, np.float32(u))
+            tokens.append(token)
+        return tokens

@@ -181,6 +181,10 @@ class Oracle:
                                    c_int, c_int, c_int, c_int]
         lib.orc_argmax.argtypes = [c_void_p, c_int]
         lib.orc_argmax.restype = c_int64
+        lib.orc_logit_bounds.argtypes = [c_void_p, c_float, c_float, c_float, c_void_p, c_void_p, c_int]
+        lib.orc_sample_token.argtypes = [c_void_p, c_float, c_float, c_float, c_void_p, c_int64, c_int, c_float, c_int,
+                                         c_void_p, c_void_p, c_void_p]
+        lib.orc_sample_token.restype = c_int64
         self.lib = lib
 
     def expf(self, x: float) -> float:
@@ -297,6 +301,29 @@ class Oracle:
     def argmax(self, x: np.ndarray) -> int:
         x = np.ascontiguousarray(x, dtype=np.float32)
         return int(self.lib.orc_argmax(_ptr(x), x.shape[0]))
+
+    def logit_bounds(self, logits: np.ndarray, seen: np.ndarray, temperature: float, penalty: float,
+                     inverse_penalty: float) -> np.ndarray:
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        seen = np.ascontiguousarray(seen, dtype=np.uint8)
+        bounds = np.zeros((logits.shape[0] + 63) // 64, dtype=np.float32)
+        self.lib.orc_logit_bounds(_ptr(logits), temperature, penalty, inverse_penalty, _ptr(seen), _ptr(bounds),
+                                  logits.shape[0])
+        return bounds
+
+    def sample_token(self, logits: np.ndarray, seen: np.ndarray, temperature: float, penalty: float,
+                     inverse_penalty: float, top_k: int, max_topk: int, uniform: float):
+        """(token, picks in index order, their CDF); `seen` (uint8 numpy) gets seen[token] = 1."""
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        if seen.dtype != np.uint8 or not seen.flags.c_contiguous:
+            raise TypeError("seen must be a contiguous uint8 array (it is updated in place)")
+        picks = np.zeros(1024, dtype=np.int32)
+        cdf = np.zeros(1024, dtype=np.float32)
+        count = ctypes.c_int(0)
+        token = self.lib.orc_sample_token(_ptr(logits), temperature, penalty, inverse_penalty, _ptr(seen), int(top_k),
+                                          int(max_topk), uniform, logits.shape[0], _ptr(picks), _ptr(cdf),
+                                          ctypes.byref(count))
+        return int(token), picks[:count.value].copy(), cdf[:count.value].copy()
 
 
 class CpuBaseline:

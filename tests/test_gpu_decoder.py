@@ -92,3 +92,31 @@ def test_full_size_stack_greedy_tokens_are_identical(cuda):
     expected, logits = _oracle(weights).generate(prompt, 256, keep_logits=True)
     assert tokens == expected
     np.testing.assert_array_equal(last_logits, logits[-1])
+
+
+@pytest.mark.parametrize("name", ["narrow", "ragged"])
+def test_sampled_tokens_match_the_oracle(cuda, name):
+    """Sampling (temperature 0.8, top_k 40, repetition penalty 1.3, two penalized ids): the first token
+    after the prompt, two graph bursts and three eager steps, each drawn with the uniform the device
+    generated, against the oracle's draws with the same uniforms."""
+    import torch
+
+    from ivonar_amd.decoder import StackDecoder
+
+    weights = decoder_stack(CONFIGS[name], seed=6, keep_codes=True)
+    decoder = StackDecoder(weights, cuda, burst=8, sampling=True, max_top_k=64)
+    decoder.configure_sampling(temperature=0.8, top_k=40, repetition_penalty=1.3, penalized_ids=[3, 17, -1])
+    prompt = prompt_ids(decoder.config.vocab, 36, seed=3)
+    decoder.prefill(prompt)
+    uniforms = [float(decoder.uniforms[decoder.burst - 1])]
+    tokens = [int(decoder.history[decoder.burst - 1])]
+    decoder.capture()
+    decoder.drawn_uniforms.clear()
+    tokens += decoder.advance_many(2 * decoder.burst + 3)
+    uniforms += decoder.drawn_uniforms
+    torch.cuda.synchronize()
+    assert len(set(uniforms)) == len(uniforms)
+    expected = _oracle(weights).generate_sampled(prompt, uniforms, 0.8, 40, 1.3, [3, 17, -1], max_top_k=64)
+    assert tokens == expected
+    seen = np.flatnonzero(decoder.sampler.seen.cpu().numpy().reshape(-1))
+    assert set(seen.tolist()) == {3, 17} | set(tokens)

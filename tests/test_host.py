@@ -25,7 +25,7 @@ def test_library_exports_every_declared_entry_point():
 
     lib = runtime.library()
     declared = _declared_functions()
-    assert len(declared) >= 38
+    assert len(declared) >= 40
     missing = [name for name in declared if not hasattr(lib, name)]
     assert not missing, missing
 
@@ -36,7 +36,7 @@ def test_python_signatures_cover_the_launchable_entry_points():
     declared = set(_declared_functions())
     assert set(runtime.SIGNATURES) <= declared
     for name in declared:
-        if name.startswith(("gemv_", "gemm_tile_", "quantize_", "embed_", "gather_")):
+        if name.startswith(("gemv_", "gemm_tile_", "quantize_", "embed_", "gather_", "logit_", "sample_")):
             assert name in runtime.SIGNATURES, name
 
 
@@ -50,6 +50,7 @@ def test_reference_kernel_names_are_all_present():
                   "gather_token"]
     reference += [f"quantize_tile_{k}{w}" for k in ("plain", "norm", "attn") for w in ("", "_wide")]
     reference += [f"gemm_tile_{k}{w}" for k in ("store", "residual", "silu_pair") for w in ("", "_wide")]
+    reference += ["logit_bounds", "sample_token"]
     lib = runtime.library()
     assert all(hasattr(lib, name) for name in reference)
     assert all(name in runtime.SIGNATURES for name in reference)
@@ -63,12 +64,22 @@ def test_host_only_calls():
     assert lib.ivonar_define(b"NOT_A_DEFINE", 3) != 0
     assert lib.ivonar_define(b"TILE", 0) != 0
     assert lib.ivonar_define(b"TILE", 32) == 0
+    assert lib.ivonar_define(b"MAX_TOPK", 1025) != 0
+    assert lib.ivonar_define(b"MAX_TOPK", 256) == 0
     assert lib.ivonar_error_string(1)
     assert runtime.gemm_plan(2048, 4096, 1024) == 1
     assert runtime.gemm_plan(1, 4096, 1024) >= 1
     for n, expected in [(8, 2), (64, 2), (100, 2), (1024, 16), (4096, 64), (8192, 64), (28672, 64)]:
         lanes, per_lane = runtime.gemv_plan(100, n)
         assert lanes == expected and per_lane == 2
+
+
+def test_sampler_refuses_the_cpu():
+    from ivonar_amd import runtime
+    from ivonar_amd.sampling import DeviceSampler
+
+    with pytest.raises(runtime.KernelError):
+        DeviceSampler(32000, "cpu")
 
 
 def test_launch_checks_argument_count():
