@@ -277,11 +277,12 @@ def measure_traffic(calls: int = 8) -> dict:
             "per_launch": [round(v) for v in per_launch]}
 
 
-def measure_mfma(calls: int = 16, cus: int = 256) -> dict:
-    """MFMA-busy share of the token GEMM from one counter pass over the GEMM probe: per dispatch,
-    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the expression of rocprofv3's MfmaUtil, and the
-    int8 ops the MFMA unit counted (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512) against 2*M*N*K."""
-    counters = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_I8", "GRBM_GUI_ACTIVE"]
+def measure_mfma(calls: int = 16, cus: int = 256, xcds: int = 8) -> dict:
+    """MFMA-busy share of the token GEMM from one counter pass over the GEMM probe, per case: rocprofv3's
+    derived MfmaUtil (SQ_VALU_MFMA_BUSY_CYCLES summed over SIMDs / (GRBM_GUI_ACTIVE max over XCDs x SIMDs)),
+    the same ratio from the raw counters (GRBM_GUI_ACTIVE as read is the sum over the XCDs), and the int8
+    ops the MFMA unit counted (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512) against 2*M*N*K."""
+    counters = ["MfmaUtil", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_I8", "GRBM_GUI_ACTIVE"]
     rows = counter_pass(counters, "gemm-prefill", calls)
     if isinstance(rows, str):
         return {"error": rows}
@@ -293,14 +294,18 @@ def measure_mfma(calls: int = 16, cus: int = 256) -> dict:
     table = {}
     for index, (k, n, m) in enumerate(cases):
         chunk = gemm[index * calls:(index + 1) * calls]
-        busy = sum(r["SQ_VALU_MFMA_BUSY_CYCLES"] for r in chunk) / calls
-        active = sum(r["GRBM_GUI_ACTIVE"] for r in chunk) / calls
-        mops = sum(r["SQ_INSTS_VALU_MFMA_MOPS_I8"] for r in chunk) / calls
-        table[f"{k}x{n}_M{m}"] = {"mfma_busy_share": round(busy / (active * 4 * cus), 4),
-                                  "mfma_ops_counted": int(mops * 512), "ops_algorithmic": 2 * m * n * k,
-                                  "kernel": chunk[0]["kernel"].split("(")[0]}
+
+        def mean(name, chunk=chunk):
+            return sum(r[name] for r in chunk) / calls
+
+        busy, active = mean("SQ_VALU_MFMA_BUSY_CYCLES"), mean("GRBM_GUI_ACTIVE")
+        name = chunk[0]["kernel"].replace("void ivo::(anonymous namespace)::", "").split("(")[0]
+        table[f"{k}x{n}_M{m}"] = {"MfmaUtil_pct": round(mean("MfmaUtil"), 2),
+                                  "busy_share_raw": round(busy * xcds / (active * 4 * cus), 4),
+                                  "mfma_ops_counted": int(mean("SQ_INSTS_VALU_MFMA_MOPS_I8") * 512),
+                                  "ops_algorithmic": 2 * m * n * k, "kernel": name}
     return {"by_case": table, "simds": 4 * cus,
-            "note": "GRBM_GUI_ACTIVE counts the whole dispatch, launch and drain included"}
+            "note": "GRBM_GUI_ACTIVE covers the whole dispatch under counter collection, launch and drain included"}
 
 
 def m_sweep(device, stream) -> dict:

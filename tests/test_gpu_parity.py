@@ -156,12 +156,12 @@ def test_gemv_plain_store_edge_shapes(cuda, oracle, rows, k):
 
 
 @pytest.mark.parametrize("rows,k", [(4096, 1024), (1024, 4096), (3072, 1024), (512, 8192), (256, 28672),
-                                    (333, 5000)])
+                                    (333, 5000), (64, 8193), (128, 12288), (96, 32768), (40, 32769)])
 def test_gemv_plain_store_model_shapes(cuda, oracle, rows, k):
     _check_gemv_store(cuda, oracle, rows, k, bias=False)
 
 
-@pytest.mark.parametrize("k", [24, 1024, 4096, 8192])
+@pytest.mark.parametrize("k", [24, 1024, 4096, 5000, 8192, 8200, 28672])
 def test_gemv_residual_and_silu_pair(cuda, oracle, k):
     import torch
     from ivonar_amd import ops, runtime
@@ -190,7 +190,7 @@ def test_gemv_residual_and_silu_pair(cuda, oracle, k):
     assert_within(to_np(half), ref, rtol=1e-5, atol=1e-6, what="silu pair vs reference order")
 
 
-@pytest.mark.parametrize("k", [96, 1024, 8192])
+@pytest.mark.parametrize("k", [96, 1024, 4100, 8192, 8193])
 def test_gemv_norm_store_and_prequant(cuda, oracle, k):
     import torch
     from ivonar_amd import ops, runtime
