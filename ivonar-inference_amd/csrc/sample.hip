@@ -94,6 +94,7 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 __device__ __forceinline__ uint64_t lanes_below() { return (1ull << lane_id()) - 1ull; }
 
 struct SampleShared {
+  unsigned bound_key[kMaxGroups];  // order keys of the group bounds, read once
   int group_list[kMaxGroups];
   unsigned cand_key[kCandidates];
   int cand_index[kCandidates];
@@ -164,12 +165,12 @@ __device__ unsigned block_min_u(unsigned v, SampleShared& sh) {
 
 // Element sources for the selection steps: element j of a sequence gives a
 // key, an index and whether it takes part.
-struct BoundSource {  // the group bounds, j = group
-  const float* bounds;
+struct BoundSource {  // the group bounds' keys in LDS, j = group
+  const unsigned* keys;
   int count;
   __device__ int size() const { return count; }
   __device__ bool get(int j, unsigned& key, int& index) const {
-    key = order_key(bounds[j]);
+    key = keys[j];
     index = j;
     return true;
   }
@@ -310,15 +311,19 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
   const int k = (int)max(1LL, min(requested, (long long)min(max_topk, vocab)));
 
   unsigned peak = 0u;
-  for (int g = tid; g < groups; g += kSampleThreads) peak = max(peak, order_key(bounds[g]));
-  peak = block_max_key(peak, sh);
+  for (int g = tid; g < groups; g += kSampleThreads) {
+    const unsigned key = order_key(bounds[g]);
+    sh.bound_key[g] = key;
+    peak = max(peak, key);
+  }
+  peak = block_max_key(peak, sh);  // its barrier also publishes bound_key
 
   int count;
   if (k == 1) {
     // First group whose bound is the peak, then the first element in it.
     unsigned first = 0xffffffffu;
     for (int g = tid; g < groups; g += kSampleThreads)
-      if (order_key(bounds[g]) == peak) first = min(first, (unsigned)g);
+      if (sh.bound_key[g] == peak) first = min(first, (unsigned)g);
     first = block_min_u(first, sh);
     if (first >= (unsigned)groups) first = 0u;  // unreachable: the peak is one of the bounds
     if (tid < 64) {
@@ -335,12 +340,12 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
   } else {
     // Tb: the k-th largest group bound (all groups when there are fewer than k).
     unsigned floor = 0u;
-    if (groups >= k) floor = kth_largest(BoundSource{bounds, groups}, k, sh).key;
+    if (groups >= k) floor = kth_largest(BoundSource{sh.bound_key, groups}, k, sh).key;
     // Groups whose bound is >= Tb, in ascending order.
     int listed = 0;
     for (int base = 0; base < groups; base += kSampleThreads) {
       const int g = base + tid;
-      const bool in = g < groups && order_key(bounds[g]) >= floor;
+      const bool in = g < groups && sh.bound_key[g] >= floor;
       int before, unused, total, unused_total;
       block_scan2(in, false, before, unused, total, unused_total, sh);
       if (in) sh.group_list[listed + before] = g;
@@ -348,20 +353,31 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
     }
     __syncthreads();
     const GroupSource elements{logits, seen, sh.group_list, rule, listed, vocab, floor};
-    // Their elements with key >= Tb, compacted in index order while they fit.
+    // Their elements with key >= Tb, compacted in index order while they fit;
+    // the logits of kGather blocks of 1024 elements are read in one round.
+    constexpr int kGather = 4;
     int candidates = 0;
-    for (int base = 0; base < elements.size(); base += kSampleThreads) {
-      const int j = base + tid;
-      unsigned key = 0u;
-      int index = 0;
-      const bool in = j < elements.size() && elements.get(j, key, index);
-      int before, unused, total, unused_total;
-      block_scan2(in, false, before, unused, total, unused_total, sh);
-      if (in && candidates + before < kCandidates) {
-        sh.cand_key[candidates + before] = key;
-        sh.cand_index[candidates + before] = index;
+    for (int base = 0; base < elements.size(); base += kSampleThreads * kGather) {
+      unsigned keys[kGather];
+      int indices[kGather];
+      bool ins[kGather];
+#pragma unroll
+      for (int c = 0; c < kGather; ++c) {
+        const int j = base + c * kSampleThreads + tid;
+        keys[c] = 0u;
+        indices[c] = 0;
+        ins[c] = j < elements.size() && elements.get(j, keys[c], indices[c]);
       }
-      candidates += total;
+#pragma unroll
+      for (int c = 0; c < kGather; ++c) {
+        int before, unused, total, unused_total;
+        block_scan2(ins[c], false, before, unused, total, unused_total, sh);
+        if (ins[c] && candidates + before < kCandidates) {
+          sh.cand_key[candidates + before] = keys[c];
+          sh.cand_index[candidates + before] = indices[c];
+        }
+        candidates += total;
+      }
     }
     __syncthreads();
     if (candidates <= kCandidates) {
