@@ -190,6 +190,22 @@ def read_ceiling(matrices, stream) -> dict:
             "kernel": "ivonar_stream_read (16-byte loads, 4 in flight per thread, 1024 blocks)"}
 
 
+def validate_throughput(matrices, stream) -> dict:
+    """ivonar_validate_ternary (the checkpoint loader's device check: reserved codes, non-finite or
+    non-positive scales) over the 16 stress operands, one launch each, median of 20 graph replays."""
+    from ivonar_amd import checkpoint
+
+    operands = [m for shape in matrices for m in shape]
+    total = sum(m.packed.numel() + 2 * m.scales.numel() for m in operands)
+
+    def run():
+        for m in operands:
+            checkpoint.validation_flags(m.packed, m.scales)
+
+    seconds = time_graph(graph_of(run, stream), 20, 2, median=True)
+    return {"GBps": round(total / seconds / 1e9, 1), "bytes": total, "us_per_operand": round(seconds / len(operands) * 1e6, 2)}
+
+
 def time_calls(call, stream, calls_per_graph: int, replays: int, warmup: int = 2) -> float:
     """Seconds per call: `calls_per_graph` back-to-back calls recorded in one HIP graph, so that the time of
     a short kernel is not the host's graph-launch time."""
@@ -423,6 +439,7 @@ def main() -> None:
     kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
     achieved = kernel_bytes / kernel_seconds / 1e9
     ceiling = read_ceiling(matrices, stream)
+    results["checkpoint_validate"] = validate_throughput(matrices, stream)
     copy = copy_bandwidth(device, stream)
 
     # ---- single linear K=1024 -> N=4096 (launch-latency bound) ------------------------------

@@ -181,6 +181,15 @@ hipError_t sample_token(hipStream_t stream, const float* logits, const float* bo
                         const float* penalty, const float* inverse_penalty, uint8_t* seen, const int64_t* top_k,
                         const float* uniform, int64_t* token, int64_t* history, int vocab);
 
+/* ------------------------------------------------------ checkpoint checks
+ * The packed-buffer tests of the reference loader (loader.py:94-112), on the
+ * device: ORs into flags[0] bit 0 when a byte of packed[0..packed_bytes)
+ * holds the reserved code 3, bit 1 when a scale of scales[0..scale_count) is
+ * not finite, bit 2 when one is not positive.  The caller zeroes flags first
+ * and reads it after the stream completes.  Both buffers 16-byte aligned. */
+hipError_t ivonar_validate_ternary(hipStream_t stream, const uint8_t* packed, long long packed_bytes,
+                                   const uint16_t* scales, long long scale_count, unsigned* flags);
+
 /* Measurement export (no reference counterpart): reads `bytes` (a multiple of
  * 16, 16-byte aligned) of `data` with 16-byte loads at full occupancy and
  * writes nothing in practice; `sink` must hold ivonar_stream_read_sink_words()

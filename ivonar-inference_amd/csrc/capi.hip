@@ -361,6 +361,16 @@ hipError_t sample_token(hipStream_t stream, const float* logits, const float* bo
                              history, vocab);
 }
 
+hipError_t ivonar_validate_ternary(hipStream_t stream, const uint8_t* packed, long long packed_bytes,
+                                   const uint16_t* scales, long long scale_count, unsigned* flags) {
+  if (flags == nullptr || packed_bytes < 0 || scale_count < 0) return hipErrorInvalidValue;
+  if ((packed_bytes > 0 && (packed == nullptr || !aligned16(packed))) ||
+      (scale_count > 0 && (scales == nullptr || !aligned16(scales))))
+    return hipErrorInvalidValue;
+  if (packed_bytes == 0 && scale_count == 0) return hipSuccess;
+  return launch_validate(stream, packed, packed_bytes, scales, scale_count, flags);
+}
+
 int ivonar_stream_read_sink_words(void) { return stream_read_sink_words(); }
 
 hipError_t ivonar_stream_read(hipStream_t stream, const void* data, long long bytes, unsigned* sink) {

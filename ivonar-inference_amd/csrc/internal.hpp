@@ -111,6 +111,10 @@ hipError_t launch_sample_token(hipStream_t stream, const float* logits, const fl
                                const float* penalty, const float* inverse_penalty, uint8_t* seen,
                                const int64_t* top_k, const float* uniform, int64_t* token, int64_t* history,
                                int vocab);
+// Reserved codes in a packed operand (flag 1), non-finite (2) or non-positive
+// (4) fp16 scales, ORed into flags[0]; packed and scales 16-byte aligned.
+hipError_t launch_validate(hipStream_t stream, const uint8_t* packed, long long packed_bytes, const uint16_t* scales,
+                           long long scale_count, unsigned* flags);
 // Streaming-read reference (measurement): reads bytes/16 16-byte words of data;
 // sink holds stream_read_sink_words() uint32 and is written only in theory.
 int stream_read_sink_words();

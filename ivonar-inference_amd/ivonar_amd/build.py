@@ -30,7 +30,7 @@ INCLUDE = PACKAGE.parent.parent / "include"
 LIBRARY = PACKAGE / "_lib" / "libivonar_ternary.so"
 ARCH = "gfx950"
 SOURCES = ("quantize.hip", "gemv.hip", "gemm.hip", "gemm_skinny.hip", "embed.hip", "sample.hip", "stream_read.hip",
-           "capi.hip")
+           "validate.hip", "capi.hip")
 HIP_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",

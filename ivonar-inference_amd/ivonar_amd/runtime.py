@@ -71,6 +71,7 @@ SIGNATURES: dict[str, list] = {
     "logit_bounds": [_P, _P, _P, _P, _P, _P, _I],
     "sample_token": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I],
     "ivonar_stream_read": [_P, ctypes.c_longlong, _P],
+    "ivonar_validate_ternary": [_P, ctypes.c_longlong, _P, ctypes.c_longlong, _P],
 }
 
 _lock = threading.Lock()

@@ -213,3 +213,84 @@ def decoder_stack(config: StackConfig | None = None, seed: int = 1, keep_codes: 
 def prompt_ids(vocab: int, length: int = 36, seed: int = 1) -> list[int]:
     """Random prompt ids in [2, vocab)."""
     return [int(v) for v in np.random.default_rng(10_000 + seed).integers(2, vocab, size=length)]
+
+
+# Packed checkpoints ----------------------------------------------------------
+
+
+def checkpoint_config(vocab: int = 300, hidden: int = 256, layer_types=("mamba", "mla"), dense: int = 512,
+                      latent: int = 128, heads: int = 4, state_dim: int = 16) -> dict:
+    """A configuration dictionary that satisfies the packed-checkpoint contract (reference config.py:6-74)."""
+    return {
+        "architecture": "ivonar_native_ternary", "architecture_version": 1, "ternary_group_size": 128,
+        "ternary_storage": "q2_g128", "activation_quantization": "int8_per_token",
+        "output_head_type": "tied_ternary_embedding_head", "mla_rope_layout": "decoupled_direct_rope",
+        "mamba_implementation": "ivonar_mamba3_conv_et_mimo", "mamba_variant": "MIMO", "tie_embeddings": True,
+        "name": "synthetic", "vocab_size": vocab, "seq_len": 512, "hidden_dim": hidden,
+        "num_layers": len(layer_types), "num_heads": heads, "state_dim": state_dim,
+        "layer_types": list(layer_types), "dense_intermediate_dim": dense, "mla_latent_dim": latent,
+    }
+
+
+def checkpoint_state(config: dict, seed: int = 0) -> dict:
+    """A model_state with the reference's key names and shapes for `config` (random ternary codes,
+    positive fp16 scales, norms near 1; the mixers' own tensors are small random arrays).  Output
+    widths of the mixer projections are this generator's choice: the checkpoint format fixes only
+    their input widths."""
+    import torch
+
+    rng = np.random.default_rng(seed)
+    hidden, dense, latent = config["hidden_dim"], config["dense_intermediate_dim"], config["mla_latent_dim"]
+    heads, state_dim = config["num_heads"], config["state_dim"]
+    state: dict = {}
+
+    def linear(prefix: str, rows: int, k: int) -> None:
+        state[f"{prefix}.packed_weight"] = torch.from_numpy(pack_codes(sample_codes(rng, rows, k)))
+        state[f"{prefix}.weight_scales"] = torch.from_numpy(
+            to_half_scales(np.abs(rng.normal(0.0, 0.02, size=(rows, math.ceil(k / GROUP)))) + 1e-4))
+
+    def vector(key: str, n: int, base: float = 1.0, spread: float = 0.1) -> None:
+        state[key] = torch.from_numpy((base + spread * rng.standard_normal(n)).astype(np.float32))
+
+    linear("token_io.projection", config["vocab_size"], hidden)
+    for index, kind in enumerate(config["layer_types"]):
+        prefix = f"blocks.{index}"
+        if kind == "mamba":
+            linear(f"{prefix}.mixer.in_proj", 2 * hidden + 2 * heads * state_dim, hidden)
+            linear(f"{prefix}.mixer.bc_dt_proj", 2 * heads * state_dim + heads, hidden)
+            linear(f"{prefix}.mixer.out_proj", hidden, hidden)
+            vector(f"{prefix}.mixer.log_decay", heads, 0.0, 1.0)
+            vector(f"{prefix}.mixer.theta", heads, 0.0, 1.0)
+            vector(f"{prefix}.mixer.skip", hidden, 0.0, 1.0)
+            vector(f"{prefix}.mixer.conv_weight", hidden * 4, 0.0, 0.1)
+            vector(f"{prefix}.mixer.conv_bias", hidden, 0.0, 0.1)
+        else:
+            linear(f"{prefix}.mixer.q_proj", hidden, hidden)
+            linear(f"{prefix}.mixer.kv_down_proj", latent, hidden)
+            linear(f"{prefix}.mixer.k_nope_up_proj", hidden, latent)
+            linear(f"{prefix}.mixer.k_rope_proj", 64, hidden)
+            linear(f"{prefix}.mixer.v_up_proj", hidden, latent)
+            linear(f"{prefix}.mixer.out_proj", hidden, hidden)
+        linear(f"{prefix}.ffn.gate_proj", dense, hidden)
+        linear(f"{prefix}.ffn.up_proj", dense, hidden)
+        linear(f"{prefix}.ffn.down_proj", hidden, dense)
+        vector(f"{prefix}.mixer_norm.weight", hidden)
+        vector(f"{prefix}.ffn_norm.weight", hidden)
+    vector("final_norm.weight", hidden)
+    return state
+
+
+def write_checkpoint(path, config: dict | None = None, state: dict | None = None, seed: int = 0,
+                     tokenizer_sha256: str | None = "0" * 64, **extra) -> dict:
+    """Writes a packed checkpoint in the reference's payload layout (loader.py:222-258) with torch.save;
+    returns the payload."""
+    import torch
+
+    config = config or checkpoint_config()
+    payload = {"format": "ivonar_packed_ternary_inference", "schema_version": 1, "config": config,
+               "model_state": state if state is not None else checkpoint_state(config, seed),
+               "tokenizer_sha256": tokenizer_sha256, "lineup": "synthetic", "stage": "test", "phase": "packed",
+               "step": 7}
+    payload.update(extra)
+    torch.save(payload, path)
+    return payload
