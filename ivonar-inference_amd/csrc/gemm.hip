@@ -384,6 +384,7 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (((long long)a.m + 256) * ceil_div(a.n, kChunk) * kChunk >= limit ||
       ((long long)a.rows + 256) * a.row_bytes >= limit || ((long long)a.rows + 256) * a.groups * 2 >= limit)
     return hipErrorInvalidValue;
+  if (gemm_wide_applies(a.m, a.rows)) return launch_gemm_wide(stream, a);
   switch (a.epi) {
     case kStore: return launch_epi<kStore>(stream, a);
     case kResidual: return launch_epi<kResidual>(stream, a);

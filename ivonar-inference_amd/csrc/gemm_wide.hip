@@ -1,0 +1,386 @@
+// Token GEMM for long prompts on CDNA4 int8 MFMA (reference: kernels/ternary.cu:
+// 688-784, entry points gemm_tile_* with GEMM_ARGS; the reference uses dp4a).
+//
+// y[t, r] = s_x[t] * sum_g P[t, r, g] * scale[r, g] (+ bias[r]), where
+// P[t, r, g] = sum over the 128 inputs of group g of (code - 1) * q is exact.
+//
+// Why a second tiled kernel: every (token, row, group) needs one int -> fp32
+// conversion and one fmaf after its two MFMAs, i.e. four VALU instructions per
+// v_mfma_i32_16x16x64_i8.  On gfx950 a VALU instruction between MFMAs costs
+// about as much issue time as a quarter of an MFMA, so the MFMA pipe stays
+// busy only if (a) nothing else adds VALU work and (b) the conversions of one
+// tile run while the next tile's MFMAs execute.  This kernel is built for
+// that:
+//   * a wave owns 16*MT tokens x 64 rows (MT = 8: 128 tokens), so each
+//     expanded weight fragment feeds MT MFMA rows and the expansion costs
+//     under one VALU instruction per MFMA;
+//   * operands reach LDS by direct buffer-to-LDS loads (no staging registers,
+//     no VALU, no LDS write instructions); tokens past m, rows past the
+//     matrix and the missing second chunk of an odd chunk count read as zeros
+//     through the buffer range check;
+//   * the fold of token row mt-1 (int32 -> fp32, one fmaf per output with the
+//     row's group scale, ascending groups: the order the CPU oracle restates
+//     as orc_gemm_seq) is interleaved with the MFMAs of token row mt, and the
+//     last row of a group with the first row of the next group.
+//
+// LDS stage (three, so that two groups are in flight; one barrier per group):
+//   A: 16*MT token rows x 8 pieces of 16 bytes (the group's q8 bytes), piece p
+//      of token t at slot t*8 + (p ^ swz(t)), swz(t) = (t & 7) ^ ((t >> 3) & 1),
+//      which keeps each 8- or 16-lane phase of the operand reads on distinct
+//      banks;
+//   B: 64*WN weight rows x 2 pieces of 16 bytes (the group's packed bytes),
+//      piece p of row r at slot p * 64*WN + r, so the 8-byte operand reads of
+//      a wave cover two contiguous 256-byte runs;
+//   minus each token's group sum (seeds the MFMA accumulator so that
+//   sum(code * q) - sum(q) = P comes out exact) and the rows' fp32 scales,
+//   both written from registers one group ahead.
+#include "internal.hpp"
+#include "ternary_device.hpp"
+
+namespace ivo {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// Buffer resource over `bytes` bytes (raw, no stride): offsets at or past the
+// size read zeros.  The launcher keeps every operand below 2 GiB.
+__device__ __forceinline__ v4u wide_buffer(const void* base, long long bytes) {
+  const unsigned long long address = (unsigned long long)base;
+  return v4u{(unsigned)address, (unsigned)(address >> 32) & 0xFFFFu, (unsigned)bytes, 0x00020000u};
+}
+
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// The loads of the main loop are issued as inline assembly, so the compiler
+// inserts no waits for them: it cannot tell which stage a direct-to-LDS load
+// fills and would otherwise wait for every load in flight before the first
+// LDS read of a step.  The kernel places the waits itself (see the loop).
+//
+// One 16-byte piece per lane from a buffer straight into LDS: lane i writes
+// lds_base + 16 * i (lds_base is wave-uniform; M0 is restored afterwards).
+__device__ __forceinline__ void dma16(v4u buffer, unsigned lds_base, int voffset, int soffset) {
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(voffset), "s"(buffer), "s"(soffset)
+      : "memory");
+}
+
+__device__ __forceinline__ int load_b32(v4u buffer, int voffset, int soffset) {
+  int r;
+  asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(r) : "v"(voffset), "s"(buffer), "s"(soffset) : "memory");
+  return r;
+}
+
+__device__ __forceinline__ int load_u16(v4u buffer, int voffset, int soffset) {
+  int r;
+  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(r) : "v"(voffset), "s"(buffer), "s"(soffset) : "memory");
+  return r;
+}
+
+__device__ __forceinline__ int a_swizzle(int t) { return (t & 7) ^ ((t >> 3) & 1); }
+
+template <int MT, int WN>
+struct WideTile {
+  static constexpr int kThreads = 64 * WN;
+  static constexpr int kTokens = 16 * MT;
+  static constexpr int kRows = 64 * WN;
+  static constexpr int kAOffset = 0;
+  static constexpr int kBOffset = kTokens * 128;
+  static constexpr int kStageBytes = kBOffset + kRows * 32;  // DMA part of one stage
+  static constexpr int kLdsBytes = 3 * (kStageBytes + kTokens * 4 + kRows * 4);
+  static constexpr int kLoadsA = kTokens * 8 / kThreads;  // 16-byte pieces per thread and group
+  static constexpr int kLoadsB = kRows * 2 / kThreads;
+  static constexpr int kLoads = kLoadsA + kLoadsB;         // DMA instructions per thread and group
+  static_assert(kTokens * 8 % kThreads == 0 && kRows * 2 == 2 * kThreads, "whole DMA rounds");
+  static_assert(kTokens <= kThreads, "one thread per token seed");
+};
+
+template <int EPI, int MT, int WN>
+__global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __restrict__ q8,
+                                                            const float* __restrict__ scale_in,
+                                                            const uint8_t* __restrict__ packed,
+                                                            const uint16_t* __restrict__ scales,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ output, GemmArgs a) {
+  using T = WideTile<MT, WN>;
+  __shared__ __align__(16) unsigned char stages[3][T::kStageBytes];
+  __shared__ __align__(16) int seeds[3][T::kTokens];
+  __shared__ __align__(16) float row_scales[3][T::kRows];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, kb = lane >> 4;
+  const int chunks = (a.n + kChunk - 1) / kChunk;
+  const int groups = (a.n + kGroup - 1) / kGroup;
+  const int q8_stride = chunks * kChunk;
+  const int token0 = blockIdx.y * T::kTokens;
+  const int row0 = blockIdx.x * T::kRows;
+  constexpr int kPast = 0x7FFFFFF0;
+
+  const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
+  const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
+  const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
+  const v4u x_buf = wide_buffer(a.xsum_in, (long long)a.m * chunks * 4);
+
+  // Per-thread DMA offsets, fixed for the kernel (the group moves the scalar
+  // offset).  A: slot s = j * threads + tid holds token s >> 3, piece
+  // (s & 7) ^ swz(token).  Pieces 4..7 are the group's second chunk.
+  int a_live[T::kLoadsA], a_dead[T::kLoadsA];
+#pragma unroll
+  for (int j = 0; j < T::kLoadsA; ++j) {
+    const int s = j * T::kThreads + tid;
+    const int t = s >> 3;
+    const int p = (s & 7) ^ a_swizzle(t);
+    a_live[j] = (token0 + t) * q8_stride + p * 16;
+    a_dead[j] = p < 4 ? a_live[j] : kPast;
+  }
+  // B: slot s = j * threads + tid holds row tid, piece j.
+  const int b_off = (row0 + tid) * a.row_bytes;
+  const int seed_token = tid % T::kTokens;
+  const int x_off = (token0 + seed_token) * chunks * 4;
+  const int s_off = (row0 + tid) * a.groups * 2;
+
+  auto dma = [&](int g, int stage) {
+    const bool second_live = 2 * g + 1 < chunks;
+    const unsigned base = __builtin_amdgcn_readfirstlane(lds_address(stages[stage]) + wave * 64 * 16);
+#pragma unroll
+    for (int j = 0; j < T::kLoadsA; ++j)
+      dma16(q8_buf, base + T::kAOffset + j * T::kThreads * 16, second_live ? a_live[j] : a_dead[j], g * kGroup);
+#pragma unroll
+    for (int j = 0; j < T::kLoadsB; ++j)
+      dma16(w_buf, base + T::kBOffset + j * T::kThreads * 16, b_off + j * 16, g * 32);
+  };
+  // The token sums and the row scale of a group, loaded into registers and
+  // written to LDS (as minus the group sum and as fp32) once they arrive.
+  struct Side {
+    int x0, x1, s;
+  };
+  auto side_load = [&](int g) {
+    const bool second_live = 2 * g + 1 < chunks;
+    Side r;
+    r.x0 = load_b32(x_buf, x_off, g * 8);
+    r.x1 = load_b32(x_buf, second_live ? x_off + 4 : kPast, g * 8);
+    r.s = load_u16(s_buf, s_off, g * 2);
+    return r;
+  };
+  // Waits until at most `kLoads` loads are in flight - the DMA issued after
+  // the side loads - then stores the side values.
+  auto side_store = [&](Side& r, int stage) {
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(r.x0), "+v"(r.x1), "+v"(r.s) : "n"(T::kLoads) : "memory");
+    seeds[stage][seed_token] = -(r.x0 + r.x1);
+    row_scales[stage][tid] = h2f((uint16_t)r.s);
+  };
+
+  float acc[MT][4][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
+
+  // The previous token row's int32 tiles and scales, folded while the next
+  // row's MFMAs run.  Zero before the first group (a fold of zeros leaves
+  // acc at +0).
+  v4i prev[4];
+  float prev_sc[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    prev[nt] = v4i{0, 0, 0, 0};
+    prev_sc[nt] = 0.0f;
+  }
+  auto fold = [&](int mt) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = __builtin_fmaf((float)prev[nt][i], prev_sc[nt], acc[mt][nt][i]);
+  };
+
+  const int b_read = ((kb >> 1) * T::kRows + wave * 64 + col) * 16 + (kb & 1) * 8;
+  const int sc_read = wave * 64 + col;
+
+  // One group step.  Group g+2 streams into the stage group g-1 used while
+  // group g is computed: first the side loads of g+2, then its DMA, then the
+  // MFMAs of g, then the side values of g+2 go to LDS.  The wait for those
+  // side loads also retires the DMA of g+1 (loads complete in order) and
+  // leaves the DMA of g+2 in flight, so the barrier at the top of the next
+  // step publishes every wave's pieces of g+1.
+  auto step = [&](int g, int cur, int fill) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int g_fill = min(g + 2, groups - 1);  // past the end: the last group again (never read)
+    Side side = side_load(g_fill);
+    dma(g_fill, fill);
+
+    const unsigned char* base = stages[cur];
+    v4i bf[2][4];
+    float sc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const uint2 w = *reinterpret_cast<const uint2*>(base + T::kBOffset + b_read + nt * 16 * 16);
+      bf[0][nt] = v4i{(int)(w.x & kLow2), (int)((w.x >> 2) & kLow2), (int)((w.x >> 4) & kLow2),
+                      (int)((w.x >> 6) & kLow2)};
+      bf[1][nt] = v4i{(int)(w.y & kLow2), (int)((w.y >> 2) & kLow2), (int)((w.y >> 4) & kLow2),
+                      (int)((w.y >> 6) & kLow2)};
+      sc[nt] = row_scales[cur][sc_read + nt * 16];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int t = mt * 16 + col;
+      const unsigned char* arow = base + T::kAOffset + t * 128;
+      const v4i a0 = *reinterpret_cast<const v4i*>(arow + (((2 * kb) ^ a_swizzle(t)) * 16));
+      const v4i a1 = *reinterpret_cast<const v4i*>(arow + (((2 * kb + 1) ^ a_swizzle(t)) * 16));
+      const v4i seed = *reinterpret_cast<const v4i*>(&seeds[cur][mt * 16 + 4 * kb]);
+      v4i p[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bf[0][nt], seed, 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bf[1][nt], p[nt], 0, 0, 0);
+      fold(mt == 0 ? MT - 1 : mt - 1);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) prev[nt] = p[nt];
+      if (mt == 0) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) prev_sc[nt] = sc[nt];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+    }
+    side_store(side, fill);
+  };
+
+  {
+    Side s0 = side_load(0);
+    dma(0, 0);
+    Side s1 = side_load(min(1, groups - 1));
+    dma(min(1, groups - 1), 1);
+    side_store(s0, 0);  // waits for all but the DMA of group 1: group 0 is complete
+    side_store(s1, 1);
+  }
+  int cur = 0;
+  for (int g = 0; g < groups; ++g) {
+    const int fill = cur == 0 ? 2 : cur - 1;  // (g + 2) % 3
+    step(g, cur, fill);
+    cur = cur == 2 ? 0 : cur + 1;
+  }
+  // No direct-to-LDS load may still be in flight when the block's LDS is
+  // handed to the next block.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  fold(MT - 1);
+
+  // Epilogue.  y = acc * s_x[t] (+ bias[r]) in the MFMA layout (lane holds
+  // rows wave*64 + nt*16 + col of tokens mt*16 + 4*kb + i), transposed through
+  // LDS one 16-token row of tiles at a time, so that each lane then owns four
+  // consecutive rows of one token and every store is a 16-byte vector, 16
+  // lanes covering 256 contiguous bytes of an output row.  Each wave uses its
+  // own slice of the first stage; a wave's LDS operations complete in order,
+  // so the slice needs no barrier between its writes and reads.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  constexpr int kPitch = 68;  // floats per token row of a slice (conflict-free column writes)
+  static_assert(4 * 16 * kPitch * 4 <= T::kStageBytes, "transpose slices fit one stage");
+  float* slice = reinterpret_cast<float*>(stages[0]) + wave * 16 * kPitch;
+  const bool has_bias = bias != nullptr;
+  float bv[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int row = row0 + wave * 64 + nt * 16 + col;
+    bv[nt] = (has_bias && row < a.rows) ? bias[row] : 0.0f;
+  }
+  const int r4 = (lane & 15) * 4;
+  const int row = row0 + wave * 64 + r4;  // first of the lane's four rows (a multiple of 4)
+  const bool rows_whole = row + 3 < a.rows;
+  const uintptr_t base_addr = reinterpret_cast<uintptr_t>(output);
+  const bool vec4 = (a.out_stride & 3) == 0 && (base_addr & 15) == 0;
+  const bool vec2 = (a.out_stride & 1) == 0 && (base_addr & 7) == 0;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    float sx[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sx[i] = scale_in[min(token0 + mt * 16 + 4 * kb + i, a.m - 1)];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float y = acc[mt][nt][i] * sx[i];
+        if (has_bias) y = y + bv[nt];
+        slice[(4 * kb + i) * kPitch + nt * 16 + col] = y;
+      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tl = j * 4 + (lane >> 4);
+      const int t = token0 + mt * 16 + tl;
+      const float4 v = *reinterpret_cast<const float4*>(slice + tl * kPitch + r4);
+      if (t >= a.m) continue;
+      float* orow = output + (size_t)t * a.out_stride;
+      if constexpr (EPI == kSiluPair) {
+        const float p0 = ivo_silu(v.x) * v.y, p1 = ivo_silu(v.z) * v.w;
+        if (rows_whole && vec2) {
+          *reinterpret_cast<float2*>(orow + (row >> 1)) = make_float2(p0, p1);
+        } else {
+          if (row + 1 < a.rows) orow[row >> 1] = p0;
+          if (row + 3 < a.rows) orow[(row >> 1) + 1] = p1;
+        }
+      } else if (rows_whole && vec4) {
+        float4* dst = reinterpret_cast<float4*>(orow + row);
+        if constexpr (EPI == kResidual) {
+          const float4 o = *dst;
+          *dst = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        } else {
+          *dst = v;
+        }
+      } else {
+        const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (row + k < a.rows) {
+            if constexpr (EPI == kResidual) orow[row + k] = orow[row + k] + vs[k];
+            else orow[row + k] = vs[k];
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int EPI, int MT, int WN>
+hipError_t launch_wide_shape(hipStream_t stream, const GemmArgs& a) {
+  using T = WideTile<MT, WN>;
+  const dim3 grid(ceil_div(a.rows, T::kRows), ceil_div(a.m, T::kTokens));
+  hipLaunchKernelGGL((gemm_wide_kernel<EPI, MT, WN>), grid, dim3(T::kThreads), 0, stream,
+                     a.q8_in, a.scale_in, a.packed, a.scales, a.bias, a.output, a);
+  return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a) {
+  return launch_wide_shape<EPI, 8, 4>(stream, a);
+}
+
+}  // namespace
+
+bool gemm_wide_applies(int m, int rows) {
+  const long long blocks = (long long)ceil_div(rows, 256) * ceil_div(m, 128);
+  return m >= 128 && blocks >= 256 && WideTile<8, 4>::kLdsBytes <= max_lds_per_block();
+}
+
+hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
+  switch (a.epi) {
+    case kStore: return launch_wide_epi<kStore>(stream, a);
+    case kResidual: return launch_wide_epi<kResidual>(stream, a);
+    case kSiluPair: return launch_wide_epi<kSiluPair>(stream, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ivo

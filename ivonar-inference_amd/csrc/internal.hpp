@@ -92,6 +92,10 @@ struct GemmArgs {
   int m;
 };
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a);
+// Long-prompt token GEMM (128-token wave tiles, LDS DMA staging); same fp32
+// order as the tiled GEMM.
+bool gemm_wide_applies(int m, int rows);
+hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a);
 
 // K-splits of the GEMM for m tokens (its fp32 order: S contiguous group ranges,
 // each an fmaf chain, added in order); 1 = one chain over all groups.

@@ -452,3 +452,51 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
     q, s = T.quantize_closed_form(x[0])
     truth = T.truth_fp64(T.group_partials_int64(codes, q), T.half_bits_to_float(scale_bits), s)
     assert_within(y[0], truth, what="skinny gemm vs fp64 truth")
+
+
+# Long prompts with many row blocks run the 128-token-tile kernel (chosen when m >= 128 and the
+# 128-token x 256-row tiling gives >= 256 blocks): ragged token and row counts, an odd chunk count,
+# a single-chunk K, bias, and every epilogue with a padded output stride.
+@pytest.mark.parametrize("m,k,rows,bias", [(1000, 1088, 8200, True), (2048, 64, 4096, False),
+                                          (128, 4096, 65536, False), (1537, 1100, 5120, True)])
+def test_gemm_wide_tiles_edges(cuda, oracle, m, k, rows, bias):
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(m * 7 + k + rows)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=bias)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    sample = np.unique(np.array([0, 1, 15, 16, 127, 128, 129, 255, m // 2, m - 2, m - 1]) % m)
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    assert runtime.gemm_plan(m, rows, k) == 1
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), 1)
+    assert_bits_equal(y[sample], expected, "sampled tokens")
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_gemm_wide_tiles_epilogues(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(97 if epilogue == "residual" else 96)
+    m, k, rows = 300, 1024, 24576
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    width = rows if epilogue == "residual" else rows // 2
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    sample = np.array([0, 5, 127, 128, 255, 256, 299])
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
+                                 len(sample), 1)
+    assert_bits_equal(to_np(out)[sample], expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
