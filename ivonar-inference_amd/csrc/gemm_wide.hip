@@ -220,41 +220,58 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
     Side side = side_load(g_fill);
     dma(g_fill, fill);
 
+    // The step is written as a fixed issue order (scheduling fences between
+    // units): per token row, eight units of one MFMA and two outputs (four
+    // VALU instructions) of the previous row's fold; the next row's operand
+    // reads go out at the start of a row; in the first row each unit also
+    // expands the weight fragment its MFMA takes.
     const unsigned char* base = stages[cur];
-    v4i bf[2][4];
+    uint2 w[4];
     float sc[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      const uint2 w = *reinterpret_cast<const uint2*>(base + T::kBOffset + b_read + nt * 16 * 16);
-      bf[0][nt] = v4i{(int)(w.x & kLow2), (int)((w.x >> 2) & kLow2), (int)((w.x >> 4) & kLow2),
-                      (int)((w.x >> 6) & kLow2)};
-      bf[1][nt] = v4i{(int)(w.y & kLow2), (int)((w.y >> 2) & kLow2), (int)((w.y >> 4) & kLow2),
-                      (int)((w.y >> 6) & kLow2)};
+      w[nt] = *reinterpret_cast<const uint2*>(base + T::kBOffset + b_read + nt * 16 * 16);
       sc[nt] = row_scales[cur][sc_read + nt * 16];
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    auto operands = [&](int mt, v4i& a0, v4i& a1, v4i& seed) {
       const int t = mt * 16 + col;
       const unsigned char* arow = base + T::kAOffset + t * 128;
-      const v4i a0 = *reinterpret_cast<const v4i*>(arow + (((2 * kb) ^ a_swizzle(t)) * 16));
-      const v4i a1 = *reinterpret_cast<const v4i*>(arow + (((2 * kb + 1) ^ a_swizzle(t)) * 16));
-      const v4i seed = *reinterpret_cast<const v4i*>(&seeds[cur][mt * 16 + 4 * kb]);
+      a0 = *reinterpret_cast<const v4i*>(arow + (((2 * kb) ^ a_swizzle(t)) * 16));
+      a1 = *reinterpret_cast<const v4i*>(arow + (((2 * kb + 1) ^ a_swizzle(t)) * 16));
+      seed = *reinterpret_cast<const v4i*>(&seeds[cur][mt * 16 + 4 * kb]);
+    };
+    v4i a0, a1, seed;
+    operands(0, a0, a1, seed);
+    v4i bf[2][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      v4i na0, na1, nseed;
+      if (mt + 1 < MT) operands(mt + 1, na0, na1, nseed);
+      const int fold_row = mt == 0 ? MT - 1 : mt - 1;
       v4i p[4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bf[0][nt], seed, 0, 0, 0);
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bf[1][nt], p[nt], 0, 0, 0);
-      fold(mt == 0 ? MT - 1 : mt - 1);
+      for (int u = 0; u < 8; ++u) {
+        const int h = u >> 2, nt = u & 3;
+        if (mt == 0) {
+          const unsigned x = h ? w[nt].y : w[nt].x;
+          bf[h][nt] = v4i{(int)(x & kLow2), (int)((x >> 2) & kLow2), (int)((x >> 4) & kLow2), (int)((x >> 6) & kLow2)};
+        }
+        p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : seed, 0, 0, 0);
+        const int ft = u >> 1, fi = (u & 1) * 2;
+        acc[fold_row][ft][fi] = __builtin_fmaf((float)prev[ft][fi], prev_sc[ft], acc[fold_row][ft][fi]);
+        acc[fold_row][ft][fi + 1] = __builtin_fmaf((float)prev[ft][fi + 1], prev_sc[ft], acc[fold_row][ft][fi + 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) prev[nt] = p[nt];
       if (mt == 0) {
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) prev_sc[nt] = sc[nt];
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      if (mt + 1 < MT) {
+        a0 = na0;
+        a1 = na1;
+        seed = nseed;
       }
     }
     side_store(side, fill);
