@@ -302,8 +302,8 @@ def measure_mfma(calls: int = 16, cus: int = 256, xcds: int = 8) -> dict:
     rows = counter_pass(counters, "gemm-prefill", calls)
     if isinstance(rows, str):
         return {"error": rows}
-    gemm = [row for row in rows if ("gemm_kernel" in row["kernel"] or "skinny_kernel" in row["kernel"])
-            and all(c in row for c in counters)]
+    kernels = ("gemm_kernel", "gemm_wide_kernel", "skinny_kernel")
+    gemm = [row for row in rows if any(name in row["kernel"] for name in kernels) and all(c in row for c in counters)]
     cases = [(k, n, m) for k, n in PROBE_GEMM_SHAPES for m in PROBE_GEMM_M]
     if len(gemm) != len(cases) * calls:
         return {"error": f"expected {len(cases) * calls} GEMM dispatches, found {len(gemm)}"}

@@ -455,7 +455,7 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
 
 
 # Long prompts with many row blocks run the 128-token-tile kernel (chosen when m >= 128 and the
-# 128-token x 256-row tiling gives >= 256 blocks): ragged token and row counts, an odd chunk count,
+# 128-token x 256-row tiling gives >= 192 blocks): ragged token and row counts, an odd chunk count,
 # a single-chunk K, bias, and every epilogue with a padded output stride.
 @pytest.mark.parametrize("m,k,rows,bias", [(1000, 1088, 8200, True), (2048, 64, 4096, False),
                                           (128, 4096, 65536, False), (1537, 1100, 5120, True)])
