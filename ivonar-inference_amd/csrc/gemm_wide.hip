@@ -43,6 +43,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f2v __attribute__((ext_vector_type(2)));
 
 // Buffer resource over `bytes` bytes (raw, no stride): offsets at or past the
 // size read zeros.  The launcher keeps every operand below 2 GiB.
@@ -300,7 +302,9 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
   // rows wave*64 + nt*16 + col of tokens mt*16 + 4*kb + i), transposed through
   // LDS one 16-token row of tiles at a time, so that each lane then owns four
   // consecutive rows of one token and every store is a 16-byte vector, 16
-  // lanes covering 256 contiguous bytes of an output row.  Each wave uses its
+  // lanes covering 256 contiguous bytes of an output row, written with the
+  // non-temporal hint (the output is streamed once; measured 2-9% faster on
+  // the prefill shapes than plain stores).  Each wave uses its
   // own slice of the first stage; a wave's LDS operations complete in order,
   // so the slice needs no barrier between its writes and reads.
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -343,18 +347,18 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
       if constexpr (EPI == kSiluPair) {
         const float p0 = ivo_silu(v.x) * v.y, p1 = ivo_silu(v.z) * v.w;
         if (rows_whole && vec2) {
-          *reinterpret_cast<float2*>(orow + (row >> 1)) = make_float2(p0, p1);
+          __builtin_nontemporal_store(f2v{p0, p1}, reinterpret_cast<f2v*>(orow + (row >> 1)));
         } else {
           if (row + 1 < a.rows) orow[row >> 1] = p0;
           if (row + 3 < a.rows) orow[(row >> 1) + 1] = p1;
         }
       } else if (rows_whole && vec4) {
-        float4* dst = reinterpret_cast<float4*>(orow + row);
+        f4v* dst = reinterpret_cast<f4v*>(orow + row);
         if constexpr (EPI == kResidual) {
-          const float4 o = *dst;
-          *dst = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+          const f4v o = *dst;
+          __builtin_nontemporal_store(f4v{o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w}, dst);
         } else {
-          *dst = v;
+          __builtin_nontemporal_store(f4v{v.x, v.y, v.z, v.w}, dst);
         }
       } else {
         const float vs[4] = {v.x, v.y, v.z, v.w};
