@@ -309,6 +309,167 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   }
 }
 
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+// Loads the compiler does not track (see gemv_rows_kernel).
+__device__ __forceinline__ v4i32 load_b128(const void* p) {
+  v4i32 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+__device__ __forceinline__ int load_b32(const void* p) {
+  int r;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+__device__ __forceinline__ int load_u16(const void* p) {
+  int r;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+
+// Byte offset of gemv_rows_kernel's 16-byte dump slot: past the q8 row and
+// its chunk sums, 16-byte aligned.
+__host__ __device__ constexpr int rows_dump_offset(int chunks) { return (chunks * (kChunk + 4) + 15) & ~15; }
+
+// One step of a row pair in flight: the two rows' 16 weight bytes of the
+// lane's chunk and the group scale of the lane's own row.
+struct RowStep {
+  v4i32 w0, w1;
+  int s;
+};
+
+// Pre-quantized rows of 3..8 steps (8193 <= K <= 32768 inputs), 64 lanes per
+// row, q8 row in LDS.  Every lane keeps all STEPS steps of its row pair in
+// flight (3*STEPS loads: 14 KB per wave at K=28672, 8 waves and 112 KB per
+// CU) instead of the rolling pipeline's one or two, and refills a step with
+// the same step of the wave's next row pair as soon as it is computed.
+//
+// All loads of the kernel are issued as inline assembly in a fixed order, so
+// the number issued after any step's loads is a constant and the kernel
+// waits for exactly that step: vmcnt(3*(STEPS-1)) before step 0 and
+// vmcnt(3*(STEPS-1) + 2) before the others (the next row pair's bias and
+// residual base go out just before its step 0).  Vector memory loads return
+// in order, so a count that leaves only younger loads outstanding proves the
+// step complete; stores only make the waits longer.  (Compiled loads would
+// get compiler-placed waits, which at this depth drain every load in flight
+// at loop joins.)  The q8 copy's loads go out first and are waited for with
+// the first row pair's weights still in flight.  Lane layout and fp32 order
+// are those of gemv_kernel (orc_gemv_pairs).
+template <int EPI, int STEPS, bool EXACT>
+__global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
+                                                        const uint16_t* __restrict__ scales,
+                                                        const float* __restrict__ bias, float* __restrict__ output,
+                                                        int32_t* __restrict__ partials, GemvShape sh) {
+  constexpr int kBlock = 512;  // one block of 8 waves per CU: up to 256 VGPRs for the steps in flight
+  constexpr int kCopy = 4;     // int4 words of the q8 row per thread: rows up to 32768 inputs
+  constexpr int kSide = 2;     // loads of a row pair besides its steps: bias and residual base
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int chunks = (sh.n + kChunk - 1) / kChunk;
+  int4* lds_q = reinterpret_cast<int4*>(lds_raw);  // quad w of chunk u at w*C + u
+  int* lds_x = reinterpret_cast<int*>(lds_raw + (size_t)chunks * kChunk);
+  const int4* gq = reinterpret_cast<const int4*>(in.q8_in);
+  const int tid = threadIdx.x;
+  const int sub = tid & 63;  // 64 lanes per row: lane = sub, one row slot per wave
+  const int waves = gridDim.x * (kBlock / 64);
+  const int words = chunks * 4;
+  constexpr bool kScales = EPI != kPartials;  // the partials export passes no scales
+  const float sx = kScales ? *in.scale_in : 1.0f;
+
+  // Loads that a layout does not need still go out, from the first bytes of
+  // the packed matrix (the one operand every entry point passes), so that the
+  // count of loads per step stays fixed.
+  auto issue_step = [&](RowStep& st, int row_pair, int step) {
+    const int u = min(step * 64 + sub, chunks - 1);
+    const int r0 = min(row_pair * kRows, sh.rows - 1), r1 = min(row_pair * kRows + 1, sh.rows - 1);
+    const int own = (sub & 1) ? r1 : r0;
+    st.w0 = load_b128(packed + (size_t)r0 * sh.row_bytes + (size_t)u * 16);
+    st.w1 = load_b128(packed + (size_t)r1 * sh.row_bytes + (size_t)u * 16);
+    st.s = load_u16(kScales ? static_cast<const void*>(scales + (size_t)own * sh.groups + (u >> 1))
+                            : static_cast<const void*>(packed));
+  };
+  // Bias and residual base of the lane's own row.
+  auto issue_side = [&](int row_pair, int& b, int& base) {
+    const int own = min(row_pair * kRows + (sub & 1), sh.rows - 1);
+    b = load_b32(bias != nullptr ? static_cast<const void*>(bias + own) : static_cast<const void*>(packed));
+    base = load_b32(EPI == kResidual ? static_cast<const void*>(output + own) : static_cast<const void*>(packed));
+  };
+
+  v4i32 qv[kCopy];
+#pragma unroll
+  for (int k = 0; k < kCopy; ++k) qv[k] = load_b128(gq + min(k * kBlock + tid, words - 1));
+  int xv = load_b32(in.xsum_in + min(tid, chunks - 1));
+
+  RowStep st[STEPS];
+  int it = blockIdx.x * (kBlock / 64) + (tid >> 6);
+  int b_cur, base_cur;
+  issue_side(it, b_cur, base_cur);
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) issue_step(st[s], it, s);
+
+  asm volatile("s_waitcnt vmcnt(%5)"
+               : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv)
+               : "n"(kSide + 3 * STEPS)
+               : "memory");
+  int4* dump = reinterpret_cast<int4*>(lds_raw + rows_dump_offset(chunks));
+#pragma unroll
+  for (int k = 0; k < kCopy; ++k) {
+    const int e = k * kBlock + tid;
+    *reinterpret_cast<v4i32*>(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = qv[k];
+  }
+  *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = xv;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  const int4 qr_unused[1][4] = {};
+  const int xr_unused[1] = {0};
+  while (it < sh.iters) {
+    const int row0 = it * kRows;
+    const int it_next = it + waves;
+    int b_next, base_next;
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      if (s == 0) {
+        asm volatile("s_waitcnt vmcnt(%5)"
+                     : "+v"(st[0].w0), "+v"(st[0].w1), "+v"(st[0].s), "+v"(b_cur), "+v"(base_cur)
+                     : "n"(3 * (STEPS - 1))
+                     : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(%3)"
+                     : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
+                     : "n"(3 * (STEPS - 1) + kSide)
+                     : "memory");
+      }
+      Step<1> view;
+      view.w[0][0] = __builtin_bit_cast(uint4, st[s].w0);
+      view.w[0][1] = __builtin_bit_cast(uint4, st[s].w1);
+      view.s[0] = (uint16_t)st[s].s;
+      compute_step<EPI, 1, false, 64, EXACT>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0, s,
+                                             sub, chunks);
+      if (s == 0) issue_side(it_next, b_next, base_next);
+      issue_step(st[s], it_next, s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EPI != kPartials) {
+      for (int offset = 2; offset < 64; offset <<= 1) acc = acc + __shfl_xor(acc, offset);
+      const int row = row0 + (sub & 1);
+      float y = acc * sx;
+      if (bias != nullptr) y = y + __int_as_float(b_cur);
+      if constexpr (EPI == kSiluPair) {
+        const float up = __int_as_float(pair_swap(__float_as_int(y)));
+        if (sub == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y) * up;
+      } else if (sub < 2 && row < sh.rows) {
+        if constexpr (EPI == kStore) output[row] = y;
+        else output[row] = __int_as_float(base_cur) + y;
+      }
+    }
+    b_cur = b_next;
+    base_cur = base_next;
+    it = it_next;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the refills of the pass past the end
+}
+
 int device_cus() {
   static int cached[64] = {0};
   int device = 0;
@@ -348,6 +509,21 @@ bool launch_layout(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, con
   return false;
 }
 
+template <int EPI, int STEPS>
+void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int /*blocks*/,
+                 size_t /*lds*/) {
+  size_t lds;
+  const int cus = device_cus();
+  const int blocks = ceil_div(sh.iters, 8) < cus ? ceil_div(sh.iters, 8) : cus;
+  lds = (size_t)rows_dump_offset((sh.n + kChunk - 1) / kChunk) + 16;
+  if (sh.exact)
+    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, true>), dim3(blocks), dim3(512), lds, stream, p, a.packed,
+                       a.scales, a.bias, a.output, a.partials, sh);
+  else
+    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, false>), dim3(blocks), dim3(512), lds, stream, p, a.packed,
+                       a.scales, a.bias, a.output, a.partials, sh);
+}
+
 // Steps per pipeline item: a whole row of up to two steps (q8 in registers),
 // else the largest of 4, 2, 1 that divides the row's steps (no dead steps).
 int steps_per_item(int steps) {
@@ -366,6 +542,17 @@ hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, c
     if (nj == 1) launched = launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
     else launched = launch_layout<MODE, EPI, FUSED, 2, false>(stream, p, a, sh, blocks, lds);
   } else if constexpr (!FUSED) {
+    if (sh.lanes == 64 && steps <= 8) {
+      switch (steps) {
+        case 3: launch_rows<EPI, 3>(stream, p, a, sh, blocks, lds); break;
+        case 4: launch_rows<EPI, 4>(stream, p, a, sh, blocks, lds); break;
+        case 5: launch_rows<EPI, 5>(stream, p, a, sh, blocks, lds); break;
+        case 6: launch_rows<EPI, 6>(stream, p, a, sh, blocks, lds); break;
+        case 7: launch_rows<EPI, 7>(stream, p, a, sh, blocks, lds); break;
+        default: launch_rows<EPI, 8>(stream, p, a, sh, blocks, lds); break;
+      }
+      return hipGetLastError();
+    }
     if (nj == 4) launched = launch_layout<MODE, EPI, FUSED, 4, true>(stream, p, a, sh, blocks, lds);
     else if (nj == 2) launched = launch_layout<MODE, EPI, FUSED, 2, true>(stream, p, a, sh, blocks, lds);
     else launched = launch_layout<MODE, EPI, FUSED, 1, true>(stream, p, a, sh, blocks, lds);
