@@ -515,7 +515,7 @@ def main() -> None:
             "traffic": None if not traffic or "error" in traffic else round(traffic["bytes_per_launch"]),
             "traffic_detail": traffic,
             "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
-            "kernel": "gemv_kernel (pre-quantized activations)",
+            "kernel": "gemv_kernel at K=8192, gemv_rows_kernel at K=28672 (pre-quantized activations)",
             "read_ceiling": ceiling,
             "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 4),
             "copy_bandwidth": copy,
