@@ -371,6 +371,7 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 }  // namespace
 
 int gemm_splits(int m, int rows, int n) {
+  if (m > 32 && gemm_split_applies(m, rows, n)) return 4;
   const int splits = skinny_splits(m, rows, n, (size_t)max_lds_per_block());
   return splits > 0 ? splits : 1;
 }
@@ -385,6 +386,7 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
       ((long long)a.rows + 256) * a.row_bytes >= limit || ((long long)a.rows + 256) * a.groups * 2 >= limit)
     return hipErrorInvalidValue;
   if (gemm_wide_applies(a.m, a.rows)) return launch_gemm_wide(stream, a);
+  if (gemm_split_applies(a.m, a.rows, a.n)) return launch_gemm_split(stream, a);
   switch (a.epi) {
     case kStore: return launch_epi<kStore>(stream, a);
     case kResidual: return launch_epi<kResidual>(stream, a);

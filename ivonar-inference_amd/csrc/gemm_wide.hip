@@ -388,6 +388,265 @@ hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a) {
   return launch_wide_shape<EPI, 8, 4>(stream, a);
 }
 
+// Split-K variant for long prompts with few output rows (K=4096 -> N=1024 at
+// M=2048 has only 64 tiles of 128 x 256): a block of four waves owns one
+// 128-token x 64-row output tile and wave w walks the contiguous group range
+// [w*per, (w+1)*per), per = ceil(G/4).  Each wave stages its own operands
+// (its own two-stage ring of direct-to-LDS loads, no block barrier in the
+// loop: no other wave reads them) and runs the same fixed-order MFMA/fold
+// units as gemm_wide_kernel.  The four partial tiles are then added in wave
+// order through LDS - the order the CPU oracle restates as orc_gemm_split(4):
+// each range an fmaf chain, total = ((s0 + s1) + s2) + s3 - scaled by s_x and
+// biased, and stored as 16-byte vectors.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitTokens = 128;
+constexpr int kSplitRows = 64;
+constexpr int kSplitStage = kSplitTokens * 128 + kSplitRows * 32;  // A then B, one group
+constexpr int kSplitDmaA = kSplitTokens * 8 / 64;                  // 16-byte pieces per lane and group
+constexpr int kSplitPitch = 68;                                    // floats per token row of a partial tile
+
+template <int EPI>
+__global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8_t* __restrict__ q8,
+                                                                     const float* __restrict__ scale_in,
+                                                                     const uint8_t* __restrict__ packed,
+                                                                     const uint16_t* __restrict__ scales,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ output, GemmArgs a) {
+  constexpr int MT = kSplitTokens / 16;
+  __shared__ __align__(16) unsigned char stages[kSplitWaves][2][kSplitStage];
+  __shared__ __align__(16) int seeds[kSplitWaves][2][kSplitTokens];
+  __shared__ __align__(16) float row_scales[kSplitWaves][2][kSplitRows];
+  static_assert(kSplitWaves * kSplitTokens * kSplitPitch * 4 <= (int)sizeof(stages), "partial tiles fit");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, kb = lane >> 4;
+  const int chunks = (a.n + kChunk - 1) / kChunk;
+  const int groups = (a.n + kGroup - 1) / kGroup;
+  const int q8_stride = chunks * kChunk;
+  const int token0 = blockIdx.y * kSplitTokens;
+  const int row0 = blockIdx.x * kSplitRows;
+  const int per = (groups + kSplitWaves - 1) / kSplitWaves;
+  const int g_begin = min(wave * per, groups), g_end = min(g_begin + per, groups);
+  constexpr int kPast = 0x7FFFFFF0;
+
+  const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
+  const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
+  const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
+  const v4u x_buf = wide_buffer(a.xsum_in, (long long)a.m * chunks * 4);
+
+  // A piece j of a lane: slot j*64 + lane = token 8j + (lane >> 3), piece
+  // (lane & 7) ^ swz(token), where swz(8j + (lane >> 3)) = (lane >> 3) ^ (j & 1).
+  int a_base[2], a_second[2];
+#pragma unroll
+  for (int parity = 0; parity < 2; ++parity) {
+    const int p = (lane & 7) ^ (lane >> 3) ^ parity;
+    a_base[parity] = (token0 + (lane >> 3)) * q8_stride + p * 16;
+    a_second[parity] = p >= 4;
+  }
+  const int a_step = 8 * q8_stride;  // next DMA round: 8 tokens on
+  const int b_off = (row0 + lane) * a.row_bytes;
+  const int x_off0 = (token0 + lane) * chunks * 4, x_off1 = (token0 + 64 + lane) * chunks * 4;
+  const int s_off = (row0 + lane) * a.groups * 2;
+
+  auto dma = [&](int g, int stage) {
+    const bool second_live = 2 * g + 1 < chunks;
+    const unsigned base = __builtin_amdgcn_readfirstlane(lds_address(stages[wave][stage]));
+#pragma unroll
+    for (int j = 0; j < kSplitDmaA; ++j) {
+      const int live = a_base[j & 1] + j * a_step;
+      dma16(q8_buf, base + j * 64 * 16, second_live || !a_second[j & 1] ? live : kPast, g * kGroup);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(w_buf, base + kSplitTokens * 128 + j * 64 * 16, b_off + j * 16, g * 32);
+  };
+  struct Side {
+    int x00, x01, x10, x11, s;
+  };
+  auto side_load = [&](int g) {
+    const bool second_live = 2 * g + 1 < chunks;
+    Side r;
+    r.x00 = load_b32(x_buf, x_off0, g * 8);
+    r.x01 = load_b32(x_buf, second_live ? x_off0 + 4 : kPast, g * 8);
+    r.x10 = load_b32(x_buf, x_off1, g * 8);
+    r.x11 = load_b32(x_buf, second_live ? x_off1 + 4 : kPast, g * 8);
+    r.s = load_u16(s_buf, s_off, g * 2);
+    return r;
+  };
+  // Every load of the wave retired: the side values arrived and the stage
+  // just filled is complete.
+  auto side_store = [&](Side& r, int stage) {
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(r.x00), "+v"(r.x01), "+v"(r.x10), "+v"(r.x11), "+v"(r.s)::"memory");
+    seeds[wave][stage][lane] = -(r.x00 + r.x01);
+    seeds[wave][stage][64 + lane] = -(r.x10 + r.x11);
+    row_scales[wave][stage][lane] = h2f((uint16_t)r.s);
+  };
+
+  float acc[MT][4][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.0f;
+  v4i prev[4];
+  float prev_sc[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    prev[nt] = v4i{0, 0, 0, 0};
+    prev_sc[nt] = 0.0f;
+  }
+  const int b_read = ((kb >> 1) * kSplitRows + col) * 16 + (kb & 1) * 8;
+
+  auto step = [&](int cur, int fill, int g_fill) {
+    Side side = side_load(g_fill);
+    dma(g_fill, fill);
+    const unsigned char* base = stages[wave][cur];
+    uint2 w[4];
+    float sc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      w[nt] = *reinterpret_cast<const uint2*>(base + kSplitTokens * 128 + b_read + nt * 16 * 16);
+      sc[nt] = row_scales[wave][cur][col + nt * 16];
+    }
+    auto operands = [&](int mt, v4i& a0, v4i& a1, v4i& seed) {
+      const int t = mt * 16 + col;
+      const unsigned char* arow = base + t * 128;
+      a0 = *reinterpret_cast<const v4i*>(arow + (((2 * kb) ^ a_swizzle(t)) * 16));
+      a1 = *reinterpret_cast<const v4i*>(arow + (((2 * kb + 1) ^ a_swizzle(t)) * 16));
+      seed = *reinterpret_cast<const v4i*>(&seeds[wave][cur][mt * 16 + 4 * kb]);
+    };
+    v4i a0, a1, seed;
+    operands(0, a0, a1, seed);
+    v4i bf[2][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      v4i na0, na1, nseed;
+      if (mt + 1 < MT) operands(mt + 1, na0, na1, nseed);
+      const int fold_row = mt == 0 ? MT - 1 : mt - 1;
+      v4i p[4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int h = u >> 2, nt = u & 3;
+        if (mt == 0) {
+          const unsigned x = h ? w[nt].y : w[nt].x;
+          bf[h][nt] = v4i{(int)(x & kLow2), (int)((x >> 2) & kLow2), (int)((x >> 4) & kLow2), (int)((x >> 6) & kLow2)};
+        }
+        p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : seed, 0, 0, 0);
+        const int ft = u >> 1, fi = (u & 1) * 2;
+        acc[fold_row][ft][fi] = __builtin_fmaf((float)prev[ft][fi], prev_sc[ft], acc[fold_row][ft][fi]);
+        acc[fold_row][ft][fi + 1] = __builtin_fmaf((float)prev[ft][fi + 1], prev_sc[ft], acc[fold_row][ft][fi + 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) prev[nt] = p[nt];
+      if (mt == 0) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) prev_sc[nt] = sc[nt];
+      }
+      if (mt + 1 < MT) {
+        a0 = na0;
+        a1 = na1;
+        seed = nseed;
+      }
+    }
+    side_store(side, fill);
+  };
+
+  if (g_begin < g_end) {
+    {
+      Side s0 = side_load(g_begin);
+      dma(g_begin, 0);
+      side_store(s0, 0);
+    }
+    int cur = 0;
+    for (int g = g_begin; g < g_end; ++g) {
+      step(cur, cur ^ 1, min(g + 1, g_end - 1));
+      cur ^= 1;
+    }
+  }
+  // The last row of tiles; a wave without groups folds zeros.
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[MT - 1][nt][i] = __builtin_fmaf((float)prev[nt][i], prev_sc[nt], acc[MT - 1][nt][i]);
+
+  // Partial tiles of the four waves into LDS (the stages are free once every
+  // wave is here), then wave w finishes tokens 32w .. 32w + 31.
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float* tiles = reinterpret_cast<float*>(&stages[0][0][0]);
+  float* own = tiles + wave * kSplitTokens * kSplitPitch;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) own[(mt * 16 + 4 * kb + i) * kSplitPitch + nt * 16 + col] = acc[mt][nt][i];
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  const bool has_bias = bias != nullptr;
+  const int r4 = (lane & 15) * 4;
+  const int row = row0 + r4;  // first of the lane's four rows (a multiple of 4)
+  float bv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) bv[k] = (has_bias && row + k < a.rows) ? bias[row + k] : 0.0f;
+  const bool rows_whole = row + 3 < a.rows;
+  const uintptr_t base_addr = reinterpret_cast<uintptr_t>(output);
+  const bool vec4 = (a.out_stride & 3) == 0 && (base_addr & 15) == 0;
+  const bool vec2 = (a.out_stride & 1) == 0 && (base_addr & 7) == 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int tl = wave * 32 + j * 4 + (lane >> 4);
+    const int t = token0 + tl;
+    f4v total = *reinterpret_cast<const f4v*>(tiles + tl * kSplitPitch + r4);
+#pragma unroll
+    for (int w = 1; w < kSplitWaves; ++w)
+      total = total + *reinterpret_cast<const f4v*>(tiles + (w * kSplitTokens + tl) * kSplitPitch + r4);
+    if (t >= a.m) continue;
+    const float sx = scale_in[t];
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      y[k] = total[k] * sx;
+      if (has_bias) y[k] = y[k] + bv[k];
+    }
+    float* orow = output + (size_t)t * a.out_stride;
+    if constexpr (EPI == kSiluPair) {
+      const float p0 = ivo_silu(y[0]) * y[1], p1 = ivo_silu(y[2]) * y[3];
+      if (rows_whole && vec2) {
+        __builtin_nontemporal_store(f2v{p0, p1}, reinterpret_cast<f2v*>(orow + (row >> 1)));
+      } else {
+        if (row + 1 < a.rows) orow[row >> 1] = p0;
+        if (row + 3 < a.rows) orow[(row >> 1) + 1] = p1;
+      }
+    } else if (rows_whole && vec4) {
+      f4v* dst = reinterpret_cast<f4v*>(orow + row);
+      if constexpr (EPI == kResidual) {
+        const f4v o = *dst;
+        __builtin_nontemporal_store(f4v{o.x + y[0], o.y + y[1], o.z + y[2], o.w + y[3]}, dst);
+      } else {
+        __builtin_nontemporal_store(f4v{y[0], y[1], y[2], y[3]}, dst);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (row + k < a.rows) {
+          if constexpr (EPI == kResidual) orow[row + k] = orow[row + k] + y[k];
+          else orow[row + k] = y[k];
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+hipError_t launch_split_epi(hipStream_t stream, const GemmArgs& a) {
+  const dim3 grid(ceil_div(a.rows, kSplitRows), ceil_div(a.m, kSplitTokens));
+  hipLaunchKernelGGL((gemm_split_kernel<EPI>), grid, dim3(64 * kSplitWaves), 0, stream, a.q8_in, a.scale_in,
+                     a.packed, a.scales, a.bias, a.output, a);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Measured on MI355X against the 64 x 64-wave-tile kernel (random operands):
@@ -404,6 +663,24 @@ hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
     case kStore: return launch_wide_epi<kStore>(stream, a);
     case kResidual: return launch_wide_epi<kResidual>(stream, a);
     case kSiluPair: return launch_wide_epi<kSiluPair>(stream, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// The split-K tiling for prompts that the 128 x 256 tiling leaves with too
+// few blocks: at least 32 tiles of 128 tokens x 64 rows and at least 4
+// groups per wave.  Measured: K=4096 -> N=1024 at M=2048 25.0 us against
+// 45.4 us for the 64 x 64-wave-tile kernel.
+bool gemm_split_applies(int m, int rows, int n) {
+  const long long tiles = (long long)ceil_div(rows, kSplitRows) * ceil_div(m, kSplitTokens);
+  return m >= 128 && !gemm_wide_applies(m, rows) && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
+}
+
+hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a) {
+  switch (a.epi) {
+    case kStore: return launch_split_epi<kStore>(stream, a);
+    case kResidual: return launch_split_epi<kResidual>(stream, a);
+    case kSiluPair: return launch_split_epi<kSiluPair>(stream, a);
     default: return hipErrorInvalidValue;
   }
 }

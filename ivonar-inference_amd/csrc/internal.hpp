@@ -96,6 +96,10 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a);
 // order as the tiled GEMM.
 bool gemm_wide_applies(int m, int rows);
 hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a);
+// Long-prompt token GEMM split four ways along K (few output rows); its fp32
+// order is four contiguous group ranges added in order.
+bool gemm_split_applies(int m, int rows, int n);
+hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a);
 
 // K-splits of the GEMM for m tokens (its fp32 order: S contiguous group ranges,
 // each an fmaf chain, added in order); 1 = one chain over all groups.

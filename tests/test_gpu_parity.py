@@ -500,3 +500,55 @@ def test_gemm_wide_tiles_epilogues(cuda, oracle, epilogue):
                                  len(sample), 1)
     assert_bits_equal(to_np(out)[sample], expected, epilogue)
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
+
+
+# Long prompts with few output rows run the split-K kernel (four waves per 128 x 64 tile, each a
+# contiguous quarter of the groups, added in order): its plan reports 4 splits.  Ragged tokens and
+# rows, an odd chunk count with a group count not divisible by four, bias, and both epilogues.
+@pytest.mark.parametrize("m,k,rows,bias", [(1000, 4160, 1000, True), (2048, 2048, 1024, False),
+                                          (2048, 4096, 1024, True)])
+def test_gemm_split_k_edges(cuda, oracle, m, k, rows, bias):
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(m * 3 + k + rows)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=bias)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    assert runtime.gemm_plan(m, rows, k) == 4
+    sample = np.unique(np.array([0, 1, 31, 32, 95, 127, 128, 129, m // 2, m - 2, m - 1]) % m)
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), 4)
+    assert_bits_equal(y[sample], expected, "sampled tokens (4 splits)")
+    ref = oracle.reforder(T.EPI_STORE, True, eq8, exsum, esx, packed, scale_bits, b,
+                          np.zeros((len(sample), rows), np.float32), k, reference_lanes(k, rows), rows, len(sample))
+    assert_within(y[sample], ref, what="split-K GEMM vs reference-kernel order")
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_gemm_split_k_epilogues(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(95 if epilogue == "residual" else 94)
+    m, k, rows = 256, 4096, 4096
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    width = rows if epilogue == "residual" else rows // 2
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    assert runtime.gemm_plan(m, rows, k) == 4
+    sample = np.array([0, 7, 127, 128, 200, 255])
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
+                                 len(sample), 4)
+    assert_bits_equal(to_np(out)[sample], expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
