@@ -371,15 +371,15 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 }  // namespace
 
 int gemm_splits(int m, int rows, int n) {
-  if (m > 32 && gemm_split_applies(m, rows, n)) return 4;
-  const int splits = skinny_splits(m, rows, n, (size_t)max_lds_per_block());
-  return splits > 0 ? splits : 1;
+  if (gemm_split_applies(m, rows, n)) return 4;
+  const SkinnyPlan plan = skinny_plan(m, rows, n, (size_t)max_lds_per_block());
+  return plan.splits > 0 ? plan.splits : 1;
 }
 
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (a.rows <= 0 || a.m <= 0) return hipSuccess;
-  const int splits = skinny_splits(a.m, a.rows, a.n, (size_t)max_lds_per_block());
-  if (splits > 0) return launch_skinny(stream, a, splits);
+  const SkinnyPlan plan = skinny_plan(a.m, a.rows, a.n, (size_t)max_lds_per_block());
+  if (plan.splits > 0) return launch_skinny(stream, a, plan);
   // Buffer offsets are 32-bit: every operand (with a tile of slack) stays below 2 GiB.
   const long long limit = 0x7FFFFFF0LL;
   if (((long long)a.m + 256) * ceil_div(a.n, kChunk) * kChunk >= limit ||

@@ -2,24 +2,29 @@
 // short-prefill shapes, where a tile of 64+ tokens would idle most of the
 // MFMA work and leave most CUs without a block.
 //
-// A block owns 16 weight rows and S waves; wave s walks the contiguous group
-// range [s*GS, min((s+1)*GS, G)), GS = ceil(G/S), so the matrix is streamed by
-// (rows/16) * S waves.  Per 128-input group a lane (c = lane % 16, kb =
-// lane / 16) loads the 8 packed bytes of words 2kb, 2kb+1 of weight row c and
-// expands them to signed int8 codes (one v_perm_b32 table lookup per 4
-// codes): the B operands of two v_mfma_i32_16x16x64_i8.  The A operands are
-// the q8 bytes of the same words for token c of each 16-token tile, read
-// straight from global memory (32 contiguous bytes per lane and group), so
-// no stage, copy or barrier precedes the first MFMA.  All loads are
-// unconditional, with addresses clamped into the operands, and go out
-// kStage groups ahead, double buffered; the second chunk of the last group
-// of an odd chunk count is masked to zero on the A side (its weight bytes
-// may then be anything).
+// A wave owns R tiles of 16 weight rows (16R rows) and 16*MT tokens; the S
+// waves of a block share those rows and walk the contiguous group ranges
+// [s*GS, min((s+1)*GS, G)), GS = ceil(G/S).  Per 128-input group a lane
+// (c = lane % 16, kb = lane / 16) loads, for each row tile, the 8 packed
+// bytes of words 2kb, 2kb+1 of its row c and expands them to signed int8
+// codes (one v_perm_b32 table lookup per 4 codes): the B operands of two
+// v_mfma_i32_16x16x64_i8.  The A operands are the q8 bytes of the same words
+// for token c of each 16-token tile, read straight from global memory (32
+// contiguous bytes per lane and group) and used by all R row tiles: the
+// token operand is re-read from the caches once per 16R rows, which is what
+// bounds this kernel when R = 1 (at 32 tokens the token bytes read per group
+// are 8x the weight bytes).  All loads are unconditional, with addresses
+// clamped into the operands, and go out one stage of groups ahead, double
+// buffered; the second chunk of the last group of an odd chunk count is
+// masked to zero on the A side (its weight bytes may then be anything).
 //
 // fp32 order (restated by the CPU oracle as orc_gemm_split): each wave folds
 // its groups' exact int32 tiles into fp32 with one fmaf per output in
-// ascending group order; the S partial sums are then added in wave order
-// through LDS, and the token scale and bias applied.
+// ascending group order; the S partial tiles go through LDS and are added in
+// wave order, then the token scale and the bias are applied.  The whole block
+// shares that epilogue: thread i finishes outputs i, i + 64S, ... of the tile
+// (rows fastest), so the stores are contiguous runs of 16R floats.
+#include "buffer_ops.hpp"
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -29,28 +34,36 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr unsigned kSignedLut = 0x000100FFu;  // v_perm table: code 0 -> -1, 1 -> 0, 2 -> +1
-constexpr int kMaxSplits = 16;  // 1024-thread blocks; two token tiles stop at 8 (register budget)
 
 __device__ __forceinline__ unsigned signed_codes(unsigned w, int k) {
   return __builtin_amdgcn_perm(0u, kSignedLut, (w >> (2 * k)) & kLow2);
 }
 
-template <int MT>
+template <int MT, int R>
 struct SkinnyStage {
-  static constexpr int kGroups = MT == 1 ? 4 : 2;  // groups per stage (register budget)
-  uint2 w[kGroups];
-  uint16_t s[kGroups];
+  static constexpr int kGroups = (MT == 1 && R <= 2) ? 4 : 2;  // groups per stage (register budget)
+  uint2 w[kGroups][R];
+  uint16_t s[kGroups][R];
   v4i a[kGroups][MT][2];
 };
 
-template <int EPI, int MT, int S>
+// Partial tiles in LDS: [wave][token][row], row pitch 16R + 4 floats (the
+// four kb lane groups of a fold land on distinct banks).
+template <int MT, int R>
+struct SkinnyRed {
+  static constexpr int kPitch = 16 * R + 4;
+  static constexpr int kWaveFloats = 16 * MT * kPitch;
+};
+
+template <int EPI, int MT, int R, int S>
 __global__ __launch_bounds__(64 * S) void skinny_kernel(const int8_t* __restrict__ q8,
                                                         const float* __restrict__ scale_in,
                                                         const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
                                                         const float* __restrict__ bias,
                                                         float* __restrict__ output, GemmArgs a) {
-  using Stage = SkinnyStage<MT>;
+  using Stage = SkinnyStage<MT, R>;
+  using Red = SkinnyRed<MT, R>;
   constexpr int kStage = Stage::kGroups;
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -61,13 +74,18 @@ __global__ __launch_bounds__(64 * S) void skinny_kernel(const int8_t* __restrict
   const int groups = (a.n + kGroup - 1) / kGroup;
   // The last group lacks its second chunk (lanes kb >= 2) when the chunk count is odd.
   const int short_group = (chunks & 1) ? groups - 1 : groups;
-  const int row0 = blockIdx.x * 16;
-  const int row = min(row0 + col, a.rows - 1);
+  const int row0 = blockIdx.x * 16 * R;
   const int per_wave = (groups + S - 1) / S;
   const int g_begin = min(s * per_wave, groups);
   const int g_end = min(g_begin + per_wave, groups);
-  const uint8_t* wrow = packed + (size_t)row * a.row_bytes;
-  const uint16_t* srow = scales + (size_t)row * a.groups;
+  const uint8_t* wrow[R];
+  const uint16_t* srow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r * 16 + col, a.rows - 1);
+    wrow[r] = packed + (size_t)row * a.row_bytes;
+    srow[r] = scales + (size_t)row * a.groups;
+  }
   const size_t q8_stride = (size_t)chunks * kChunk;
   const int8_t* arow[MT];
 #pragma unroll
@@ -78,51 +96,64 @@ __global__ __launch_bounds__(64 * S) void skinny_kernel(const int8_t* __restrict
     for (int j = 0; j < kStage; ++j) {
       const int g = min(first + j, groups - 1);
       const bool dead = g == short_group && kb >= 2;  // read the group's first chunk instead
-      st.w[j] = *reinterpret_cast<const uint2*>(wrow + (size_t)g * 32 + (dead ? 0 : kb * 8));
-      st.s[j] = srow[g];
       const size_t offset = (size_t)g * kGroup + (dead ? 0 : kb * 32);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         st.a[j][mt][0] = *reinterpret_cast<const v4i*>(arow[mt] + offset);
         st.a[j][mt][1] = *reinterpret_cast<const v4i*>(arow[mt] + offset + 16);
       }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        st.w[j][r] = *reinterpret_cast<const uint2*>(wrow[r] + (size_t)g * 32 + (dead ? 0 : kb * 8));
+        st.s[j][r] = srow[r][g];
+      }
     }
   };
 
-  float acc[MT][4];
+  float acc[MT][R][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][r][i] = 0.0f;
 
   auto compute_stage = [&](const Stage& st, int first) {
 #pragma unroll
     for (int j = 0; j < kStage; ++j) {
       const int g = first + j;
       if (g >= g_end) break;  // wave-uniform
-      v4i b0, b1;
-      b0.x = (int)signed_codes(st.w[j].x, 0);
-      b0.y = (int)signed_codes(st.w[j].x, 1);
-      b0.z = (int)signed_codes(st.w[j].x, 2);
-      b0.w = (int)signed_codes(st.w[j].x, 3);
-      b1.x = (int)signed_codes(st.w[j].y, 0);
-      b1.y = (int)signed_codes(st.w[j].y, 1);
-      b1.z = (int)signed_codes(st.w[j].y, 2);
-      b1.w = (int)signed_codes(st.w[j].y, 3);
-      const float scale = h2f(st.s[j]);
       const int keep = (g == short_group && kb >= 2) ? 0 : -1;
+      v4i a0[MT], a1[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        v4i a0 = st.a[j][mt][0], a1 = st.a[j][mt][1];
+        a0[mt] = st.a[j][mt][0];
+        a1[mt] = st.a[j][mt][1];
         if (g == short_group) {  // wave-uniform
-          a0 &= keep;
-          a1 &= keep;
+          a0[mt] &= keep;
+          a1[mt] &= keep;
         }
-        const v4i zero = {0, 0, 0, 0};
-        v4i p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, zero, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, p, 0, 0, 0);
+      }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][i] = __builtin_fmaf((float)p[i], scale, acc[mt][i]);
+      for (int r = 0; r < R; ++r) {
+        v4i b0, b1;
+        b0.x = (int)signed_codes(st.w[j][r].x, 0);
+        b0.y = (int)signed_codes(st.w[j][r].x, 1);
+        b0.z = (int)signed_codes(st.w[j][r].x, 2);
+        b0.w = (int)signed_codes(st.w[j][r].x, 3);
+        b1.x = (int)signed_codes(st.w[j][r].y, 0);
+        b1.y = (int)signed_codes(st.w[j][r].y, 1);
+        b1.z = (int)signed_codes(st.w[j][r].y, 2);
+        b1.w = (int)signed_codes(st.w[j][r].y, 3);
+        const float scale = h2f(st.s[j][r]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const v4i zero = {0, 0, 0, 0};
+          v4i p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[mt], b0, zero, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[mt], b1, p, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mt][r][i] = __builtin_fmaf((float)p[i], scale, acc[mt][r][i]);
+        }
       }
     }
   };
@@ -137,95 +168,289 @@ __global__ __launch_bounds__(64 * S) void skinny_kernel(const int8_t* __restrict
     compute_stage(bufb, first + kStage);
   }
 
-  // Add the S partial sums in wave order: red[s][mt*16 + 4kb + i][col].
+  // Partial tiles to LDS: lane (col, kb) holds token mt*16 + 4kb + i of row r*16 + col.
   float* red = reinterpret_cast<float*>(smem);
-  if constexpr (S > 1) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[((s * MT + mt) * 16 + 4 * kb + i) * 16 + col] = acc[mt][i];
-    __syncthreads();
-    if (s != 0) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float total = acc[mt][i];
-        for (int w = 1; w < S; ++w) total = total + red[((w * MT + mt) * 16 + 4 * kb + i) * 16 + col];
-        acc[mt][i] = total;
-      }
-  }
-
-  const int out_row = row0 + col;
-  const bool row_live = out_row < a.rows;
-  const float b = (bias != nullptr && row_live) ? bias[out_row] : 0.0f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = mt * 16 + 4 * kb + i;
-      const bool live = row_live && t < a.m;
-      float y = acc[mt][i] * scale_in[min(t, a.m - 1)];
-      if (bias != nullptr) y = y + b;
-      float* orow = output + (size_t)min(t, a.m - 1) * a.out_stride;
-      if constexpr (EPI == kSiluPair) {
-        const float partner = __shfl_xor(y, 1);
-        if (live && (out_row & 1) == 0 && out_row + 1 < a.rows) orow[out_row >> 1] = ivo_silu(y) * partner;
-      } else if constexpr (EPI == kResidual) {
-        if (live) orow[out_row] = orow[out_row] + y;
-      } else {
-        if (live) orow[out_row] = y;
-      }
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[s * Red::kWaveFloats + (mt * 16 + 4 * kb + i) * Red::kPitch + r * 16 + col] = acc[mt][r][i];
+  __syncthreads();
+
+  // Epilogue: output o of the tile is token o / 16R, row o % 16R; wave partials added in order.
+  constexpr int kOutputs = 16 * MT * 16 * R;
+  constexpr int kPerThread = (kOutputs + 64 * S - 1) / (64 * S);
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int o = tid + j * 64 * S;
+    if (kOutputs % (64 * S) != 0 && o >= kOutputs) break;  // whole waves (16R is a multiple of 16)
+    const int t = o / (16 * R), rr = o % (16 * R);
+    const int out_row = row0 + rr;
+    float total = red[t * Red::kPitch + rr];
+#pragma unroll
+    for (int w = 1; w < S; ++w) total = total + red[w * Red::kWaveFloats + t * Red::kPitch + rr];
+    const bool row_live = out_row < a.rows;
+    const bool live = row_live && t < a.m;
+    float y = total * scale_in[min(t, a.m - 1)];
+    if (bias != nullptr) y = y + bias[min(out_row, a.rows - 1)];
+    float* orow = output + (size_t)min(t, a.m - 1) * a.out_stride;
+    if constexpr (EPI == kSiluPair) {
+      const float partner = __shfl_xor(y, 1);
+      if (live && (out_row & 1) == 0 && out_row + 1 < a.rows) orow[out_row >> 1] = ivo_silu(y) * partner;
+    } else if constexpr (EPI == kResidual) {
+      if (live) orow[out_row] = orow[out_row] + y;
+    } else {
+      if (live) orow[out_row] = y;
     }
+  }
 }
 
-size_t skinny_lds(int mt, int splits) { return splits > 1 ? (size_t)splits * 16 * 16 * mt * sizeof(float) : 0; }
+// Token operand staged in LDS once per block (prompts whose whole token tile
+// fits: 16*MT tokens x K bytes).  A block is 8 waves: WR = 8/S row tiles of
+// 16 rows times S contiguous group ranges (the same fp32 order as above).
+// Every wave first sends its share of the token tile to LDS (direct
+// buffer-to-LDS loads of 16 bytes per lane, XOR-swizzled pieces), then loads
+// the packed bytes and scales of all its groups into registers, so that the
+// whole working set of the block is in flight before the first wait; the
+// compute reads the token fragments from LDS.  Tokens past m and the missing
+// second chunk of an odd chunk count read as zeros through the buffer range
+// check; rows past the matrix are clamped and not stored.
+constexpr int kLdsWaves = 8;
 
-template <int EPI, int MT, int S>
-hipError_t launch_skinny_shape(hipStream_t stream, const GemmArgs& a) {
-  const size_t lds = skinny_lds(MT, S);
-  hipLaunchKernelGGL((skinny_kernel<EPI, MT, S>), dim3(ceil_div(a.rows, 16)), dim3(64 * S), lds, stream, a.q8_in,
-                     a.scale_in, a.packed, a.scales, a.bias, a.output, a);
+template <int MT>
+struct LdsTile {
+  static constexpr int kTokens = 16 * MT;
+  static constexpr int kGroupBytes = kTokens * kGroup;  // token bytes of one group
+  static constexpr int kPitch = 20;                     // partial tile row pitch (floats)
+  static constexpr int kRedBytes = kLdsWaves * kTokens * kPitch * 4;
+};
+
+template <int EPI, int MT, int S, int NG>
+__global__ __launch_bounds__(64 * kLdsWaves) void skinny_lds_kernel(const int8_t* __restrict__ q8,
+                                                                    const float* __restrict__ scale_in,
+                                                                    const uint8_t* __restrict__ packed,
+                                                                    const uint16_t* __restrict__ scales,
+                                                                    const float* __restrict__ bias,
+                                                                    float* __restrict__ output, GemmArgs a) {
+  using T = LdsTile<MT>;
+  constexpr int WR = kLdsWaves / S;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wave / S, s = wave % S;
+  const int col = lane & 15, kb = lane >> 4;
+  const int chunks = (a.n + kChunk - 1) / kChunk;
+  const int groups = (a.n + kGroup - 1) / kGroup;
+  const int short_group = (chunks & 1) ? groups - 1 : groups;
+  const int q8_stride = chunks * kChunk;
+  const unsigned a_lds = lds_address(smem);
+  float* red = reinterpret_cast<float*>(smem + groups * T::kGroupBytes);
+
+  // 1. The token tile: instruction q covers group q / (2MT), slots (q % 2MT) * 64 + lane.
+  {
+    constexpr int kPerGroup = 2 * MT;
+    const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
+    constexpr int kPast = 0x7FFFFFF0;
+    for (int q = wave; q < groups * kPerGroup; q += kLdsWaves) {
+      const int g = q / kPerGroup;
+      const int slot = (q % kPerGroup) * 64 + lane;
+      const int t = slot >> 3;
+      const int piece = (slot & 7) ^ a_swizzle(t);
+      const bool dead = g == short_group && piece >= 4;
+      dma16(q8_buf, a_lds + g * T::kGroupBytes + (q % kPerGroup) * 1024,
+            dead ? kPast : t * q8_stride + g * kGroup + piece * 16, 0);
+    }
+  }
+
+  // 2. This wave's weights: row tile blockIdx.x * WR + w, groups [g0, g0 + count).
+  const int per_wave = (groups + S - 1) / S;
+  const int g0 = min(s * per_wave, groups);
+  const int count = min(per_wave, groups - g0);
+  const int row0 = (blockIdx.x * WR + w) * 16;
+  const int row = min(row0 + col, a.rows - 1);
+  const uint8_t* wrow = packed + (size_t)row * a.row_bytes;
+  const uint16_t* srow = scales + (size_t)row * a.groups;
+  uint2 wq[NG];
+  uint16_t sq[NG];
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    const int g = min(g0 + j, groups - 1);
+    const bool dead = g == short_group && kb >= 2;
+    wq[j] = *reinterpret_cast<const uint2*>(wrow + (size_t)g * 32 + (dead ? 0 : kb * 8));
+    sq[j] = srow[g];
+  }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+  float acc[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    if (j >= count) break;  // wave-uniform
+    const int g = g0 + j;
+    v4i b0, b1;
+    b0.x = (int)signed_codes(wq[j].x, 0);
+    b0.y = (int)signed_codes(wq[j].x, 1);
+    b0.z = (int)signed_codes(wq[j].x, 2);
+    b0.w = (int)signed_codes(wq[j].x, 3);
+    b1.x = (int)signed_codes(wq[j].y, 0);
+    b1.y = (int)signed_codes(wq[j].y, 1);
+    b1.z = (int)signed_codes(wq[j].y, 2);
+    b1.w = (int)signed_codes(wq[j].y, 3);
+    const float scale = h2f(sq[j]);
+    const v4i* tile = reinterpret_cast<const v4i*>(smem + g * T::kGroupBytes);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int t = mt * 16 + col;
+      const v4i a0 = tile[t * 8 + ((2 * kb) ^ a_swizzle(t))];
+      const v4i a1 = tile[t * 8 + ((2 * kb + 1) ^ a_swizzle(t))];
+      const v4i zero = {0, 0, 0, 0};
+      v4i p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, zero, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, p, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][i] = __builtin_fmaf((float)p[i], scale, acc[mt][i]);
+    }
+  }
+
+  // 3. Partial tiles [w][s][token][row] to LDS, then the block's epilogue:
+  //    output o is token o / 16WR, row o % 16WR; the S partials added in order.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * T::kTokens + mt * 16 + 4 * kb + i) * T::kPitch + col] = acc[mt][i];
+  __syncthreads();
+  constexpr int kOutputs = T::kTokens * 16 * WR;  // a multiple of 64: whole waves stay active together
+  const int block_row0 = blockIdx.x * WR * 16;
+#pragma unroll
+  for (int j = 0; j < (kOutputs + 64 * kLdsWaves - 1) / (64 * kLdsWaves); ++j) {
+    const int o = tid + j * 64 * kLdsWaves;
+    if (kOutputs % (64 * kLdsWaves) != 0 && o >= kOutputs) break;
+    const int t = o / (16 * WR), rr = o % (16 * WR);
+    const int ww = rr >> 4, c = rr & 15;
+    const int out_row = block_row0 + rr;
+    float total = red[((ww * S) * T::kTokens + t) * T::kPitch + c];
+#pragma unroll
+    for (int k = 1; k < S; ++k) total = total + red[((ww * S + k) * T::kTokens + t) * T::kPitch + c];
+    const bool row_live = out_row < a.rows;
+    const bool live = row_live && t < a.m;
+    float y = total * scale_in[min(t, a.m - 1)];
+    if (bias != nullptr) y = y + bias[min(out_row, a.rows - 1)];
+    float* orow = output + (size_t)min(t, a.m - 1) * a.out_stride;
+    if constexpr (EPI == kSiluPair) {
+      const float partner = __shfl_xor(y, 1);
+      if (live && (out_row & 1) == 0 && out_row + 1 < a.rows) orow[out_row >> 1] = ivo_silu(y) * partner;
+    } else if constexpr (EPI == kResidual) {
+      if (live) orow[out_row] = orow[out_row] + y;
+    } else {
+      if (live) orow[out_row] = y;
+    }
+  }
+}
+
+template <int EPI, int MT, int S, int NG>
+hipError_t launch_skinny_lds_shape(hipStream_t stream, const GemmArgs& a) {
+  using T = LdsTile<MT>;
+  const int groups = ceil_div(a.n, kGroup);
+  const size_t lds = (size_t)groups * T::kGroupBytes + T::kRedBytes;
+  const int rows_per_block = 16 * (kLdsWaves / S);
+  hipLaunchKernelGGL((skinny_lds_kernel<EPI, MT, S, NG>), dim3(ceil_div(a.rows, rows_per_block)), dim3(64 * kLdsWaves),
+                     lds, stream, a.q8_in, a.scale_in, a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
 }
 
-template <int EPI, int MT>
-hipError_t launch_skinny_mt(hipStream_t stream, const GemmArgs& a, int splits) {
+template <int MT, int R>
+constexpr size_t skinny_lds(int splits) {
+  return (size_t)splits * SkinnyRed<MT, R>::kWaveFloats * sizeof(float);
+}
+
+template <int EPI, int MT, int R, int S>
+hipError_t launch_skinny_shape(hipStream_t stream, const GemmArgs& a) {
+  const size_t lds = skinny_lds<MT, R>(S);
+  hipLaunchKernelGGL((skinny_kernel<EPI, MT, R, S>), dim3(ceil_div(a.rows, 16 * R)), dim3(64 * S), lds, stream,
+                     a.q8_in, a.scale_in, a.packed, a.scales, a.bias, a.output, a);
+  return hipGetLastError();
+}
+
+template <int EPI, int MT, int R>
+hipError_t launch_skinny_r(hipStream_t stream, const GemmArgs& a, int splits) {
   switch (splits) {
-    case 1: return launch_skinny_shape<EPI, MT, 1>(stream, a);
-    case 2: return launch_skinny_shape<EPI, MT, 2>(stream, a);
-    case 4: return launch_skinny_shape<EPI, MT, 4>(stream, a);
-    case 8: return launch_skinny_shape<EPI, MT, 8>(stream, a);
-    default:
-      if constexpr (MT == 1) return launch_skinny_shape<EPI, MT, kMaxSplits>(stream, a);
-      return hipErrorInvalidValue;
+    case 1: return launch_skinny_shape<EPI, MT, R, 1>(stream, a);
+    case 2: return launch_skinny_shape<EPI, MT, R, 2>(stream, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int EPI, int MT, int S>
+hipError_t launch_skinny_lds_s(hipStream_t stream, const GemmArgs& a, int ng) {
+  switch (ng) {
+    case 1: return launch_skinny_lds_shape<EPI, MT, S, 1>(stream, a);
+    case 2: return launch_skinny_lds_shape<EPI, MT, S, 2>(stream, a);
+    case 4: return launch_skinny_lds_shape<EPI, MT, S, 4>(stream, a);
+    case 8: return launch_skinny_lds_shape<EPI, MT, S, 8>(stream, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int EPI, int MT>
+hipError_t launch_skinny_mt(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan) {
+  if (plan.lds_groups > 0) {
+    switch (plan.splits) {
+      case 4: return launch_skinny_lds_s<EPI, MT, 4>(stream, a, plan.lds_groups);
+      case 8: return launch_skinny_lds_s<EPI, MT, 8>(stream, a, plan.lds_groups);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (plan.row_tiles) {
+    case 1: return launch_skinny_r<EPI, MT, 1>(stream, a, plan.splits);
+    case 4: return launch_skinny_r<EPI, MT, 4>(stream, a, plan.splits);
+    default: return hipErrorInvalidValue;
   }
 }
 
 template <int EPI>
-hipError_t launch_skinny_epi(hipStream_t stream, const GemmArgs& a, int splits) {
-  return a.m <= 16 ? launch_skinny_mt<EPI, 1>(stream, a, splits) : launch_skinny_mt<EPI, 2>(stream, a, splits);
+hipError_t launch_skinny_epi(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan) {
+  return a.m <= 16 ? launch_skinny_mt<EPI, 1>(stream, a, plan) : launch_skinny_mt<EPI, 2>(stream, a, plan);
+}
+
+size_t skinny_lds_bytes(int m, int n, SkinnyPlan plan) {
+  const int mt = m <= 16 ? 1 : 2;
+  if (plan.lds_groups > 0) return (size_t)ceil_div(n, kGroup) * 16 * mt * kGroup + (size_t)kLdsWaves * 16 * mt * 20 * 4;
+  return (size_t)plan.splits * 16 * mt * (16 * plan.row_tiles + 4) * sizeof(float);
 }
 
 }  // namespace
 
-int skinny_splits(int m, int rows, int n, size_t max_lds) {
-  if (m < 1 || m > 32) return 0;
+// The token tile goes to LDS when it fits there (K up to about 4.4k inputs at
+// 17..32 tokens, 9.4k at 16 or fewer): 8 K-splits of one row tile per block,
+// or 4 K-splits of two row tiles when more than 512 row tiles would make more
+// than two rounds of blocks.  Otherwise the token operand is read from the
+// caches per wave: two K-splits, four row tiles per wave for 8192 rows and
+// more (fewer re-reads of the token operand), one below.
+SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds) {
+  if (m < 1 || m > 32) return {0, 0, 0};
   const int groups = ceil_div(n, kGroup);
   const int tiles = ceil_div(rows, 16);
-  const int mt = m <= 16 ? 1 : 2;
-  const int max_splits = mt == 1 ? kMaxSplits : 8;
-  int splits = 1;
-  while (splits < max_splits && (long long)tiles * splits < 2048 && splits * 2 <= groups) splits *= 2;
-  if (skinny_lds(mt, splits) > max_lds) return 0;
-  return splits;
+  SkinnyPlan plan{tiles > 512 ? 4 : 8, 1, 0};
+  const int per_wave = ceil_div(groups, plan.splits);
+  int ng = 1;
+  while (ng < per_wave) ng *= 2;
+  plan.lds_groups = ng;
+  if (ng <= 8 && skinny_lds_bytes(m, n, plan) <= max_lds) return plan;
+  plan = {groups >= 2 ? 2 : 1, rows >= 8192 ? 4 : 1, 0};
+  return plan;
 }
 
-hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, int splits) {
+hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan) {
+  if (plan.splits < 1 || skinny_lds_bytes(a.m, a.n, plan) > (size_t)max_lds_per_block()) return hipErrorInvalidValue;
   switch (a.epi) {
-    case kStore: return launch_skinny_epi<kStore>(stream, a, splits);
-    case kResidual: return launch_skinny_epi<kResidual>(stream, a, splits);
-    case kSiluPair: return launch_skinny_epi<kSiluPair>(stream, a, splits);
+    case kStore: return launch_skinny_epi<kStore>(stream, a, plan);
+    case kResidual: return launch_skinny_epi<kResidual>(stream, a, plan);
+    case kSiluPair: return launch_skinny_epi<kSiluPair>(stream, a, plan);
     default: return hipErrorInvalidValue;
   }
 }

@@ -34,6 +34,7 @@
 //   minus each token's group sum (seeds the MFMA accumulator so that
 //   sum(code * q) - sum(q) = P comes out exact) and the rows' fp32 scales,
 //   both written from registers one group ahead.
+#include "buffer_ops.hpp"
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -41,54 +42,6 @@ namespace ivo {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef float f2v __attribute__((ext_vector_type(2)));
-
-// Buffer resource over `bytes` bytes (raw, no stride): offsets at or past the
-// size read zeros.  The launcher keeps every operand below 2 GiB.
-__device__ __forceinline__ v4u wide_buffer(const void* base, long long bytes) {
-  const unsigned long long address = (unsigned long long)base;
-  return v4u{(unsigned)address, (unsigned)(address >> 32) & 0xFFFFu, (unsigned)bytes, 0x00020000u};
-}
-
-__device__ __forceinline__ unsigned lds_address(const void* p) {
-  return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// The loads of the main loop are issued as inline assembly, so the compiler
-// inserts no waits for them: it cannot tell which stage a direct-to-LDS load
-// fills and would otherwise wait for every load in flight before the first
-// LDS read of a step.  The kernel places the waits itself (see the loop).
-//
-// One 16-byte piece per lane from a buffer straight into LDS: lane i writes
-// lds_base + 16 * i (lds_base is wave-uniform; M0 is restored afterwards).
-__device__ __forceinline__ void dma16(v4u buffer, unsigned lds_base, int voffset, int soffset) {
-  int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_base), "v"(voffset), "s"(buffer), "s"(soffset)
-      : "memory");
-}
-
-__device__ __forceinline__ int load_b32(v4u buffer, int voffset, int soffset) {
-  int r;
-  asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(r) : "v"(voffset), "s"(buffer), "s"(soffset) : "memory");
-  return r;
-}
-
-__device__ __forceinline__ int load_u16(v4u buffer, int voffset, int soffset) {
-  int r;
-  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(r) : "v"(voffset), "s"(buffer), "s"(soffset) : "memory");
-  return r;
-}
-
-__device__ __forceinline__ int a_swizzle(int t) { return (t & 7) ^ ((t >> 3) & 1); }
 
 template <int MT, int WN>
 struct WideTile {
@@ -667,13 +620,14 @@ hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
   }
 }
 
-// The split-K tiling for prompts that the 128 x 256 tiling leaves with too
-// few blocks: at least 32 tiles of 128 tokens x 64 rows and at least 4
-// groups per wave.  Measured: K=4096 -> N=1024 at M=2048 25.0 us against
-// 45.4 us for the 64 x 64-wave-tile kernel.
+// The split-K tiling for prompts of more than 32 tokens that the 128 x 256
+// tiling leaves with too few blocks: at least 32 tiles of 128 tokens x 64
+// rows and at least 4 groups per wave (a partial token tile reads zeros).
+// Measured: K=4096 -> N=1024 at M=2048 25.0 us and K=4096 -> N=14336 at
+// M=128 22.0 us, against 45.4 and 42.6 us for the 64 x 64-wave-tile kernel.
 bool gemm_split_applies(int m, int rows, int n) {
   const long long tiles = (long long)ceil_div(rows, kSplitRows) * ceil_div(m, kSplitTokens);
-  return m >= 128 && !gemm_wide_applies(m, rows) && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
+  return m > 32 && !gemm_wide_applies(m, rows) && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
 }
 
 hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a) {

@@ -105,8 +105,17 @@ hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a);
 // each an fmaf chain, added in order); 1 = one chain over all groups.
 int gemm_splits(int m, int rows, int n);
 int max_lds_per_block();
-int skinny_splits(int m, int rows, int n, size_t max_lds);  // 0 = does not apply
-hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, int splits);
+// Skinny token GEMM (m <= 32): K-splits (its fp32 order), 16-row tiles per
+// wave and, for the kernel that stages the token tile in LDS, the register
+// slots for groups per wave (0: the token operand is read from the caches);
+// splits == 0 means it does not apply.
+struct SkinnyPlan {
+  int splits;
+  int row_tiles;
+  int lds_groups;
+};
+SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds);
+hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan);
 
 hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const uint8_t* packed,
                         const uint16_t* scales, float* output, int n, int row_bytes, int groups);

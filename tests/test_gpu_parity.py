@@ -454,6 +454,55 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
     assert_within(y[0], truth, what="skinny gemm vs fp64 truth")
 
 
+# The two skinny kernels (M <= 32): the token tile staged in LDS (8 K-splits of one row tile per
+# block, or 4 K-splits of two row tiles past 512 row tiles) and, when the tile does not fit there,
+# the token operand read per wave (one or four row tiles per wave).  Odd chunk counts with several
+# groups, ragged rows, bias; sampled tokens against the oracle's split order.
+@pytest.mark.parametrize("m,k,rows,bias,splits", [(7, 4160, 1000, True, 8), (32, 4160, 1000, False, 8),
+                                                  (20, 1088, 8200, True, 4), (1, 8192, 8192, False, 8),
+                                                  (32, 8192, 8200, False, 2), (17, 8192, 300, True, 2)])
+def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(m * 13 + k + rows)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=bias)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    assert runtime.gemm_plan(m, rows, k) == splits
+    sample = np.unique(np.array([0, 3, 15, 16, m - 1]) % m)
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), splits)
+    assert_bits_equal(y[sample], expected, f"sampled tokens ({splits} splits)")
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_gemm_skinny_two_row_tiles_epilogues(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(97 if epilogue == "residual" else 96)
+    m, k, rows = 24, 1024, 8224
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    width = rows if epilogue == "residual" else rows // 2
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    assert runtime.gemm_plan(m, rows, k) == 4
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m, 4)
+    assert_bits_equal(to_np(out), expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
+
+
 # Long prompts with many row blocks run the 128-token-tile kernel (chosen when m >= 128 and the
 # 128-token x 256-row tiling gives >= 192 blocks): ragged token and row counts, an odd chunk count,
 # a single-chunk K, bias, and every epilogue with a padded output stride.
@@ -505,8 +554,10 @@ def test_gemm_wide_tiles_epilogues(cuda, oracle, epilogue):
 # Long prompts with few output rows run the split-K kernel (four waves per 128 x 64 tile, each a
 # contiguous quarter of the groups, added in order): its plan reports 4 splits.  Ragged tokens and
 # rows, an odd chunk count with a group count not divisible by four, bias, and both epilogues.
+# Prompts of 33..127 tokens fill one partial token tile (the rows past the prompt read zeros).
 @pytest.mark.parametrize("m,k,rows,bias", [(1000, 4160, 1000, True), (2048, 2048, 1024, False),
-                                          (2048, 4096, 1024, True)])
+                                          (2048, 4096, 1024, True), (33, 2048, 2048, False),
+                                          (70, 4096, 14336, True), (127, 2176, 3000, False)])
 def test_gemm_split_k_edges(cuda, oracle, m, k, rows, bias):
     from ivonar_amd import ops, runtime
 
