@@ -29,12 +29,14 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
 // first LDS read that follows; these forms leave the waits to the kernel.
 //
 // One 16-byte piece per lane from a buffer straight into LDS: lane i writes
-// lds_base + 16 * i (lds_base is wave-uniform; M0 is restored afterwards).
+// lds_base + 16 * i (lds_base is wave-uniform; M0 is restored afterwards).  The
+// load reads M0, one wait state after the scalar write of M0.
 __device__ __forceinline__ void dma16(v4u buffer, unsigned lds_base, int voffset, int soffset) {
   int saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
       "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
@@ -45,6 +47,12 @@ __device__ __forceinline__ void dma16(v4u buffer, unsigned lds_base, int voffset
 __device__ __forceinline__ int load_b32(v4u buffer, int voffset, int soffset) {
   int r;
   asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(r) : "v"(voffset), "s"(buffer), "s"(soffset) : "memory");
+  return r;
+}
+
+__device__ __forceinline__ uint2 load_b64(v4u buffer, int voffset, int soffset) {
+  uint2 r;
+  asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen" : "=v"(r) : "v"(voffset), "s"(buffer), "s"(soffset) : "memory");
   return r;
 }
 

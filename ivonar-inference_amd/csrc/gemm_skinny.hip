@@ -24,6 +24,8 @@
 // wave order, then the token scale and the bias are applied.  The whole block
 // shares that epilogue: thread i finishes outputs i, i + 64S, ... of the tile
 // (rows fastest), so the stores are contiguous runs of 16R floats.
+#include <type_traits>
+
 #include "buffer_ops.hpp"
 #include "internal.hpp"
 #include "ternary_device.hpp"
@@ -207,135 +209,177 @@ __global__ __launch_bounds__(64 * S) void skinny_kernel(const int8_t* __restrict
   }
 }
 
-// Token operand staged in LDS once per block (prompts whose whole token tile
-// fits: 16*MT tokens x K bytes).  A block is 8 waves: WR = 8/S row tiles of
-// 16 rows times S contiguous group ranges (the same fp32 order as above).
-// Every wave first sends its share of the token tile to LDS (direct
-// buffer-to-LDS loads of 16 bytes per lane, XOR-swizzled pieces), then loads
-// the packed bytes and scales of all its groups into registers, so that the
-// whole working set of the block is in flight before the first wait; the
-// compute reads the token fragments from LDS.  Tokens past m and the missing
-// second chunk of an odd chunk count read as zeros through the buffer range
-// check; rows past the matrix are clamped and not stored.
-constexpr int kLdsWaves = 8;
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): an unrolled loop whose index
+// can feed an immediate operand.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
 
-template <int MT>
-struct LdsTile {
+// Token operand staged in LDS (prompts whose token bytes for a wave's groups
+// fit: 16*MT tokens x 128 bytes per group).  A block is S waves over the same
+// 16R rows (R row tiles per wave), wave s owning the group range
+// [s*GS, min((s+1)*GS, G)) (the same fp32 order as above).  Each wave sends to
+// its own LDS region the token bytes of its groups (direct buffer-to-LDS
+// loads, 16 bytes per lane, XOR-swizzled pieces) and the fp16 scales of the
+// block's rows from its first group on, and loads the packed bytes of its
+// groups into registers, group by group, so that group j's loads are complete
+// once no more than (NG-1-j) groups' loads are outstanding: step j waits for
+// that count and a barrier (measured on MI355X: a wave that reads the bytes of
+// its own direct-to-LDS load right after the counter reaches them sometimes
+// reads the half of the 64 lanes that is still being written; with the barrier
+// it never did).  The token fragments of a group feed all R row tiles.  Tokens past m and the
+// missing second chunk of an odd chunk count read as zeros through the buffer
+// range check; rows past the matrix are clamped and not stored.
+template <int MT, int R, int S, int NG>
+struct RowTile {
   static constexpr int kTokens = 16 * MT;
   static constexpr int kGroupBytes = kTokens * kGroup;  // token bytes of one group
-  static constexpr int kPitch = 20;                     // partial tile row pitch (floats)
-  static constexpr int kRedBytes = kLdsWaves * kTokens * kPitch * 4;
+  static constexpr int kWaveA = NG * kGroupBytes;
+  static constexpr int kWaveScales = 2048;              // 64 lanes x two 16-byte pieces
+  static constexpr int kWaveBytes = kWaveA + kWaveScales;
+  static constexpr int kLoadsPerGroup = 2 * MT + R;      // DMA pieces + weight loads
+  static constexpr int kPitch = 16 * R + 4;             // partial tile row pitch (floats)
+  static constexpr int kRedBytes = S * kTokens * kPitch * 4;
+  static constexpr int kLdsBytes = S * kWaveBytes > kRedBytes ? S * kWaveBytes : kRedBytes;
+  static_assert(2 + NG * kLoadsPerGroup <= 63, "loads in flight fit the vmcnt counter");
+  static_assert(16 * R <= 64 && NG <= 8, "one scale piece pair per row, eight groups per wave");
 };
 
-template <int EPI, int MT, int S, int NG>
-__global__ __launch_bounds__(64 * kLdsWaves) void skinny_lds_kernel(const int8_t* __restrict__ q8,
-                                                                    const float* __restrict__ scale_in,
-                                                                    const uint8_t* __restrict__ packed,
-                                                                    const uint16_t* __restrict__ scales,
-                                                                    const float* __restrict__ bias,
-                                                                    float* __restrict__ output, GemmArgs a) {
-  using T = LdsTile<MT>;
-  constexpr int WR = kLdsWaves / S;
-  extern __shared__ __align__(16) unsigned char smem[];
+template <int EPI, int MT, int R, int S, int NG>
+__global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __restrict__ q8,
+                                                            const float* __restrict__ scale_in,
+                                                            const uint8_t* __restrict__ packed,
+                                                            const uint16_t* __restrict__ scales,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ output, GemmArgs a) {
+  using T = RowTile<MT, R, S, NG>;
+  __shared__ __align__(16) unsigned char smem[T::kLdsBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = wave / S, s = wave % S;
+  const int s = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, kb = lane >> 4;
   const int chunks = (a.n + kChunk - 1) / kChunk;
   const int groups = (a.n + kGroup - 1) / kGroup;
   const int short_group = (chunks & 1) ? groups - 1 : groups;
   const int q8_stride = chunks * kChunk;
-  const unsigned a_lds = lds_address(smem);
-  float* red = reinterpret_cast<float*>(smem + groups * T::kGroupBytes);
-
-  // 1. The token tile: instruction q covers group q / (2MT), slots (q % 2MT) * 64 + lane.
-  {
-    constexpr int kPerGroup = 2 * MT;
-    const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
-    constexpr int kPast = 0x7FFFFFF0;
-    for (int q = wave; q < groups * kPerGroup; q += kLdsWaves) {
-      const int g = q / kPerGroup;
-      const int slot = (q % kPerGroup) * 64 + lane;
-      const int t = slot >> 3;
-      const int piece = (slot & 7) ^ a_swizzle(t);
-      const bool dead = g == short_group && piece >= 4;
-      dma16(q8_buf, a_lds + g * T::kGroupBytes + (q % kPerGroup) * 1024,
-            dead ? kPast : t * q8_stride + g * kGroup + piece * 16, 0);
-    }
-  }
-
-  // 2. This wave's weights: row tile blockIdx.x * WR + w, groups [g0, g0 + count).
   const int per_wave = (groups + S - 1) / S;
   const int g0 = min(s * per_wave, groups);
   const int count = min(per_wave, groups - g0);
-  const int row0 = (blockIdx.x * WR + w) * 16;
-  const int row = min(row0 + col, a.rows - 1);
-  const uint8_t* wrow = packed + (size_t)row * a.row_bytes;
-  const uint16_t* srow = scales + (size_t)row * a.groups;
-  uint2 wq[NG];
-  uint16_t sq[NG];
+  const int row0 = blockIdx.x * 16 * R;
+  unsigned char* wave_a = smem + s * T::kWaveBytes;
+  unsigned char* wave_scales = wave_a + T::kWaveA;
+  const unsigned a_lds = lds_address(wave_a);
+  const unsigned s_lds = lds_address(wave_scales);
+  constexpr int kPast = 0x7FFFFFF0;
+  const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
+  const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
+  const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
+
+  // Scales: lane l < 16R fetches row row0 + l from group g0 on, 32 bytes from the dword below.
+  const int scale_byte = ((row0 + lane) * a.groups + g0) * 2;
+  const int scale_shift = scale_byte & 3;
+  const bool scale_lane = lane < 16 * R && row0 + lane < a.rows;
+  dma16(s_buf, s_lds, scale_lane ? scale_byte - scale_shift : kPast, 0);
+  dma16(s_buf, s_lds + 1024, scale_lane ? scale_byte - scale_shift + 16 : kPast, 0);
+
+  // Group by group: the token pieces (2MT instructions of 8 tokens), then the R weight loads.
+  uint2 wq[NG][R];
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
     const int g = min(g0 + j, groups - 1);
-    const bool dead = g == short_group && kb >= 2;
-    wq[j] = *reinterpret_cast<const uint2*>(wrow + (size_t)g * 32 + (dead ? 0 : kb * 8));
-    sq[j] = srow[g];
-  }
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-
-  float acc[MT][4];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+    for (int q = 0; q < 2 * MT; ++q) {
+      const int slot = q * 64 + lane;
+      const int t = slot >> 3;
+      const int piece = (slot & 7) ^ a_swizzle(t);
+      const bool dead = (g == short_group && piece >= 4) || q * 8 >= a.m;
+      dma16(q8_buf, a_lds + j * T::kGroupBytes + q * 1024, dead ? kPast : t * q8_stride + g * kGroup + piece * 16, 0);
+    }
+    const bool wdead = g == short_group && kb >= 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NG; ++j) {
-    if (j >= count) break;  // wave-uniform
-    const int g = g0 + j;
-    v4i b0, b1;
-    b0.x = (int)signed_codes(wq[j].x, 0);
-    b0.y = (int)signed_codes(wq[j].x, 1);
-    b0.z = (int)signed_codes(wq[j].x, 2);
-    b0.w = (int)signed_codes(wq[j].x, 3);
-    b1.x = (int)signed_codes(wq[j].y, 0);
-    b1.y = (int)signed_codes(wq[j].y, 1);
-    b1.z = (int)signed_codes(wq[j].y, 2);
-    b1.w = (int)signed_codes(wq[j].y, 3);
-    const float scale = h2f(sq[j]);
-    const v4i* tile = reinterpret_cast<const v4i*>(smem + g * T::kGroupBytes);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int t = mt * 16 + col;
-      const v4i a0 = tile[t * 8 + ((2 * kb) ^ a_swizzle(t))];
-      const v4i a1 = tile[t * 8 + ((2 * kb + 1) ^ a_swizzle(t))];
-      const v4i zero = {0, 0, 0, 0};
-      v4i p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, zero, 0, 0, 0);
-      p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, p, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mt][i] = __builtin_fmaf((float)p[i], scale, acc[mt][i]);
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r * 16 + col, a.rows - 1);
+      wq[j][r] = load_b64(w_buf, row * a.row_bytes + g * 32 + (wdead ? 0 : kb * 8), 0);
     }
   }
 
-  // 3. Partial tiles [w][s][token][row] to LDS, then the block's epilogue:
-  //    output o is token o / 16WR, row o % 16WR; the S partials added in order.
+  float acc[MT][R][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * T::kTokens + mt * 16 + 4 * kb + i) * T::kPitch + col] = acc[mt][i];
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mt][r][i] = 0.0f;
+  static_for<NG>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    // A direct-to-LDS load may still be writing LDS when the counter says it is complete: the
+    // reads of its bytes wait for the counter and then a barrier (every wave passes all NG).
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"((NG - 1 - j) * T::kLoadsPerGroup)
+                 : "memory");
+    if (j >= count) return;  // wave-uniform
+#pragma unroll
+    for (int r = 0; r < R; ++r) asm volatile("" : "+v"(wq[j][r]));
+    const v4i* tile = reinterpret_cast<const v4i*>(wave_a + j * T::kGroupBytes);
+    v4i a0[MT], a1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int t = mt * 16 + col;
+      a0[mt] = tile[t * 8 + ((2 * kb) ^ a_swizzle(t))];
+      a1[mt] = tile[t * 8 + ((2 * kb + 1) ^ a_swizzle(t))];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      v4i b0, b1;
+      b0.x = (int)signed_codes(wq[j][r].x, 0);
+      b0.y = (int)signed_codes(wq[j][r].x, 1);
+      b0.z = (int)signed_codes(wq[j][r].x, 2);
+      b0.w = (int)signed_codes(wq[j][r].x, 3);
+      b1.x = (int)signed_codes(wq[j][r].y, 0);
+      b1.y = (int)signed_codes(wq[j][r].y, 1);
+      b1.z = (int)signed_codes(wq[j][r].y, 2);
+      b1.w = (int)signed_codes(wq[j][r].y, 3);
+      // Scale of row r*16 + col, group g0 + j: byte scale_shift + 2j of that row's 32-byte window.
+      const int srow = r * 16 + col;
+      const int o = __shfl(scale_shift, srow) + 2 * j;
+      const float scale = h2f(*reinterpret_cast<const uint16_t*>(wave_scales + (o < 16 ? 0 : 1024 - 16) + srow * 16 + o));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const v4i zero = {0, 0, 0, 0};
+        v4i p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[mt], b0, zero, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[mt], b1, p, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][r][i] = __builtin_fmaf((float)p[i], scale, acc[mt][r][i]);
+      }
+    }
+  });
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slots past count
+
+  // Partial tiles [s][token][row] over the token regions (every wave is done with them), then
+  // the block's epilogue: output o is token o / 16R, row o % 16R; the S partials added in order.
   __syncthreads();
-  constexpr int kOutputs = T::kTokens * 16 * WR;  // a multiple of 64: whole waves stay active together
-  const int block_row0 = blockIdx.x * WR * 16;
+  float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
-  for (int j = 0; j < (kOutputs + 64 * kLdsWaves - 1) / (64 * kLdsWaves); ++j) {
-    const int o = tid + j * 64 * kLdsWaves;
-    if (kOutputs % (64 * kLdsWaves) != 0 && o >= kOutputs) break;
-    const int t = o / (16 * WR), rr = o % (16 * WR);
-    const int ww = rr >> 4, c = rr & 15;
-    const int out_row = block_row0 + rr;
-    float total = red[((ww * S) * T::kTokens + t) * T::kPitch + c];
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int k = 1; k < S; ++k) total = total + red[((ww * S + k) * T::kTokens + t) * T::kPitch + c];
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[(s * T::kTokens + mt * 16 + 4 * kb + i) * T::kPitch + r * 16 + col] = acc[mt][r][i];
+  __syncthreads();
+  constexpr int kOutputs = T::kTokens * 16 * R;  // a multiple of 64: whole waves stay active together
+#pragma unroll
+  for (int jo = 0; jo < (kOutputs + 64 * S - 1) / (64 * S); ++jo) {
+    const int o = tid + jo * 64 * S;
+    if (kOutputs % (64 * S) != 0 && o >= kOutputs) break;
+    const int t = o / (16 * R), rr = o % (16 * R);
+    const int out_row = row0 + rr;
+    float total = red[t * T::kPitch + rr];
+#pragma unroll
+    for (int k = 1; k < S; ++k) total = total + red[(k * T::kTokens + t) * T::kPitch + rr];
     const bool row_live = out_row < a.rows;
     const bool live = row_live && t < a.m;
     float y = total * scale_in[min(t, a.m - 1)];
@@ -352,14 +396,10 @@ __global__ __launch_bounds__(64 * kLdsWaves) void skinny_lds_kernel(const int8_t
   }
 }
 
-template <int EPI, int MT, int S, int NG>
-hipError_t launch_skinny_lds_shape(hipStream_t stream, const GemmArgs& a) {
-  using T = LdsTile<MT>;
-  const int groups = ceil_div(a.n, kGroup);
-  const size_t lds = (size_t)groups * T::kGroupBytes + T::kRedBytes;
-  const int rows_per_block = 16 * (kLdsWaves / S);
-  hipLaunchKernelGGL((skinny_lds_kernel<EPI, MT, S, NG>), dim3(ceil_div(a.rows, rows_per_block)), dim3(64 * kLdsWaves),
-                     lds, stream, a.q8_in, a.scale_in, a.packed, a.scales, a.bias, a.output, a);
+template <int EPI, int MT, int R, int S, int NG>
+hipError_t launch_skinny_row_shape(hipStream_t stream, const GemmArgs& a) {
+  hipLaunchKernelGGL((skinny_row_kernel<EPI, MT, R, S, NG>), dim3(ceil_div(a.rows, 16 * R)), dim3(64 * S), 0, stream,
+                     a.q8_in, a.scale_in, a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
 }
 
@@ -385,25 +425,46 @@ hipError_t launch_skinny_r(hipStream_t stream, const GemmArgs& a, int splits) {
   }
 }
 
-template <int EPI, int MT, int S>
-hipError_t launch_skinny_lds_s(hipStream_t stream, const GemmArgs& a, int ng) {
-  switch (ng) {
-    case 1: return launch_skinny_lds_shape<EPI, MT, S, 1>(stream, a);
-    case 2: return launch_skinny_lds_shape<EPI, MT, S, 2>(stream, a);
-    case 4: return launch_skinny_lds_shape<EPI, MT, S, 4>(stream, a);
-    case 8: return launch_skinny_lds_shape<EPI, MT, S, 8>(stream, a);
-    default: return hipErrorInvalidValue;
+// Shapes of the LDS-staged kernel that the plan can pick: (S, NG) with R = 1;
+// R = 2 (16 tokens) or 4 (32 tokens) with S = 8.
+template <int EPI, int MT, int R>
+hipError_t launch_skinny_row_r(hipStream_t stream, const GemmArgs& a, int splits, int ng) {
+  const int key = splits * 16 + ng;
+  if constexpr (R > 1) {
+    switch (key) {
+      case 8 * 16 + 1: return launch_skinny_row_shape<EPI, MT, R, 8, 1>(stream, a);
+      case 8 * 16 + 2: return launch_skinny_row_shape<EPI, MT, R, 8, 2>(stream, a);
+      case 8 * 16 + 4: return launch_skinny_row_shape<EPI, MT, R, 8, 4>(stream, a);
+      case 8 * 16 + 8:
+        if constexpr (MT == 1) return launch_skinny_row_shape<EPI, MT, R, 8, 8>(stream, a);
+        return hipErrorInvalidValue;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (key) {
+      case 1 * 16 + 1: return launch_skinny_row_shape<EPI, MT, 1, 1, 1>(stream, a);
+      case 2 * 16 + 1: return launch_skinny_row_shape<EPI, MT, 1, 2, 1>(stream, a);
+      case 2 * 16 + 2: return launch_skinny_row_shape<EPI, MT, 1, 2, 2>(stream, a);
+      case 4 * 16 + 1: return launch_skinny_row_shape<EPI, MT, 1, 4, 1>(stream, a);
+      case 4 * 16 + 2: return launch_skinny_row_shape<EPI, MT, 1, 4, 2>(stream, a);
+      case 8 * 16 + 1: return launch_skinny_row_shape<EPI, MT, 1, 8, 1>(stream, a);
+      case 8 * 16 + 2: return launch_skinny_row_shape<EPI, MT, 1, 8, 2>(stream, a);
+      case 8 * 16 + 4: return launch_skinny_row_shape<EPI, MT, 1, 8, 4>(stream, a);
+      case 8 * 16 + 8:
+        if constexpr (MT == 1) return launch_skinny_row_shape<EPI, MT, 1, 8, 8>(stream, a);
+        return hipErrorInvalidValue;  // 272 KB of LDS
+      default: return hipErrorInvalidValue;
+    }
   }
 }
 
 template <int EPI, int MT>
 hipError_t launch_skinny_mt(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan) {
   if (plan.lds_groups > 0) {
-    switch (plan.splits) {
-      case 4: return launch_skinny_lds_s<EPI, MT, 4>(stream, a, plan.lds_groups);
-      case 8: return launch_skinny_lds_s<EPI, MT, 8>(stream, a, plan.lds_groups);
-      default: return hipErrorInvalidValue;
-    }
+    if (plan.row_tiles == 1) return launch_skinny_row_r<EPI, MT, 1>(stream, a, plan.splits, plan.lds_groups);
+    if (plan.row_tiles == (MT == 1 ? 2 : 4))
+      return launch_skinny_row_r<EPI, MT, MT == 1 ? 2 : 4>(stream, a, plan.splits, plan.lds_groups);
+    return hipErrorInvalidValue;
   }
   switch (plan.row_tiles) {
     case 1: return launch_skinny_r<EPI, MT, 1>(stream, a, plan.splits);
@@ -417,36 +478,46 @@ hipError_t launch_skinny_epi(hipStream_t stream, const GemmArgs& a, SkinnyPlan p
   return a.m <= 16 ? launch_skinny_mt<EPI, 1>(stream, a, plan) : launch_skinny_mt<EPI, 2>(stream, a, plan);
 }
 
-size_t skinny_lds_bytes(int m, int n, SkinnyPlan plan) {
-  const int mt = m <= 16 ? 1 : 2;
-  if (plan.lds_groups > 0) return (size_t)ceil_div(n, kGroup) * 16 * mt * kGroup + (size_t)kLdsWaves * 16 * mt * 20 * 4;
+// LDS of the LDS-staged kernel (per wave: the token bytes of NG groups and two
+// 1 KB scale pieces), or of the cache-read kernel's partial tiles.
+size_t skinny_lds_bytes(int m, SkinnyPlan plan) {
+  const size_t mt = m <= 16 ? 1 : 2;
+  if (plan.lds_groups > 0) return (size_t)plan.splits * (plan.lds_groups * 16 * mt * kGroup + 2048);
   return (size_t)plan.splits * 16 * mt * (16 * plan.row_tiles + 4) * sizeof(float);
 }
 
 }  // namespace
 
-// The token tile goes to LDS when it fits there (K up to about 4.4k inputs at
-// 17..32 tokens, 9.4k at 16 or fewer): 8 K-splits of one row tile per block,
-// or 4 K-splits of two row tiles when more than 512 row tiles would make more
-// than two rounds of blocks.  Otherwise the token operand is read from the
-// caches per wave: two K-splits, four row tiles per wave for 8192 rows and
-// more (fewer re-reads of the token operand), one below.
+// The LDS-staged kernel whenever a wave's share fits (up to 64 groups, i.e.
+// K <= 8192): 8 K-splits from 8 groups on, 4 from 4, 2 from 2; from 768 row
+// tiles on, two row tiles per wave for up to 16 tokens and four above (fewer
+// blocks, each token fragment read once for more rows), one below.  Otherwise
+// the token operand is read from the caches per wave: two K-splits, four row
+// tiles per wave for 8192 rows and more (fewer re-reads of the token
+// operand), one below.
 SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds) {
   if (m < 1 || m > 32) return {0, 0, 0};
   const int groups = ceil_div(n, kGroup);
   const int tiles = ceil_div(rows, 16);
-  SkinnyPlan plan{tiles > 512 ? 4 : 8, 1, 0};
+  const int mt = m <= 16 ? 1 : 2;
+  SkinnyPlan plan{groups >= 8 ? 8 : groups >= 4 ? 4 : groups >= 2 ? 2 : 1, 1, 0};
   const int per_wave = ceil_div(groups, plan.splits);
   int ng = 1;
   while (ng < per_wave) ng *= 2;
   plan.lds_groups = ng;
-  if (ng <= 8 && skinny_lds_bytes(m, n, plan) <= max_lds) return plan;
-  plan = {groups >= 2 ? 2 : 1, rows >= 8192 ? 4 : 1, 0};
-  return plan;
+  if (plan.splits == 8 && tiles >= 768 && (mt == 1 || ng <= 4)) plan.row_tiles = mt == 1 ? 2 : 4;
+  // Its buffer offsets are 32-bit.
+  const long long row_bytes = (ceil_div(n, 4) + 15) / 16 * 16;
+  const bool small = (long long)rows * row_bytes < (1LL << 31) && (long long)rows * groups * 2 < (1LL << 31);
+  if (ng <= 8 && small && skinny_lds_bytes(m, plan) <= max_lds) return plan;
+  return {groups >= 2 ? 2 : 1, rows >= 8192 ? 4 : 1, 0};
 }
 
 hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan) {
-  if (plan.splits < 1 || skinny_lds_bytes(a.m, a.n, plan) > (size_t)max_lds_per_block()) return hipErrorInvalidValue;
+  if (plan.splits < 1 || skinny_lds_bytes(a.m, plan) > (size_t)max_lds_per_block()) return hipErrorInvalidValue;
+  if (plan.lds_groups > 0 &&
+      ((long long)a.rows * a.row_bytes >= (1LL << 31) || (long long)a.rows * a.groups * 2 >= (1LL << 31)))
+    return hipErrorInvalidValue;
   switch (a.epi) {
     case kStore: return launch_skinny_epi<kStore>(stream, a, plan);
     case kResidual: return launch_skinny_epi<kResidual>(stream, a, plan);

@@ -454,13 +454,16 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
     assert_within(y[0], truth, what="skinny gemm vs fp64 truth")
 
 
-# The two skinny kernels (M <= 32): the token tile staged in LDS (8 K-splits of one row tile per
-# block, or 4 K-splits of two row tiles past 512 row tiles) and, when the tile does not fit there,
-# the token operand read per wave (one or four row tiles per wave).  Odd chunk counts with several
-# groups, ragged rows, bias; sampled tokens against the oracle's split order.
-@pytest.mark.parametrize("m,k,rows,bias,splits", [(7, 4160, 1000, True, 8), (32, 4160, 1000, False, 8),
-                                                  (20, 1088, 8200, True, 4), (1, 8192, 8192, False, 8),
-                                                  (32, 8192, 8200, False, 2), (17, 8192, 300, True, 2)])
+# The two skinny kernels (M <= 32): the token bytes staged in LDS per wave (8, 4, 2 or 1 K-splits by
+# group count; one row tile per wave, two or four from 768 row tiles on) and, when a wave's share does not
+# fit there, the token operand read per wave from the caches (one or four row tiles per wave).  Odd
+# chunk counts with several groups, ragged rows, bias; sampled tokens against the oracle's split
+# order.
+@pytest.mark.parametrize("m,k,rows,bias,splits", [(7, 4160, 1000, True, 8), (32, 2112, 1000, False, 8),
+                                                  (20, 1088, 8200, True, 8), (1, 8192, 8192, False, 8),
+                                                  (9, 4096, 12300, True, 8), (32, 2112, 12290, False, 8),
+                                                  (32, 4160, 1000, False, 2), (32, 8192, 8200, False, 2),
+                                                  (17, 8192, 300, True, 2), (3, 200, 40, True, 2)])
 def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
     from ivonar_amd import ops, runtime
 
@@ -480,12 +483,12 @@ def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
 
 
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
-def test_gemm_skinny_two_row_tiles_epilogues(cuda, oracle, epilogue):
+def test_gemm_skinny_four_row_tiles_epilogues(cuda, oracle, epilogue):
     import torch
     from ivonar_amd import ops, runtime
 
     rng = np.random.default_rng(97 if epilogue == "residual" else 96)
-    m, k, rows = 24, 1024, 8224
+    m, k, rows = 24, 2048, 12304
     codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
     x = rng.standard_normal((m, k)).astype(np.float32)
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
@@ -495,10 +498,10 @@ def test_gemm_skinny_two_row_tiles_epilogues(cuda, oracle, epilogue):
     base = rng.standard_normal((m, stride)).astype(np.float32)
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
-    assert runtime.gemm_plan(m, rows, k) == 4
+    assert runtime.gemm_plan(m, rows, k) == 8
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
     epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
-    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m, 4)
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m, 8)
     assert_bits_equal(to_np(out), expected, epilogue)
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
