@@ -370,16 +370,24 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 
 }  // namespace
 
+// Kernel choice: the skinny kernels up to 32 tokens; then the long-prompt
+// tilings; then the LDS-staged skinny kernel in 32-token slices up to
+// kSlicedTokens; otherwise the tiled kernel.
 int gemm_splits(int m, int rows, int n) {
+  const size_t lds = (size_t)max_lds_per_block();
+  if (m > 32 && gemm_wide_applies(m, rows)) return 1;
   if (gemm_split_applies(m, rows, n)) return 4;
-  const SkinnyPlan plan = skinny_plan(m, rows, n, (size_t)max_lds_per_block());
+  const SkinnyPlan plan = skinny_plan(m, rows, n, lds);
   return plan.splits > 0 ? plan.splits : 1;
 }
 
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (a.rows <= 0 || a.m <= 0) return hipSuccess;
-  const SkinnyPlan plan = skinny_plan(a.m, a.rows, a.n, (size_t)max_lds_per_block());
-  if (plan.splits > 0) return launch_skinny(stream, a, plan);
+  const size_t lds = (size_t)max_lds_per_block();
+  if (a.m <= 32) {
+    const SkinnyPlan plan = skinny_plan(a.m, a.rows, a.n, lds);
+    if (plan.splits > 0) return launch_skinny(stream, a, plan);
+  }
   // Buffer offsets are 32-bit: every operand (with a tile of slack) stays below 2 GiB.
   const long long limit = 0x7FFFFFF0LL;
   if (((long long)a.m + 256) * ceil_div(a.n, kChunk) * kChunk >= limit ||
@@ -387,6 +395,8 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
     return hipErrorInvalidValue;
   if (gemm_wide_applies(a.m, a.rows)) return launch_gemm_wide(stream, a);
   if (gemm_split_applies(a.m, a.rows, a.n)) return launch_gemm_split(stream, a);
+  const SkinnyPlan sliced = skinny_plan(a.m, a.rows, a.n, lds);
+  if (sliced.splits > 0) return launch_skinny(stream, a, sliced);
   switch (a.epi) {
     case kStore: return launch_epi<kStore>(stream, a);
     case kResidual: return launch_epi<kResidual>(stream, a);

@@ -231,9 +231,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 // that count and a barrier (measured on MI355X: a wave that reads the bytes of
 // its own direct-to-LDS load right after the counter reaches them sometimes
 // reads the half of the 64 lanes that is still being written; with the barrier
-// it never did).  The token fragments of a group feed all R row tiles.  Tokens past m and the
-// missing second chunk of an odd chunk count read as zeros through the buffer
-// range check; rows past the matrix are clamped and not stored.
+// it never did).  The token fragments of a group feed all R row tiles.  Prompts
+// of more than 32 tokens run as slices of 32 tokens (grid dimension y).  Tokens
+// past the slice and the missing second chunk of an odd chunk count read as
+// zeros through the buffer range check; rows past the matrix are clamped and
+// not stored.
 template <int MT, int R, int S, int NG>
 struct RowTile {
   static constexpr int kTokens = 16 * MT;
@@ -266,6 +268,12 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
   const int groups = (a.n + kGroup - 1) / kGroup;
   const int short_group = (chunks & 1) ? groups - 1 : groups;
   const int q8_stride = chunks * kChunk;
+  // Token slice blockIdx.y: tokens [16*MT*y, 16*MT*y + m) of the prompt.
+  const int token0 = blockIdx.y * T::kTokens;
+  const int m = min(a.m - token0, T::kTokens);
+  q8 += (size_t)token0 * q8_stride;
+  scale_in += token0;
+  output += (size_t)token0 * a.out_stride;
   const int per_wave = (groups + S - 1) / S;
   const int g0 = min(s * per_wave, groups);
   const int count = min(per_wave, groups - g0);
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
   const unsigned a_lds = lds_address(wave_a);
   const unsigned s_lds = lds_address(wave_scales);
   constexpr int kPast = 0x7FFFFFF0;
-  const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
+  const v4u q8_buf = wide_buffer(q8, (long long)m * q8_stride);
   const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
   const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
 
@@ -296,7 +304,7 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
       const int slot = q * 64 + lane;
       const int t = slot >> 3;
       const int piece = (slot & 7) ^ a_swizzle(t);
-      const bool dead = (g == short_group && piece >= 4) || q * 8 >= a.m;
+      const bool dead = (g == short_group && piece >= 4) || q * 8 >= m;
       dma16(q8_buf, a_lds + j * T::kGroupBytes + q * 1024, dead ? kPast : t * q8_stride + g * kGroup + piece * 16, 0);
     }
     const bool wdead = g == short_group && kb >= 2;
@@ -381,10 +389,10 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
 #pragma unroll
     for (int k = 1; k < S; ++k) total = total + red[(k * T::kTokens + t) * T::kPitch + rr];
     const bool row_live = out_row < a.rows;
-    const bool live = row_live && t < a.m;
-    float y = total * scale_in[min(t, a.m - 1)];
+    const bool live = row_live && t < m;
+    float y = total * scale_in[min(t, m - 1)];
     if (bias != nullptr) y = y + bias[min(out_row, a.rows - 1)];
-    float* orow = output + (size_t)min(t, a.m - 1) * a.out_stride;
+    float* orow = output + (size_t)min(t, m - 1) * a.out_stride;
     if constexpr (EPI == kSiluPair) {
       const float partner = __shfl_xor(y, 1);
       if (live && (out_row & 1) == 0 && out_row + 1 < a.rows) orow[out_row >> 1] = ivo_silu(y) * partner;
@@ -398,7 +406,8 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
 
 template <int EPI, int MT, int R, int S, int NG>
 hipError_t launch_skinny_row_shape(hipStream_t stream, const GemmArgs& a) {
-  hipLaunchKernelGGL((skinny_row_kernel<EPI, MT, R, S, NG>), dim3(ceil_div(a.rows, 16 * R)), dim3(64 * S), 0, stream,
+  hipLaunchKernelGGL((skinny_row_kernel<EPI, MT, R, S, NG>), dim3(ceil_div(a.rows, 16 * R), ceil_div(a.m, 16 * MT)),
+                     dim3(64 * S), 0, stream,
                      a.q8_in, a.scale_in, a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
 }
@@ -488,6 +497,8 @@ size_t skinny_lds_bytes(int m, SkinnyPlan plan) {
 
 }  // namespace
 
+// Prompts of 33..kSlicedTokens tokens that neither long-prompt tiling takes run
+// the LDS-staged kernel in 32-token slices when it fits.
 // The LDS-staged kernel whenever a wave's share fits (up to 64 groups, i.e.
 // K <= 8192): 8 K-splits from 8 groups on, 4 from 4, 2 from 2; from 768 row
 // tiles on, two row tiles per wave for up to 16 tokens and four above (fewer
@@ -496,7 +507,7 @@ size_t skinny_lds_bytes(int m, SkinnyPlan plan) {
 // tiles per wave for 8192 rows and more (fewer re-reads of the token
 // operand), one below.
 SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds) {
-  if (m < 1 || m > 32) return {0, 0, 0};
+  if (m < 1 || m > kSlicedTokens) return {0, 0, 0};
   const int groups = ceil_div(n, kGroup);
   const int tiles = ceil_div(rows, 16);
   const int mt = m <= 16 ? 1 : 2;
@@ -510,6 +521,7 @@ SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds) {
   const long long row_bytes = (ceil_div(n, 4) + 15) / 16 * 16;
   const bool small = (long long)rows * row_bytes < (1LL << 31) && (long long)rows * groups * 2 < (1LL << 31);
   if (ng <= 8 && small && skinny_lds_bytes(m, plan) <= max_lds) return plan;
+  if (m > 32) return {0, 0, 0};
   return {groups >= 2 ? 2 : 1, rows >= 8192 ? 4 : 1, 0};
 }
 

@@ -105,10 +105,11 @@ hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a);
 // each an fmaf chain, added in order); 1 = one chain over all groups.
 int gemm_splits(int m, int rows, int n);
 int max_lds_per_block();
-// Skinny token GEMM (m <= 32): K-splits (its fp32 order), 16-row tiles per
-// wave and, for the kernel that stages the token tile in LDS, the register
-// slots for groups per wave (0: the token operand is read from the caches);
-// splits == 0 means it does not apply.
+// Skinny token GEMM (m <= 32, and up to kSlicedTokens in 32-token slices):
+// K-splits (its fp32 order), 16-row tiles per wave and, for the kernel that
+// stages the token tile in LDS, the register slots for groups per wave (0: the
+// token operand is read from the caches); splits == 0 means it does not apply.
+constexpr int kSlicedTokens = 512;
 struct SkinnyPlan {
   int splits;
   int row_tiles;

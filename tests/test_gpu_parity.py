@@ -482,6 +482,53 @@ def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
     assert np.isfinite(y).all()
 
 
+# Prompts of 33..512 tokens that neither long-prompt tiling takes (few row blocks, few groups) run the
+# LDS-staged skinny kernel in 32-token slices; 513 tokens fall back to the tiled kernel (one split).
+@pytest.mark.parametrize("m,k,rows,bias,splits", [(300, 1088, 1000, True, 8), (130, 2112, 500, False, 8),
+                                                  (45, 200, 40, True, 2), (512, 1024, 96, False, 8),
+                                                  (513, 1088, 300, False, 1)])
+def test_gemm_sliced_skinny(cuda, oracle, m, k, rows, bias, splits):
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(m * 17 + k + rows)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=bias)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    y = to_np(ops.gemm(matrix, q8, xsum, sx))
+    assert runtime.gemm_plan(m, rows, k) == splits
+    sample = np.unique(np.array([0, 15, 16, 31, 32, 33, 63, 64, m // 2, m - 2, m - 1]) % m)
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), splits)
+    assert_bits_equal(y[sample], expected, f"sampled tokens ({splits} splits)")
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_gemm_sliced_skinny_epilogues(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(93 if epilogue == "residual" else 92)
+    m, k, rows = 70, 1024, 600
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    width = rows if epilogue == "residual" else rows // 2
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    assert runtime.gemm_plan(m, rows, k) == 8
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base.copy(), k, stride, m, 8)
+    assert_bits_equal(to_np(out), expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
+
+
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
 def test_gemm_skinny_four_row_tiles_epilogues(cuda, oracle, epilogue):
     import torch
