@@ -302,7 +302,7 @@ def measure_mfma(calls: int = 16, cus: int = 256, xcds: int = 8) -> dict:
     rows = counter_pass(counters, "gemm-prefill", calls)
     if isinstance(rows, str):
         return {"error": rows}
-    kernels = ("gemm_kernel", "gemm_wide_kernel", "gemm_split_kernel", "skinny_kernel")
+    kernels = ("gemm_kernel", "gemm_wide_kernel", "gemm_split_kernel", "skinny_kernel", "skinny_row_kernel")
     gemm = [row for row in rows if any(name in row["kernel"] for name in kernels) and all(c in row for c in counters)]
     cases = [(k, n, m) for k, n in PROBE_GEMM_SHAPES for m in PROBE_GEMM_M]
     if len(gemm) != len(cases) * calls:

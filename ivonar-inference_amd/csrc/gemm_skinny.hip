@@ -430,6 +430,7 @@ hipError_t launch_skinny_r(hipStream_t stream, const GemmArgs& a, int splits) {
   switch (splits) {
     case 1: return launch_skinny_shape<EPI, MT, R, 1>(stream, a);
     case 2: return launch_skinny_shape<EPI, MT, R, 2>(stream, a);
+    case 4: return launch_skinny_shape<EPI, MT, R, 4>(stream, a);
     default: return hipErrorInvalidValue;
   }
 }
@@ -477,7 +478,7 @@ hipError_t launch_skinny_mt(hipStream_t stream, const GemmArgs& a, SkinnyPlan pl
   }
   switch (plan.row_tiles) {
     case 1: return launch_skinny_r<EPI, MT, 1>(stream, a, plan.splits);
-    case 4: return launch_skinny_r<EPI, MT, 4>(stream, a, plan.splits);
+    case 2: return launch_skinny_r<EPI, MT, 2>(stream, a, plan.splits);
     default: return hipErrorInvalidValue;
   }
 }
@@ -503,9 +504,10 @@ size_t skinny_lds_bytes(int m, SkinnyPlan plan) {
 // K <= 8192): 8 K-splits from 8 groups on, 4 from 4, 2 from 2; from 768 row
 // tiles on, two row tiles per wave for up to 16 tokens and four above (fewer
 // blocks, each token fragment read once for more rows), one below.  Otherwise
-// the token operand is read from the caches per wave: two K-splits, four row
+// the token operand is read from the caches per wave: four K-splits, two row
 // tiles per wave for 8192 rows and more (fewer re-reads of the token
-// operand), one below.
+// operand), one below (measured at K=28672 -> N=8192, 1 token: 31 us against
+// 56 us with four row tiles and two K-splits).
 SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds) {
   if (m < 1 || m > kSlicedTokens) return {0, 0, 0};
   const int groups = ceil_div(n, kGroup);
@@ -522,7 +524,7 @@ SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds) {
   const bool small = (long long)rows * row_bytes < (1LL << 31) && (long long)rows * groups * 2 < (1LL << 31);
   if (ng <= 8 && small && skinny_lds_bytes(m, plan) <= max_lds) return plan;
   if (m > 32) return {0, 0, 0};
-  return {groups >= 2 ? 2 : 1, rows >= 8192 ? 4 : 1, 0};
+  return {groups >= 4 ? 4 : groups >= 2 ? 2 : 1, rows >= 8192 ? 2 : 1, 0};
 }
 
 hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan) {

@@ -456,14 +456,14 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
 
 # The two skinny kernels (M <= 32): the token bytes staged in LDS per wave (8, 4, 2 or 1 K-splits by
 # group count; one row tile per wave, two or four from 768 row tiles on) and, when a wave's share does not
-# fit there, the token operand read per wave from the caches (one or four row tiles per wave).  Odd
+# fit there, the token operand read per wave from the caches (one or two row tiles per wave).  Odd
 # chunk counts with several groups, ragged rows, bias; sampled tokens against the oracle's split
 # order.
 @pytest.mark.parametrize("m,k,rows,bias,splits", [(7, 4160, 1000, True, 8), (32, 2112, 1000, False, 8),
                                                   (20, 1088, 8200, True, 8), (1, 8192, 8192, False, 8),
                                                   (9, 4096, 12300, True, 8), (32, 2112, 12290, False, 8),
-                                                  (32, 4160, 1000, False, 2), (32, 8192, 8200, False, 2),
-                                                  (17, 8192, 300, True, 2), (3, 200, 40, True, 2)])
+                                                  (32, 4160, 1000, False, 4), (32, 8192, 8200, False, 4),
+                                                  (17, 8192, 300, True, 4), (3, 200, 40, True, 2), (1, 28672, 8192, False, 4)])
 def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
     from ivonar_amd import ops, runtime
 
