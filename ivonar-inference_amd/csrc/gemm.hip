@@ -375,7 +375,7 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 // kSlicedTokens; otherwise the tiled kernel.
 int gemm_splits(int m, int rows, int n) {
   const size_t lds = (size_t)max_lds_per_block();
-  if (m > 32 && gemm_wide_applies(m, rows)) return 1;
+  if (gemm_wide_tokens(m, rows, n) > 0) return 1;
   if (gemm_split_applies(m, rows, n)) return 4;
   const SkinnyPlan plan = skinny_plan(m, rows, n, lds);
   return plan.splits > 0 ? plan.splits : 1;
@@ -393,7 +393,7 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (((long long)a.m + 256) * ceil_div(a.n, kChunk) * kChunk >= limit ||
       ((long long)a.rows + 256) * a.row_bytes >= limit || ((long long)a.rows + 256) * a.groups * 2 >= limit)
     return hipErrorInvalidValue;
-  if (gemm_wide_applies(a.m, a.rows)) return launch_gemm_wide(stream, a);
+  if (gemm_wide_tokens(a.m, a.rows, a.n) > 0) return launch_gemm_wide(stream, a);
   if (gemm_split_applies(a.m, a.rows, a.n)) return launch_gemm_split(stream, a);
   const SkinnyPlan sliced = skinny_plan(a.m, a.rows, a.n, lds);
   if (sliced.splits > 0) return launch_skinny(stream, a, sliced);

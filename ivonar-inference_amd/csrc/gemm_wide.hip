@@ -258,12 +258,12 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
   // lanes covering 256 contiguous bytes of an output row, written with the
   // non-temporal hint (the output is streamed once; measured 2-9% faster on
   // the prefill shapes than plain stores).  Each wave uses its
-  // own slice of the first stage; a wave's LDS operations complete in order,
+  // own slice of the stages; a wave's LDS operations complete in order,
   // so the slice needs no barrier between its writes and reads.
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   constexpr int kPitch = 68;  // floats per token row of a slice (conflict-free column writes)
-  static_assert(4 * 16 * kPitch * 4 <= T::kStageBytes, "transpose slices fit one stage");
-  float* slice = reinterpret_cast<float*>(stages[0]) + wave * 16 * kPitch;
+  static_assert(4 * 16 * kPitch * 4 <= 3 * T::kStageBytes, "transpose slices fit the stages");
+  float* slice = reinterpret_cast<float*>(&stages[0][0]) + wave * 16 * kPitch;
   const bool has_bias = bias != nullptr;
   float bv[4];
 #pragma unroll
@@ -337,7 +337,8 @@ hipError_t launch_wide_shape(hipStream_t stream, const GemmArgs& a) {
 }
 
 template <int EPI>
-hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a) {
+hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a, int tokens) {
+  if (tokens == 64) return launch_wide_shape<EPI, 4, 4>(stream, a);
   return launch_wide_shape<EPI, 8, 4>(stream, a);
 }
 
@@ -602,20 +603,33 @@ hipError_t launch_split_epi(hipStream_t stream, const GemmArgs& a) {
 
 }  // namespace
 
-// Measured on MI355X against the 64 x 64-wave-tile kernel (random operands):
-// K=4096 -> N=14336 at M=512 (224 blocks) 60.8 us against 66.7 us; K=1024 ->
-// N=4096 at M=512 (64 blocks) 19.0 us against 16.5 us.  The 128 x 256 tiling
-// pays from about 192 blocks (three quarters of the CUs busy).
-bool gemm_wide_applies(int m, int rows) {
-  const long long blocks = (long long)ceil_div(rows, 256) * ceil_div(m, 128);
-  return m >= 128 && blocks >= 192 && WideTile<8, 4>::kLdsBytes <= max_lds_per_block();
+// Token tile of the long-prompt kernel (0: it does not apply).  128 tokens x
+// 256 rows from 2048 inputs on, where the loop dominates: it pays from about
+// 192 blocks (three quarters of the CUs busy; K=4096 -> N=14336 at M=512, 224
+// blocks: 60.8 us against 66.7 us for the 64 x 64-wave-tile kernel).  Below
+// 2048 inputs the loads before the first MFMA and the output write dominate
+// and 64-token tiles (half the registers, two blocks per CU) pay from 96
+// blocks: K=1024 -> N=4096 at M=512 13.1 us against 18.8 us with 128-token
+// tiles, at M=2048 20.9 against 21.8 us; with 4096 inputs they lose (68.8
+// against 61.0 us at M=2048, N=4096).
+int gemm_wide_tokens(int m, int rows, int n) {
+  if (m < 128) return 0;
+  const long long row_blocks = ceil_div(rows, 256);
+  if (ceil_div(n, kGroup) >= 16) {
+    const bool fits = WideTile<8, 4>::kLdsBytes <= max_lds_per_block();
+    return fits && row_blocks * ceil_div(m, 128) >= 192 ? 128 : 0;
+  }
+  const bool fits = WideTile<4, 4>::kLdsBytes <= max_lds_per_block();
+  return fits && row_blocks * ceil_div(m, 64) >= 96 ? 64 : 0;
 }
 
 hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
+  const int tokens = gemm_wide_tokens(a.m, a.rows, a.n);
+  if (tokens == 0) return hipErrorInvalidValue;
   switch (a.epi) {
-    case kStore: return launch_wide_epi<kStore>(stream, a);
-    case kResidual: return launch_wide_epi<kResidual>(stream, a);
-    case kSiluPair: return launch_wide_epi<kSiluPair>(stream, a);
+    case kStore: return launch_wide_epi<kStore>(stream, a, tokens);
+    case kResidual: return launch_wide_epi<kResidual>(stream, a, tokens);
+    case kSiluPair: return launch_wide_epi<kSiluPair>(stream, a, tokens);
     default: return hipErrorInvalidValue;
   }
 }
@@ -627,7 +641,7 @@ hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
 // M=128 22.0 us, against 45.4 and 42.6 us for the 64 x 64-wave-tile kernel.
 bool gemm_split_applies(int m, int rows, int n) {
   const long long tiles = (long long)ceil_div(rows, kSplitRows) * ceil_div(m, kSplitTokens);
-  return m > 32 && !gemm_wide_applies(m, rows) && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
+  return m > 32 && gemm_wide_tokens(m, rows, n) == 0 && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
 }
 
 hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a) {

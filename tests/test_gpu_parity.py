@@ -553,11 +553,13 @@ def test_gemm_skinny_four_row_tiles_epilogues(cuda, oracle, epilogue):
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
-# Long prompts with many row blocks run the 128-token-tile kernel (chosen when m >= 128 and the
-# 128-token x 256-row tiling gives >= 192 blocks): ragged token and row counts, an odd chunk count,
-# a single-chunk K, bias, and every epilogue with a padded output stride.
+# Long prompts with many row blocks run the long-prompt kernel (m >= 128; 128-token x 256-row tiles
+# from 2048 inputs on with >= 192 blocks, 64-token tiles below with >= 96 blocks): ragged token and
+# row counts, an odd chunk count, a single-chunk K, bias, and every epilogue with a padded output
+# stride.
 @pytest.mark.parametrize("m,k,rows,bias", [(1000, 1088, 8200, True), (2048, 64, 4096, False),
-                                          (128, 4096, 65536, False), (1537, 1100, 5120, True)])
+                                          (128, 4096, 65536, False), (1537, 1100, 5120, True),
+                                          (700, 1024, 4096, True), (130, 1024, 24576, False)])
 def test_gemm_wide_tiles_edges(cuda, oracle, m, k, rows, bias):
     from ivonar_amd import ops, runtime
 
@@ -593,6 +595,34 @@ def test_gemm_wide_tiles_epilogues(cuda, oracle, epilogue):
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
     sample = np.array([0, 5, 127, 128, 255, 256, 299])
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
+    epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
+    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
+                                 len(sample), 1)
+    assert_bits_equal(to_np(out)[sample], expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
+
+
+# 128-token tiles (2048 inputs and more) with both epilogues, on sampled tokens: 192 blocks of 128
+# tokens x 256 rows.
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_gemm_wide_128_token_tiles_epilogues(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(91 if epilogue == "residual" else 90)
+    m, k, rows = 1024, 2048, 6144
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    width = rows if epilogue == "residual" else rows // 2
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    assert runtime.gemm_plan(m, rows, k) == 1
+    sample = np.array([0, 1, 127, 128, 500, 1023])
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
     expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
