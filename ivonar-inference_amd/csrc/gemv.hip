@@ -249,7 +249,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   // then lane sub = r finishes row row0 + r.
   auto finish = [&](float acc, int row0) {
     if constexpr (EPI != kPartials) {
-      for (int offset = 2; offset < lanes; offset <<= 1) acc = acc + __shfl_xor(acc, offset);
+      acc = pair_tree_sum(acc, lanes);
       const int row = row0 + (sub & 1);
       float y = acc * sx;
       if (bias != nullptr && row < sh.rows) y = y + bias[row];
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (EPI != kPartials) {
-      for (int offset = 2; offset < 64; offset <<= 1) acc = acc + __shfl_xor(acc, offset);
+      acc = pair_tree_sum(acc, 64);
       const int row = row0 + (sub & 1);
       float y = acc * sx;
       if (bias != nullptr) y = y + __int_as_float(b_cur);

@@ -91,6 +91,37 @@ __device__ __forceinline__ int chunk_code_dot(const uint4 w, const int4 q0, cons
 // Lane value of the partner in the same lane pair (quad_perm [1,0,3,2]).
 __device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 
+// Lane L reads lane L + N of its 16-lane row (lanes past the row read 0).
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + N, 0xF, 0xF, true));
+}
+
+// Lanes of even 16-lane rows read the same lane of the next row; lanes of the
+// lower 32 read the same lane of the upper 32 (v_permlane16/32_swap).
+__device__ __forceinline__ float row_swap16(float v) {
+  const unsigned u = __float_as_uint(v);
+  return __uint_as_float(__builtin_amdgcn_permlane16_swap(u, u, false, false)[1]);
+}
+__device__ __forceinline__ float row_swap32(float v) {
+  const unsigned u = __float_as_uint(v);
+  return __uint_as_float(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
+}
+
+// The xor butterfly over lane pairs, acc += acc of lane L ^ o for o = 2, 4, ..
+// lanes/2, evaluated for the lanes that finish a row (L mod lanes < 2) only:
+// at stage o such a lane, and every lane its result depends on, has bit o
+// clear, so L ^ o = L + o and adding lane L + o is the same operand pair in
+// the same order.  DPP row shifts and row swaps instead of LDS permutes.
+__device__ __forceinline__ float pair_tree_sum(float acc, int lanes) {
+  if (lanes > 2) acc = acc + row_shl<2>(acc);
+  if (lanes > 4) acc = acc + row_shl<4>(acc);
+  if (lanes > 8) acc = acc + row_shl<8>(acc);
+  if (lanes > 16) acc = acc + row_swap16(acc);
+  if (lanes > 32) acc = acc + row_swap32(acc);
+  return acc;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));
   return v;
