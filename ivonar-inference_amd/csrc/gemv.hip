@@ -58,22 +58,25 @@ struct GemvPtrs {
   const float* scale_in;
 };
 
-// One pipeline item's loads: weights of NJ steps for kRows rows, and per
-// step the group scale of the lane's own row (row0 + (sub & 1)).
+// One pipeline item's loads: weights of NJ steps for kRows rows, per step
+// the group scale of the lane's own row (row0 + (sub & 1)), and for the
+// residual epilogue that row's output value, so the read of the residual base
+// travels with the weights instead of adding a round trip after the sums.
 template <int NJ>
 struct Step {
   uint4 w[NJ][kRows];
   uint16_t s[NJ];
+  float base;
 };
 
 __device__ __forceinline__ uint4 load16(const uint8_t* __restrict__ p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-template <int NJ, bool SCALES, int LANES>
+template <int NJ, bool SCALES, int LANES, bool BASE>
 __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restrict__ packed,
-                                          const uint16_t* __restrict__ scales, const GemvShape& sh, int row0,
-                                          int j0, int sub, int chunks) {
+                                          const uint16_t* __restrict__ scales, const float* __restrict__ base,
+                                          const GemvShape& sh, int row0, int j0, int sub, int chunks) {
   const int lanes = LANES ? LANES : sh.lanes;
   const int own_row = min(row0 + (sub & 1), sh.rows - 1);
 #pragma unroll
@@ -86,6 +89,7 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
     }
     st.s[j] = SCALES ? scales[(size_t)own_row * sh.groups + (u >> 1)] : (uint16_t)0;
   }
+  if constexpr (BASE) st.base = base[own_row];
 }
 
 // Lane pair (sub, sub ^ 1) covers the two chunks of a group for rows row0 and
@@ -182,7 +186,8 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   // load_step), so the wait counts before each use stay exact.
   Step<NJ> a, b;
   int it = first;
-  load_step<NJ, EPI != kPartials, LANES>(a, packed, scales, sh, it * rows_per_iter + slot * kRows, 0, sub, chunks);
+  load_step<NJ, EPI != kPartials, LANES, EPI == kResidual>(a, packed, scales, output, sh,
+                                                          it * rows_per_iter + slot * kRows, 0, sub, chunks);
 
   float sx;
   int4 qr[QREG ? NJ : 1][4];
@@ -247,7 +252,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
 
   // Butterfly over the pairs (offsets 2 .. lanes/2 keep each lane's row),
   // then lane sub = r finishes row row0 + r.
-  auto finish = [&](float acc, int row0) {
+  auto finish = [&](float acc, int row0, float base) {
     if constexpr (EPI != kPartials) {
       acc = pair_tree_sum(acc, lanes);
       const int row = row0 + (sub & 1);
@@ -258,7 +263,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         if (sub == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y) * up;
       } else if (sub < 2 && row < sh.rows) {
         if constexpr (EPI == kStore) output[row] = y;
-        else output[row] = output[row] + y;
+        else output[row] = base + y;
       }
     }
   };
@@ -276,12 +281,13 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         it_next = it + waves;
       }
       const int row0 = it * rows_per_iter + slot * kRows;
-      load_step<NJ, EPI != kPartials, LANES>(b, packed, scales, sh, it_next * rows_per_iter + slot * kRows,
-                                             jb_next * NJ, sub, chunks);
+      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual>(b, packed, scales, output, sh,
+                                                              it_next * rows_per_iter + slot * kRows, jb_next * NJ,
+                                                              sub, chunks);
       compute_step<EPI, NJ, QREG, LANES, EXACT>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
                                                 chunks);
       if (jb == blocks_per_row - 1) {
-        finish(acc, row0);
+        finish(acc, row0, a.base);
         acc = 0.0f;
       }
       it = it_next;
@@ -295,12 +301,13 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         it_next = it + waves;
       }
       const int row0 = it * rows_per_iter + slot * kRows;
-      load_step<NJ, EPI != kPartials, LANES>(a, packed, scales, sh, it_next * rows_per_iter + slot * kRows,
-                                             jb_next * NJ, sub, chunks);
+      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual>(a, packed, scales, output, sh,
+                                                              it_next * rows_per_iter + slot * kRows, jb_next * NJ,
+                                                              sub, chunks);
       compute_step<EPI, NJ, QREG, LANES, EXACT>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
                                                 chunks);
       if (jb == blocks_per_row - 1) {
-        finish(acc, row0);
+        finish(acc, row0, b.base);
         acc = 0.0f;
       }
       it = it_next;
