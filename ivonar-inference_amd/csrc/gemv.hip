@@ -31,6 +31,8 @@
 // memory: once for the whole kernel when a row needs at most two steps per
 // lane, else with every step's weights.  That path has no LDS and no
 // barrier: the q8 row is small and stays in the caches for every block.
+#include <type_traits>
+
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -58,7 +60,8 @@ struct GemvPtrs {
   const float* scale_in;
 };
 
-// One pipeline item's loads: weights of NJ steps for kRows rows, per step
+// One pipeline item's loads: weights of NJ steps for kRows rows (w[j][0] of
+// the lane's own row row0 + (sub & 1), w[j][1] of its partner's), per step
 // the group scale of the lane's own row (row0 + (sub & 1)), and for the
 // residual epilogue that row's output value, so the read of the residual base
 // travels with the weights instead of adding a round trip after the sums.
@@ -73,7 +76,7 @@ __device__ __forceinline__ uint4 load16(const uint8_t* __restrict__ p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-template <int NJ, bool SCALES, int LANES, bool BASE>
+template <int NJ, bool SCALES, int LANES, bool BASE, bool EXACT>
 __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restrict__ packed,
                                           const uint16_t* __restrict__ scales, const float* __restrict__ base,
                                           const GemvShape& sh, int row0, int j0, int sub, int chunks) {
@@ -81,10 +84,12 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
   const int own_row = min(row0 + (sub & 1), sh.rows - 1);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int u = min((j0 + j) * lanes + sub, chunks - 1);
+    // With EXACT every chunk of an item exists (items hold no dead steps), and
+    // leaving out the clamp lets the step offsets fold into the loads.
+    const int u = EXACT ? (j0 + j) * lanes + sub : min((j0 + j) * lanes + sub, chunks - 1);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-      const int row = min(row0 + r, sh.rows - 1);
+      const int row = min(row0 + (r ^ (sub & 1)), sh.rows - 1);
       st.w[j][r] = load16(packed + (size_t)row * sh.row_bytes + (size_t)u * 16);
     }
     st.s[j] = SCALES ? scales[(size_t)own_row * sh.groups + (u >> 1)] : (uint16_t)0;
@@ -94,9 +99,9 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
 
 // Lane pair (sub, sub ^ 1) covers the two chunks of a group for rows row0 and
 // row0 + 1; each lane keeps the accumulator of its own row (sub & 1).  A lane
-// forms both rows' chunk sums, sends the partner's row across the pair (one
-// DPP swap) and adds the partner's sum for its own row: the exact group
-// partial P[own row, g].
+// forms both rows' chunk sums (its own row's first), sends the partner's row
+// across the pair (one DPP swap) and adds the partner's sum for its own row:
+// the exact group partial P[own row, g].
 template <int EPI, int NJ, bool QREG, int LANES, bool EXACT>
 __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr)[QREG ? NJ : 1][4],
                                              const int (&xr)[QREG ? NJ : 1], const int4* __restrict__ lds_q,
@@ -105,7 +110,6 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
                                              int sub, int chunks) {
   static_assert(kRows == 2, "a lane pair holds two rows");
   const int lanes = LANES ? LANES : sh.lanes;
-  const bool odd = (sub & 1) != 0;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int u_raw = (j0 + j) * lanes + sub;
@@ -121,7 +125,7 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
       q3 = qr[j][3];
       xs = xr[j];
     } else {
-      const int u = min(u_raw, chunks - 1);
+      const int u = EXACT ? u_raw : min(u_raw, chunks - 1);
       q0 = lds_q[u];
       q1 = lds_q[chunks + u];
       q2 = lds_q[2 * chunks + u];
@@ -134,7 +138,7 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
       d0 = live ? d0 : 0;
       d1 = live ? d1 : 0;
     }
-    const int d = (odd ? d1 : d0) + pair_swap(odd ? d0 : d1);
+    const int d = d0 + pair_swap(d1);
     if constexpr (EPI == kPartials) {
       const int row = row0 + (sub & 1);
       if (group_live && row < sh.rows) partials[(size_t)row * sh.groups + g] = d;
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   // load_step), so the wait counts before each use stay exact.
   Step<NJ> a, b;
   int it = first;
-  load_step<NJ, EPI != kPartials, LANES, EPI == kResidual>(a, packed, scales, output, sh,
+  load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
                                                           it * rows_per_iter + slot * kRows, 0, sub, chunks);
 
   float sx;
@@ -281,7 +285,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         it_next = it + waves;
       }
       const int row0 = it * rows_per_iter + slot * kRows;
-      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual>(b, packed, scales, output, sh,
+      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(b, packed, scales, output, sh,
                                                               it_next * rows_per_iter + slot * kRows, jb_next * NJ,
                                                               sub, chunks);
       compute_step<EPI, NJ, QREG, LANES, EXACT>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
@@ -301,7 +305,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         it_next = it + waves;
       }
       const int row0 = it * rows_per_iter + slot * kRows;
-      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual>(a, packed, scales, output, sh,
+      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
                                                               it_next * rows_per_iter + slot * kRows, jb_next * NJ,
                                                               sub, chunks);
       compute_step<EPI, NJ, QREG, LANES, EXACT>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
@@ -334,13 +338,39 @@ __device__ __forceinline__ int load_u16(const void* p) {
   asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
   return r;
 }
+// The same loads at a constant byte offset (-4096..4095) from p.
+template <int OFF>
+__device__ __forceinline__ v4i32 load_b128_at(const void* p) {
+  static_assert(OFF >= -4096 && OFF < 4096, "13-bit signed instruction offset");
+  v4i32 r;
+  asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(r) : "v"(p), "n"(OFF) : "memory");
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ int load_u16_at(const void* p) {
+  static_assert(OFF >= -4096 && OFF < 4096, "13-bit signed instruction offset");
+  int r;
+  asm volatile("global_load_ushort %0, %1, off offset:%2" : "=v"(r) : "v"(p), "n"(OFF) : "memory");
+  return r;
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): an
+// unrolled loop whose index can feed an immediate operand.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
 
 // Byte offset of gemv_rows_kernel's 16-byte dump slot: past the q8 row and
 // its chunk sums, 16-byte aligned.
 __host__ __device__ constexpr int rows_dump_offset(int chunks) { return (chunks * (kChunk + 4) + 15) & ~15; }
 
-// One step of a row pair in flight: the two rows' 16 weight bytes of the
-// lane's chunk and the group scale of the lane's own row.
+// One step of a row pair in flight: the 16 weight bytes of the lane's chunk in
+// its own row (w0) and in its partner's row (w1), and the group scale of the
+// lane's own row.
 struct RowStep {
   v4i32 w0, w1;
   int s;
@@ -386,14 +416,44 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   // Loads that a layout does not need still go out, from the first bytes of
   // the packed matrix (the one operand every entry point passes), so that the
   // count of loads per step stays fixed.
-  auto issue_step = [&](RowStep& st, int row_pair, int step) {
-    const int u = min(step * 64 + sub, chunks - 1);
+  //
+  // With EXACT (K a multiple of 4096) no chunk is clamped, so a row pair's
+  // loads sit at fixed offsets from three bases: step s reads 1024*s bytes
+  // past the lane's first weight bytes and 64*s bytes past its first scale.
+  // The weight bases point 4096 bytes in, so the offsets of all 8 steps fit
+  // the instruction's signed 13-bit field.
+  constexpr int kMid = 4096;
+  static_assert(STEPS <= 8, "step offsets -4096 .. 3072");
+  struct PairBase {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const void* s;
+  };
+  auto pair_base = [&](int row_pair) {
+    PairBase b;
     const int r0 = min(row_pair * kRows, sh.rows - 1), r1 = min(row_pair * kRows + 1, sh.rows - 1);
     const int own = (sub & 1) ? r1 : r0;
-    st.w0 = load_b128(packed + (size_t)r0 * sh.row_bytes + (size_t)u * 16);
-    st.w1 = load_b128(packed + (size_t)r1 * sh.row_bytes + (size_t)u * 16);
-    st.s = load_u16(kScales ? static_cast<const void*>(scales + (size_t)own * sh.groups + (u >> 1))
-                            : static_cast<const void*>(packed));
+    b.w0 = packed + (size_t)own * sh.row_bytes + sub * 16 + kMid;
+    b.w1 = packed + (size_t)((sub & 1) ? r0 : r1) * sh.row_bytes + sub * 16 + kMid;
+    b.s = kScales ? static_cast<const void*>(scales + (size_t)own * sh.groups + (sub >> 1))
+                  : static_cast<const void*>(packed);
+    return b;
+  };
+  auto issue_step = [&](RowStep& st, const PairBase& pb, int row_pair, auto step_c) {
+    constexpr int step = decltype(step_c)::value;
+    if constexpr (EXACT) {
+      st.w0 = load_b128_at<step * 1024 - kMid>(pb.w0);
+      st.w1 = load_b128_at<step * 1024 - kMid>(pb.w1);
+      st.s = load_u16_at<step * 64>(pb.s);
+    } else {
+      const int u = min(step * 64 + sub, chunks - 1);
+      const int r0 = min(row_pair * kRows, sh.rows - 1), r1 = min(row_pair * kRows + 1, sh.rows - 1);
+      const int own = (sub & 1) ? r1 : r0;
+      st.w0 = load_b128(packed + (size_t)own * sh.row_bytes + (size_t)u * 16);
+      st.w1 = load_b128(packed + (size_t)((sub & 1) ? r0 : r1) * sh.row_bytes + (size_t)u * 16);
+      st.s = load_u16(kScales ? static_cast<const void*>(scales + (size_t)own * sh.groups + (u >> 1))
+                              : static_cast<const void*>(packed));
+    }
   };
   // Bias and residual base of the lane's own row.
   auto issue_side = [&](int row_pair, int& b, int& base) {
@@ -411,8 +471,8 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   int it = blockIdx.x * (kBlock / 64) + (tid >> 6);
   int b_cur, base_cur;
   issue_side(it, b_cur, base_cur);
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) issue_step(st[s], it, s);
+  PairBase pb = pair_base(it);
+  static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
 
   asm volatile("s_waitcnt vmcnt(%5)"
                : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv)
@@ -434,9 +494,8 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     const int it_next = it + waves;
     int b_next, base_next;
     float acc = 0.0f;
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      if (s == 0) {
+    static_for<STEPS>([&](auto s) {
+      if constexpr (decltype(s)::value == 0) {
         asm volatile("s_waitcnt vmcnt(%5)"
                      : "+v"(st[0].w0), "+v"(st[0].w1), "+v"(st[0].s), "+v"(b_cur), "+v"(base_cur)
                      : "n"(3 * (STEPS - 1))
@@ -453,10 +512,13 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
       view.s[0] = (uint16_t)st[s].s;
       compute_step<EPI, 1, false, 64, EXACT>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0, s,
                                              sub, chunks);
-      if (s == 0) issue_side(it_next, b_next, base_next);
-      issue_step(st[s], it_next, s);
+      if constexpr (decltype(s)::value == 0) {
+        issue_side(it_next, b_next, base_next);
+        pb = pair_base(it_next);
+      }
+      issue_step(st[s], pb, it_next, s);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
     if constexpr (EPI != kPartials) {
       acc = pair_tree_sum(acc, 64);
       const int row = row0 + (sub & 1);

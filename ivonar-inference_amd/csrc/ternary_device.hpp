@@ -78,10 +78,26 @@ __device__ __forceinline__ int word_code_dot(unsigned w, int4 q, int& a1, int& a
   return 0;
 }
 
+// v_dot4_i32_i8 in its three-operand form, seeded from c or from zero.  The
+// compiler prefers v_dot4c, whose accumulator is also its destination, and so
+// spends a v_mov per accumulator to seed it (four per row and chunk).
+__device__ __forceinline__ int sdot4_seed(unsigned a, int b, int c) {
+  int d;
+  asm("v_dot4_i32_i8 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ int sdot4_zero(unsigned a, int b) {
+  int d;
+  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
 __device__ __forceinline__ int chunk_code_dot(const uint4 w, const int4 q0, const int4 q1, const int4 q2,
                                               const int4 q3, int acc) {
-  int a1 = acc, a4 = 0, a16 = 0;
-  word_code_dot(w.x, q0, a1, a4, a16);
+  int a1 = sdot4_seed(w.x & 0x03030303u, q0.x, acc);
+  int a4 = sdot4_zero(w.x & 0x0c0c0c0cu, q0.y);
+  int a16 = sdot4_zero(w.x & 0x30303030u, q0.z);
+  a16 = sdot4((w.x >> 2) & 0x30303030u, q0.w, a16);
   word_code_dot(w.y, q1, a1, a4, a16);
   word_code_dot(w.z, q2, a1, a4, a16);
   word_code_dot(w.w, q3, a1, a4, a16);
