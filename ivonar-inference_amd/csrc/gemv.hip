@@ -102,7 +102,7 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
 // forms both rows' chunk sums (its own row's first), sends the partner's row
 // across the pair (one DPP swap) and adds the partner's sum for its own row:
 // the exact group partial P[own row, g].
-template <int EPI, int NJ, bool QREG, int LANES, bool EXACT>
+template <int EPI, int NJ, bool QREG, int LANES, bool EXACT, bool XNEG = false>
 __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr)[QREG ? NJ : 1][4],
                                              const int (&xr)[QREG ? NJ : 1], const int4* __restrict__ lds_q,
                                              const int* __restrict__ lds_x, float& acc,
@@ -132,8 +132,11 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
       q3 = lds_q[3 * chunks + u];
       xs = lds_x[u];
     }
-    int d0 = chunk_code_dot(st.w[j][0], q0, q1, q2, q3, -xs);
-    int d1 = chunk_code_dot(st.w[j][1], q0, q1, q2, q3, -xs);
+    const int seed = XNEG ? xs : -xs;  // XNEG: the LDS copy holds minus the chunk sums
+    // The partner's row first: its sum crosses the pair by DPP, which must not
+    // read a register the instruction just before it wrote.
+    int d1 = chunk_code_dot(st.w[j][1], q0, q1, q2, q3, seed);
+    int d0 = chunk_code_dot(st.w[j][0], q0, q1, q2, q3, seed);
     if constexpr (!EXACT) {
       d0 = live ? d0 : 0;
       d1 = live ? d1 : 0;
@@ -141,7 +144,7 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
     const int d = d0 + pair_swap(d1);
     if constexpr (EPI == kPartials) {
       const int row = row0 + (sub & 1);
-      if (group_live && row < sh.rows) partials[(size_t)row * sh.groups + g] = d;
+      if (group_live && row < sh.rows) partials[(size_t)row * sh.groups + g] = d >> 4;
     } else {
       const float contribution = EXACT || group_live ? (float)d : 0.0f;
       acc = __builtin_fmaf(contribution, h2f(st.s[j]), acc);
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
     if constexpr (EPI != kPartials) {
       acc = pair_tree_sum(acc, lanes);
       const int row = row0 + (sub & 1);
-      float y = acc * sx;
+      float y = acc * 0.0625f * sx;  // the folded sums carry chunk_code_dot's factor 16
       if (bias != nullptr && row < sh.rows) y = y + bias[row];
       if constexpr (EPI == kSiluPair) {
         const float up = __int_as_float(pair_swap(__float_as_int(y)));
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     const int e = k * kBlock + tid;
     *reinterpret_cast<v4i32*>(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = qv[k];
   }
-  *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = xv;
+  *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = -xv;  // minus the chunk sums
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   const int4 qr_unused[1][4] = {};
@@ -510,7 +513,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
       view.w[0][0] = __builtin_bit_cast(uint4, st[s].w0);
       view.w[0][1] = __builtin_bit_cast(uint4, st[s].w1);
       view.s[0] = (uint16_t)st[s].s;
-      compute_step<EPI, 1, false, 64, EXACT>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0, s,
+      compute_step<EPI, 1, false, 64, EXACT, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0, s,
                                              sub, chunks);
       if constexpr (decltype(s)::value == 0) {
         issue_side(it_next, b_next, base_next);
@@ -522,7 +525,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     if constexpr (EPI != kPartials) {
       acc = pair_tree_sum(acc, 64);
       const int row = row0 + (sub & 1);
-      float y = acc * sx;
+      float y = acc * 0.0625f * sx;  // the folded sums carry chunk_code_dot's factor 16
       if (bias != nullptr) y = y + __int_as_float(b_cur);
       if constexpr (EPI == kSiluPair) {
         const float up = __int_as_float(pair_swap(__float_as_int(y)));

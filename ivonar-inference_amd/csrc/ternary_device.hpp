@@ -63,13 +63,18 @@ __device__ __forceinline__ int sdot4(unsigned a, int b, int c) {
   return __builtin_amdgcn_sdot4((int)a, b, c, false);
 }
 
-// Sum over one 64-input chunk of code * q: 16 packed words against 16 q8 words.
+// Sum over one 64-input chunk of code * q, times 16 (chunk_code_dot): 16
+// packed words against 16 q8 words.
 // Each packed word w holds 16 codes as four byte-wise 2-bit fields; instead of
 // shifting every field down (7 ops), the fields are isolated in place with
 // masks (w & 0x03, w & 0x0c, w & 0x30 per byte, and (w >> 2) & 0x30 for the
 // top field: 5 ops), so the dot products see code, 4*code and 16*code.  Three
-// accumulators keep those weights apart and are recombined exactly
-// (a multiple of 4 or 16 shifts right without loss).
+// accumulators keep those weights apart and are recombined as
+// 16*a1 + 4*a4 + a16 = 16 * (sum of code * q): two shift-adds instead of two
+// shifts and an add.  A float scaled by 16 rounds exactly like the unscaled
+// value in every later product and sum (no overflow, and the magnitudes here
+// never reach the subnormal range), so callers fold the scaled sums and drop
+// the factor once per output.
 __device__ __forceinline__ int word_code_dot(unsigned w, int4 q, int& a1, int& a4, int& a16) {
   a1 = sdot4(w & 0x03030303u, q.x, a1);
   a4 = sdot4(w & 0x0c0c0c0cu, q.y, a4);
@@ -101,7 +106,11 @@ __device__ __forceinline__ int chunk_code_dot(const uint4 w, const int4 q0, cons
   word_code_dot(w.y, q1, a1, a4, a16);
   word_code_dot(w.z, q2, a1, a4, a16);
   word_code_dot(w.w, q3, a1, a4, a16);
-  return a1 + (a4 >> 2) + (a16 >> 4);
+  // Two shift-adds: the empty asm keeps the compiler from merging them into
+  // two shifts and a three-way add.
+  int t = (a4 << 2) + a16;
+  asm("" : "+v"(t));
+  return (a1 << 4) + t;
 }
 
 // Lane value of the partner in the same lane pair (quad_perm [1,0,3,2]).
