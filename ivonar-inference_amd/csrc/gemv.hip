@@ -277,7 +277,10 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
 
   // Rolling pipeline over items (row step, block of NJ steps): the next
   // item's weights are in flight while the current one is computed.
-  const int blocks_per_row = (steps + NJ - 1) / NJ;
+  // With q8 in registers an item is a whole row (NJ == steps, the host's
+  // layouts): jb stays 0, and saying so lets the step offsets fold into the
+  // loads' immediate offsets.
+  const int blocks_per_row = QREG ? 1 : (steps + NJ - 1) / NJ;
   int jb = 0;
   float acc = 0.0f;
   while (it < sh.iters) {
@@ -288,11 +291,12 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         it_next = it + waves;
       }
       const int row0 = it * rows_per_iter + slot * kRows;
+      const int j_next = QREG ? 0 : jb_next * NJ;
       load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(b, packed, scales, output, sh,
-                                                              it_next * rows_per_iter + slot * kRows, jb_next * NJ,
-                                                              sub, chunks);
-      compute_step<EPI, NJ, QREG, LANES, EXACT>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
-                                                chunks);
+                                                                     it_next * rows_per_iter + slot * kRows, j_next,
+                                                                     sub, chunks);
+      compute_step<EPI, NJ, QREG, LANES, EXACT>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
+                                                QREG ? 0 : jb * NJ, sub, chunks);
       if (jb == blocks_per_row - 1) {
         finish(acc, row0, a.base);
         acc = 0.0f;
@@ -308,11 +312,12 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         it_next = it + waves;
       }
       const int row0 = it * rows_per_iter + slot * kRows;
+      const int j_next = QREG ? 0 : jb_next * NJ;
       load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
-                                                              it_next * rows_per_iter + slot * kRows, jb_next * NJ,
-                                                              sub, chunks);
-      compute_step<EPI, NJ, QREG, LANES, EXACT>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row0, jb * NJ, sub,
-                                                chunks);
+                                                                     it_next * rows_per_iter + slot * kRows, j_next,
+                                                                     sub, chunks);
+      compute_step<EPI, NJ, QREG, LANES, EXACT>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
+                                                QREG ? 0 : jb * NJ, sub, chunks);
       if (jb == blocks_per_row - 1) {
         finish(acc, row0, b.base);
         acc = 0.0f;
