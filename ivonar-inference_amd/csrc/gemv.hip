@@ -94,7 +94,7 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
     }
     st.s[j] = SCALES ? scales[(size_t)own_row * sh.groups + (u >> 1)] : (uint16_t)0;
   }
-  if constexpr (BASE) st.base = base[own_row];
+  st.base = BASE ? base[own_row] : 0.0f;
 }
 
 // Lane pair (sub, sub ^ 1) covers the two chunks of a group for rows row0 and
