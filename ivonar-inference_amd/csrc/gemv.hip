@@ -11,8 +11,9 @@
 // code*q minus the chunk's q sum, and one DPP swap (quad_perm [1,0,3,2])
 // adds the pair into the group partial P[r, g].  The pair folds
 // P * scale[r, g] into an fp32 fma chain over its groups (g = pair,
-// pair + lanes/2, ...); an xor butterfly over the pairs, the token scale and
-// the bias finish the row.  The CPU oracle restates that order bit for bit
+// pair + lanes/2, ...); a butterfly over the pairs in xor order (formed with
+// DPP row shifts and permlane swaps, pair_tree_sum), the token scale and the
+// bias finish the row.  The CPU oracle restates that order bit for bit
 // (orc_gemv_pairs).
 //
 // Memory.  Loads are unconditional: indices past the row or the matrix are
