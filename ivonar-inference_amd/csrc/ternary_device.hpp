@@ -118,8 +118,13 @@ __device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dp
 
 // Lane L reads lane L + N of its 16-lane row (lanes past the row read 0).
 template <int N>
+__device__ __forceinline__ int row_shl_int(int v) {
+  static_assert(N >= 1 && N <= 15, "DPP row_shl 1..15");
+  return __builtin_amdgcn_mov_dpp(v, 0x100 + N, 0xF, 0xF, true);
+}
+template <int N>
 __device__ __forceinline__ float row_shl(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + N, 0xF, 0xF, true));
+  return __int_as_float(row_shl_int<N>(__float_as_int(v)));
 }
 
 // Lanes of even 16-lane rows read the same lane of the next row; lanes of the
@@ -147,8 +152,17 @@ __device__ __forceinline__ float pair_tree_sum(float acc, int lanes) {
   return acc;
 }
 
+// Max over the wave, complete in lane 0 only (the other lanes hold partial
+// maxima): lane 0 at each stage reads a lane that has already folded its
+// share, as in pair_tree_sum.  The callers reduce absolute values (no -0),
+// whose fmaxf does not depend on the order.
 __device__ __forceinline__ float wave_max(float v) {
-  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));
+  v = fmaxf(v, row_shl<1>(v));
+  v = fmaxf(v, row_shl<2>(v));
+  v = fmaxf(v, row_shl<4>(v));
+  v = fmaxf(v, row_shl<8>(v));
+  v = fmaxf(v, row_swap16(v));
+  v = fmaxf(v, row_swap32(v));
   return v;
 }
 
@@ -171,9 +185,17 @@ __device__ __forceinline__ float block_max(float v, float* slots) {
 constexpr int kBatch = 16;
 
 // The block part of that tree, from each thread's fma partial.
+// The butterfly (offsets 16, 8, .., 1, s + s of lane L ^ o) is needed in
+// lanes 0 and 32 only: at stage o every lane their sums depend on is below o
+// within its half, so L ^ o = L + o, the lane a DPP row shift (o < 16) or
+// the row swap (o = 16) reads; same operands, same order.
 __device__ __forceinline__ float tree_reduce(float s, float* slots) {
   const int tid = threadIdx.x;
-  for (int offset = 16; offset > 0; offset >>= 1) s = s + __shfl_xor(s, offset);
+  s = s + row_swap16(s);
+  s = s + row_shl<8>(s);
+  s = s + row_shl<4>(s);
+  s = s + row_shl<2>(s);
+  s = s + row_shl<1>(s);
   if ((tid & 31) == 0) slots[tid >> 5] = s;
   __syncthreads();
   float total = 0.0f;
@@ -300,9 +322,13 @@ __device__ __forceinline__ int quantize_word(const RowSource& src, int u, int w,
 // Sum of the four int8 lanes of a word.
 __device__ __forceinline__ int word_sum(int word) { return sdot4((unsigned)word, 0x01010101, 0); }
 
-// Sum over the 16 consecutive lanes that hold one chunk's 16 words.
+// Sum over the 16 consecutive lanes that hold one chunk's 16 words, complete
+// in the first lane of each 16 (DPP row shifts; integer, so exact).
 __device__ __forceinline__ int chunk_lane_sum(int v) {
-  for (int offset = 1; offset < 16; offset <<= 1) v += __shfl_xor(v, offset);
+  v += row_shl_int<1>(v);
+  v += row_shl_int<2>(v);
+  v += row_shl_int<4>(v);
+  v += row_shl_int<8>(v);
   return v;
 }
 
