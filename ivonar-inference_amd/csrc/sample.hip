@@ -46,6 +46,21 @@ constexpr int kCandidates = 2048;                          // LDS candidate capa
 
 static_assert(kMaxTopK <= kSampleThreads, "one thread per pick");
 
+// Max or min of an unsigned key over the wave, complete in lane 0 only: DPP
+// row shifts and permlane swaps, each stage reading a lane that has already
+// folded its share (max and min do not depend on the order).
+template <bool MAX>
+__device__ __forceinline__ unsigned wave_extreme(unsigned k) {
+  auto pick = [](unsigned a, unsigned b) { return MAX ? max(a, b) : min(a, b); };
+  k = pick(k, (unsigned)row_shl_int<1>((int)k));
+  k = pick(k, (unsigned)row_shl_int<2>((int)k));
+  k = pick(k, (unsigned)row_shl_int<4>((int)k));
+  k = pick(k, (unsigned)row_shl_int<8>((int)k));
+  k = pick(k, __float_as_uint(row_swap16(__uint_as_float(k))));
+  k = pick(k, __float_as_uint(row_swap32(__uint_as_float(k))));
+  return k;
+}
+
 struct Rule {
   float inv_t, pen, inv_pen;
 };
@@ -84,8 +99,7 @@ __global__ __launch_bounds__(kBoundsBlock) void bounds_kernel(const float* __res
   const Rule r = load_rule(temperature, penalty, inverse_penalty);
   const int i = g * kBoundGroup + (threadIdx.x & 63);
   unsigned key = i < vocab ? order_key(score_of(logits, seen, i, r)) : 0u;
-#pragma unroll
-  for (int offset = 32; offset >= 1; offset >>= 1) key = max(key, (unsigned)__shfl_xor((int)key, offset));
+  key = wave_extreme<true>(key);
   if ((threadIdx.x & 63) == 0) bounds[g] = key_value(key);
 }
 
@@ -140,8 +154,7 @@ __device__ void block_scan2(bool fa, bool fb, int& pa, int& pb, int& ta, int& tb
 }
 
 __device__ unsigned block_max_key(unsigned key, SampleShared& sh) {
-#pragma unroll
-  for (int offset = 32; offset >= 1; offset >>= 1) key = max(key, (unsigned)__shfl_xor((int)key, offset));
+  key = wave_extreme<true>(key);
   if (lane_id() == 0) sh.wave_key[wave_id()] = key;
   __syncthreads();
   unsigned best = 0u;
@@ -152,8 +165,7 @@ __device__ unsigned block_max_key(unsigned key, SampleShared& sh) {
 }
 
 __device__ unsigned block_min_u(unsigned v, SampleShared& sh) {
-#pragma unroll
-  for (int offset = 32; offset >= 1; offset >>= 1) v = min(v, (unsigned)__shfl_xor((int)v, offset));
+  v = wave_extreme<false>(v);
   if (lane_id() == 0) sh.wave_key[wave_id()] = v;
   __syncthreads();
   unsigned best = 0xffffffffu;
