@@ -81,14 +81,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
       if (i < n) consider(b[k], i);
     }
   }
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    const float other = __shfl_xor(value, offset);
-    const int other_index = __shfl_xor(index, offset);
+  // Wave reduction, complete in lane 0 only (DPP row shifts and permlane
+  // swaps; each stage reads a lane that has already folded its share, and
+  // the (value, smaller index) order over NaN-free values does not depend on
+  // the pairing).
+  auto take = [&](float other, int other_index) {
     if (other > value || (other == value && other_index < index)) {
       value = other;
       index = other_index;
     }
-  }
+  };
+  take(row_shl<1>(value), row_shl_int<1>(index));
+  take(row_shl<2>(value), row_shl_int<2>(index));
+  take(row_shl<4>(value), row_shl_int<4>(index));
+  take(row_shl<8>(value), row_shl_int<8>(index));
+  take(row_swap16(value), __float_as_int(row_swap16(__int_as_float(index))));
+  take(row_swap32(value), __float_as_int(row_swap32(__int_as_float(index))));
   if ((threadIdx.x & 63) == 0) {
     best_value[threadIdx.x >> 6] = value;
     best_index[threadIdx.x >> 6] = index;
