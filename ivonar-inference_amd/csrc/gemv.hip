@@ -393,15 +393,23 @@ struct RowStep {
 //
 // All loads of the kernel are issued as inline assembly in a fixed order, so
 // the number issued after any step's loads is a constant and the kernel
-// waits for exactly that step: vmcnt(3*(STEPS-1)) before step 0 and
-// vmcnt(3*(STEPS-1) + 2) before the others (the next row pair's bias and
-// residual base go out just before its step 0).  Vector memory loads return
-// in order, so a count that leaves only younger loads outstanding proves the
+// waits for exactly that step.  A row pair's bias and residual base are
+// loaded at the top of its own iteration, after its steps' weights, and
+// consumed at its end: vmcnt(3*(STEPS-1) + 2) before every step (younger:
+// the pair's later steps, its two side loads, the refills issued so far),
+// vmcnt(3*STEPS) before the epilogue (younger: the STEPS refills).  No value
+// an asm load writes is carried across the loop's back edge except the
+// step registers, which are rewritten in place (the compiler has no copy to
+// make of them); a value carried across the edge can be copied by the
+// compiler ahead of the wait that covers it.  Vector memory loads return in
+// order, so a count that leaves only younger loads outstanding proves the
 // step complete; stores only make the waits longer.  (Compiled loads would
 // get compiler-placed waits, which at this depth drain every load in flight
 // at loop joins.)  The q8 copy's loads go out first and are waited for with
-// the first row pair's weights still in flight.  Lane layout and fp32 order
-// are those of gemv_kernel (orc_gemv_pairs).
+// the first row pair's weights still in flight.  The build disassembles
+// these kernels and checks every VGPR access against the loads in flight
+// (asmcheck.py).  Lane layout and fp32 order are those of gemv_kernel
+// (orc_gemv_pairs).
 template <int EPI, int STEPS, bool EXACT>
 __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
@@ -478,14 +486,12 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
 
   RowStep st[STEPS];
   int it = blockIdx.x * (kBlock / 64) + (tid >> 6);
-  int b_cur, base_cur;
-  issue_side(it, b_cur, base_cur);
   PairBase pb = pair_base(it);
   static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
 
   asm volatile("s_waitcnt vmcnt(%5)"
                : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv)
-               : "n"(kSide + 3 * STEPS)
+               : "n"(3 * STEPS)
                : "memory");
   int4* dump = reinterpret_cast<int4*>(lds_raw + rows_dump_offset(chunks));
 #pragma unroll
@@ -501,48 +507,40 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   while (it < sh.iters) {
     const int row0 = it * kRows;
     const int it_next = it + waves;
-    int b_next, base_next;
+    // This row pair's bias and residual base, younger than its steps' weights.
+    int b_side, base_side;
+    issue_side(it, b_side, base_side);
+    pb = pair_base(it_next);
     float acc = 0.0f;
     static_for<STEPS>([&](auto s) {
-      if constexpr (decltype(s)::value == 0) {
-        asm volatile("s_waitcnt vmcnt(%5)"
-                     : "+v"(st[0].w0), "+v"(st[0].w1), "+v"(st[0].s), "+v"(b_cur), "+v"(base_cur)
-                     : "n"(3 * (STEPS - 1))
-                     : "memory");
-      } else {
-        asm volatile("s_waitcnt vmcnt(%3)"
-                     : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
-                     : "n"(3 * (STEPS - 1) + kSide)
-                     : "memory");
-      }
+      asm volatile("s_waitcnt vmcnt(%3)"
+                   : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
+                   : "n"(3 * (STEPS - 1) + kSide)
+                   : "memory");
       Step<1> view;
       view.w[0][0] = __builtin_bit_cast(uint4, st[s].w0);
       view.w[0][1] = __builtin_bit_cast(uint4, st[s].w1);
       view.s[0] = (uint16_t)st[s].s;
       compute_step<EPI, 1, false, 64, EXACT, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0, s,
                                              sub, chunks);
-      if constexpr (decltype(s)::value == 0) {
-        issue_side(it_next, b_next, base_next);
-        pb = pair_base(it_next);
-      }
       issue_step(st[s], pb, it_next, s);
       __builtin_amdgcn_sched_barrier(0);
     });
+    // Younger than the side loads: the STEPS refills of the next row pair.
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b_side), "+v"(base_side) : "n"(3 * STEPS) : "memory");
     if constexpr (EPI != kPartials) {
       acc = pair_tree_sum(acc, 64);
       const int row = row0 + (sub & 1);
       float y = acc * 0.0625f * sx;  // the folded sums carry chunk_code_dot's factor 16
-      if (bias != nullptr) y = y + __int_as_float(b_cur);
+      if (bias != nullptr) y = y + __int_as_float(b_side);
       if constexpr (EPI == kSiluPair) {
         const float up = __int_as_float(pair_swap(__float_as_int(y)));
         if (sub == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y) * up;
       } else if (sub < 2 && row < sh.rows) {
         if constexpr (EPI == kStore) output[row] = y;
-        else output[row] = __int_as_float(base_cur) + y;
+        else output[row] = __int_as_float(base_side) + y;
       }
     }
-    b_cur = b_next;
-    base_cur = base_next;
     it = it_next;
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the refills of the pass past the end

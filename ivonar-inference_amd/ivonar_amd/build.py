@@ -80,6 +80,16 @@ def _compile(source: Path, output: Path, hipcc: str) -> None:
         sys.stderr.write("\n".join(noise) + "\n")
 
 
+def check_waits(objects) -> None:
+    """Refuse code whose hand-placed vmcnt waits leave a VGPR access ahead of its load (asmcheck)."""
+    from .asmcheck import check_object
+
+    hazards = [hazard for obj in objects for hazard in check_object(Path(obj))]
+    if hazards:
+        listing = "\n".join(str(hazard) for hazard in hazards[:20])
+        raise RuntimeError(f"{len(hazards)} VGPR accesses precede the wait for their load:\n{listing}")
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source and link the shared library; returns its path."""
     hipcc = _hipcc()
@@ -91,6 +101,7 @@ def build(verbose: bool = False) -> Path:
     objects = [obj_dir / (Path(name).stem + ".o") for name in SOURCES]
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as pool:
         list(pool.map(lambda pair: _compile(CSRC / pair[0], pair[1], hipcc), zip(SOURCES, objects)))
+    check_waits(objects)
     temporary = LIBRARY.with_suffix(f".so.tmp{os.getpid()}")
     link = [
         os.environ.get("CXX", "g++"),

@@ -150,11 +150,12 @@ def initialise(device_index: int) -> None:
 
 
 class Kernel:
-    __slots__ = ("function", "name")
+    __slots__ = ("function", "name", "module")
 
-    def __init__(self, function, name: str) -> None:
+    def __init__(self, function, name: str, module: "Module | None" = None) -> None:
         self.function = function
         self.name = name
+        self.module = module
 
 
 class Launch:
@@ -180,28 +181,53 @@ class Launch:
             raise KernelError(f"{kernel.name} takes {expected} arguments, got {len(self._args)}")
 
     def __call__(self, stream: int) -> None:
+        module = self.kernel.module
+        if module is not None and _applied_defines is not module.define_values:
+            module.apply_defines()
         status = self.kernel.function(c_void_p(stream), *self._args)
         if status != 0:
             check(status, self.kernel.name)
 
 
+_DEFINES = ("HEAD_DIM", "TILE", "MAX_CHUNKS", "MAX_TOPK")
+_LIBRARY_DEFAULTS = {"HEAD_DIM": 64, "TILE": 32, "MAX_CHUNKS": 70, "MAX_TOPK": 256}
+# The define values the library currently holds (the tuple of the module that set them last).
+_applied_defines: tuple | None = None
+
+
 class Module:
+    """One configuration of the library: the reference's -D defines of ``compile_module``.
+
+    The library keeps one set of define values per process; every launch of a
+    module's kernel first makes that module's values current (a few host
+    calls, only when another module's launch ran in between), so modules with
+    different HEAD_DIM or TILE can be used side by side as in the reference,
+    where each define set is its own compiled module (``runtime.py:301-324``).
+    """
+
     def __init__(self, key: tuple, defines: Mapping[str, object]) -> None:
         self.key = key
         self.defines = dict(defines)
+        values = dict(_LIBRARY_DEFAULTS)
+        values.update({name: int(defines[name]) for name in _DEFINES if name in defines})
+        self.define_values = tuple(sorted(values.items()))
         self._kernels: dict[str, Kernel] = {}
+
+    def apply_defines(self) -> None:
+        global _applied_defines
+        lib = library()
+        for name, value in self.define_values:
+            check(lib.ivonar_define(name.encode(), int(value)), f"define {name}")
+        _applied_defines = self.define_values
 
     def kernel(self, name: str) -> Kernel:
         kernel = self._kernels.get(name)
         if kernel is None:
             if name not in SIGNATURES:
                 raise KernelError(f"the ternary library has no entry point {name!r}")
-            kernel = Kernel(getattr(library(), name), name)
+            kernel = Kernel(getattr(library(), name), name, self)
             self._kernels[name] = kernel
         return kernel
-
-
-_DEFINES = ("HEAD_DIM", "TILE", "MAX_CHUNKS", "MAX_TOPK")
 
 
 def compile_module(
@@ -209,9 +235,9 @@ def compile_module(
 ) -> Module:
     """Bind the prebuilt library for ``device`` and apply the reference's -D defines.
 
-    ``source`` is accepted for signature compatibility and ignored.  HEAD_DIM,
-    TILE, MAX_CHUNKS and MAX_TOPK are process-wide in this library (one decoder
-    configuration per process, as in the reference's single-flight engine).
+    ``source`` is accepted for signature compatibility and ignored.  The
+    module's HEAD_DIM, TILE, MAX_CHUNKS and MAX_TOPK are made current before
+    each of its launches.
     """
     del source, name
     device = torch.device(device)
@@ -220,10 +246,7 @@ def compile_module(
     if not torch.cuda.is_available():
         raise KernelError("no ROCm device is available for the ternary kernels")
     index = device.index if device.index is not None else torch.cuda.current_device()
-    lib = library()
-    for key in _DEFINES:
-        if key in defines:
-            check(lib.ivonar_define(key.encode(), int(defines[key])), f"define {key}")
+    library()
     initialise(index)
     key = (index, tuple(sorted((k, int(v)) for k, v in defines.items() if k in _DEFINES)))
     with _lock:
@@ -231,7 +254,8 @@ def compile_module(
         if module is None:
             module = Module(key, defines)
             _modules[key] = module
-        return module
+    module.apply_defines()  # rejects out-of-range values here, as NVRTC would at compile time
+    return module
 
 
 def pointer(tensor: torch.Tensor | None) -> c_void_p:
@@ -248,3 +272,81 @@ def float32(value: float) -> c_float:
 
 def current_stream(device: torch.device | None = None) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+class Driver:
+    """The device-context half of the reference's driver object (``kernels/runtime.py:140-191``).
+
+    The reference decoder calls four of its methods around its launches
+    (``kernel_decoder.py:226,274,448,518,552,677,684``):
+
+    * ``bind(device_index)`` makes the device current for the calling thread
+      before a launch sequence (the reference retains the CUDA primary
+      context and sets it current); here the HIP runtime's per-thread current
+      device is set, once per thread and device;
+    * ``persisting_capacity(device_index)`` is the persisting-L2 budget.  It
+      is 0 here: MI355X has no access-policy window, and its 256 MB Infinity
+      Cache keeps recently read weights without a hint, so the reference
+      decoder builds no arena and never calls the next two;
+    * ``reserve_persisting(device_index, nbytes)`` and
+      ``persist_on_stream(stream, base, nbytes)`` check their arguments and
+      set nothing.  A request above the capacity raises ``KernelError``, the
+      error the reference's caller already handles by switching persistence
+      off (``kernel_decoder.py:273-277``, ``:517-521``).
+    """
+
+    def __init__(self) -> None:
+        self._bound: dict[int, int] = {}
+        self._reserved: dict[int, int] = {}
+        self._lock = threading.Lock()
+
+    def check(self, status: int) -> None:
+        check(status, "HIP call")
+
+    def _device(self, device_index: int) -> int:
+        index = int(device_index)
+        if not torch.cuda.is_available():
+            raise KernelError("no ROCm device is available for the ternary kernels")
+        if index < 0 or index >= torch.cuda.device_count():
+            raise KernelError(f"HIP device {index} does not exist")
+        return index
+
+    def bind(self, device_index: int) -> None:
+        thread = threading.get_ident()
+        index = int(device_index)
+        if self._bound.get(thread) == index:
+            return
+        torch.cuda.set_device(self._device(index))
+        with self._lock:
+            self._bound[thread] = index
+
+    def persisting_capacity(self, device_index: int) -> int:
+        self._device(device_index)
+        return 0
+
+    def reserve_persisting(self, device_index: int, nbytes: int) -> None:
+        index = self._device(device_index)
+        if int(nbytes) < 0:
+            raise KernelError("a persisting-L2 reservation cannot be negative")
+        if int(nbytes) > self.persisting_capacity(index):
+            raise KernelError(f"device {index} has no persisting-L2 window for {int(nbytes)} bytes")
+        with self._lock:
+            self._reserved[index] = max(self._reserved.get(index, 0), int(nbytes))
+
+    def persist_on_stream(self, stream: int, base: int, nbytes: int) -> None:
+        if int(nbytes) < 0 or int(base) < 0 or int(stream) < 0:
+            raise KernelError("an access window needs a stream, a base address and a non-negative size")
+        if int(nbytes) > 0:
+            raise KernelError("this device has no access-policy window to persist weights in")
+
+
+_driver: Driver | None = None
+
+
+def driver() -> Driver:
+    """The process's ``Driver`` (one per process, as the reference's ``runtime.driver()``)."""
+    global _driver
+    with _lock:
+        if _driver is None:
+            _driver = Driver()
+        return _driver

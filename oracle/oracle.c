@@ -400,49 +400,54 @@ void orc_partials_i8(const int8_t* w, int rows, int k, const int8_t* q, int32_t*
 void orc_finish(int order, int param, int epi, const int32_t* partials, const uint16_t* scales, int groups_stride,
                 const float* scale_in, const float* bias, float* out, int rows, int k, int out_stride, int m) {
   const int groups = (k + 127) / 128;
-  float* y = (float*)malloc(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
-  float* acc = (float*)malloc(sizeof(float) * (size_t)(param > 0 ? param : 1));
-  float* next = (float*)malloc(sizeof(float) * (size_t)(param > 0 ? param : 1));
-  for (int t = 0; t < m; ++t) {
-    for (int r = 0; r < rows; ++r) {
-      const int32_t* p = partials + ((size_t)t * rows + r) * groups;
-      const uint16_t* s = scales + (size_t)r * groups_stride;
-      float total = 0.0f;
-      if (order == 0) {
-        const int pairs = param / 2;
-        for (int i = 0; i < pairs; ++i) acc[i] = 0.0f;
-        for (int g = 0; g < groups; ++g) acc[g % pairs] = fmaf((float)p[g], orc_h2f(s[g]), acc[g % pairs]);
-        for (int offset = 1; offset < pairs; offset <<= 1) {
-          for (int i = 0; i < pairs; ++i) next[i] = acc[i] + acc[i ^ offset];
-          memcpy(acc, next, sizeof(float) * (size_t)pairs);
+  /* Tokens are independent: each thread finishes whole token rows with buffers of its own. */
+#pragma omp parallel
+  {
+    float* y = (float*)malloc(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
+    float* acc = (float*)malloc(sizeof(float) * (size_t)(param > 0 ? param : 1));
+    float* next = (float*)malloc(sizeof(float) * (size_t)(param > 0 ? param : 1));
+#pragma omp for schedule(static)
+    for (int t = 0; t < m; ++t) {
+      for (int r = 0; r < rows; ++r) {
+        const int32_t* p = partials + ((size_t)t * rows + r) * groups;
+        const uint16_t* s = scales + (size_t)r * groups_stride;
+        float total = 0.0f;
+        if (order == 0) {
+          const int pairs = param / 2;
+          for (int i = 0; i < pairs; ++i) acc[i] = 0.0f;
+          for (int g = 0; g < groups; ++g) acc[g % pairs] = fmaf((float)p[g], orc_h2f(s[g]), acc[g % pairs]);
+          for (int offset = 1; offset < pairs; offset <<= 1) {
+            for (int i = 0; i < pairs; ++i) next[i] = acc[i] + acc[i ^ offset];
+            memcpy(acc, next, sizeof(float) * (size_t)pairs);
+          }
+          total = acc[0];
+        } else {
+          const int per = (groups + param - 1) / param;
+          for (int sp = 0; sp < param; ++sp) {
+            const int begin = sp * per < groups ? sp * per : groups;
+            const int end = begin + per < groups ? begin + per : groups;
+            float a = 0.0f;
+            for (int g = begin; g < end; ++g) a = fmaf((float)p[g], orc_h2f(s[g]), a);
+            total = sp == 0 ? a : total + a;
+          }
         }
-        total = acc[0];
-      } else {
-        const int per = (groups + param - 1) / param;
-        for (int sp = 0; sp < param; ++sp) {
-          const int begin = sp * per < groups ? sp * per : groups;
-          const int end = begin + per < groups ? begin + per : groups;
-          float a = 0.0f;
-          for (int g = begin; g < end; ++g) a = fmaf((float)p[g], orc_h2f(s[g]), a);
-          total = sp == 0 ? a : total + a;
+        float v = total * scale_in[t];
+        if (bias) v = v + bias[r];
+        y[r] = v;
+      }
+      float* orow = out + (size_t)t * out_stride;
+      for (int r = 0; r < rows; ++r) {
+        if (epi == EPI_SILU_PAIR) {
+          if ((r & 1) == 0 && r + 1 < rows) epilogue(epi, orow, r >> 1, r, y[r], y[r + 1]);
+        } else {
+          epilogue(epi, orow, r, r, y[r], 0.0f);
         }
       }
-      float v = total * scale_in[t];
-      if (bias) v = v + bias[r];
-      y[r] = v;
     }
-    float* orow = out + (size_t)t * out_stride;
-    for (int r = 0; r < rows; ++r) {
-      if (epi == EPI_SILU_PAIR) {
-        if ((r & 1) == 0 && r + 1 < rows) epilogue(epi, orow, r >> 1, r, y[r], y[r + 1]);
-      } else {
-        epilogue(epi, orow, r, r, y[r], 0.0f);
-      }
-    }
+    free(next);
+    free(acc);
+    free(y);
   }
-  free(next);
-  free(acc);
-  free(y);
 }
 
 /* First index of the maximum (greedy decoding). */

@@ -67,3 +67,54 @@ def assert_bits_equal(actual, expected, what: str = "") -> None:
         index = np.argwhere(~same)[0]
         raise AssertionError(f"{what}: {int((~same).sum())} of {same.size} differ; first at {tuple(index)}: "
                              f"{actual[tuple(index)]!r} vs {expected[tuple(index)]!r}")
+
+
+def big_layer(rng: np.random.Generator, rows: int, k: int, p=(0.3, 0.4, 0.3), scale: str = "abs_normal",
+              sigma: float = 0.02, mu: float = -4.0, bias: bool = False, block: int = 2048):
+    """(codes uint8 [rows, k], packed16, scale bits, bias or None) for matrices of up to a few hundred million
+    weights, drawn in row blocks so that no float64 copy of the whole matrix is made."""
+    import ternary_oracle as T
+    from ivonar_amd import synthetic
+
+    codes = np.empty((rows, k), dtype=np.uint8)
+    for start in range(0, rows, block):
+        codes[start:start + block] = synthetic.sample_codes(rng, min(block, rows - start), k, p)
+    packed = T.pad_rows16(synthetic.pack_codes(codes))
+    groups = math.ceil(k / 128)
+    if scale == "lognormal":
+        scales = synthetic.lognormal_scales(rng, rows, groups, mu, sigma)
+    else:
+        scales = synthetic.abs_normal_scales(rng, rows, groups, sigma, 1e-4)
+    b = (rng.normal(0.0, 0.02, size=rows)).astype(np.float32) if bias else None
+    return codes, packed, scales.view(np.uint16), b
+
+
+def exact_partials(codes: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """P[t, r, g] = sum_{i in g} (code[r, i] - 1) * q[t, i] as int32 [M, rows, G], for many tokens at once.
+
+    Computed with float32 matrix products per 128-input group: every term is an integer of magnitude at
+    most 127 and a group has at most 128 of them, so every partial sum in any summation order is an
+    integer below 2**24 and exact in float32."""
+    q = np.atleast_2d(q)
+    m, k = q.shape
+    rows = codes.shape[0]
+    groups = math.ceil(k / 128)
+    out = np.empty((m, rows, groups), dtype=np.int32)
+    for g in range(groups):
+        lo, hi = g * 128, min(k, g * 128 + 128)
+        w = codes[:, lo:hi].astype(np.float32) - np.float32(1.0)
+        out[:, :, g] = np.rint(q[:, lo:hi].astype(np.float32) @ w.T).astype(np.int32)
+    return out
+
+
+def finish_all_rows(oracle, order: int, param: int, epi: int, codes: np.ndarray, q: np.ndarray, scale_bits,
+                    sx: np.ndarray, bias, out: np.ndarray, k: int, out_stride: int) -> np.ndarray:
+    """Every output row of a token GEMM (order 1: K-split `param`) or GEMV (order 0: `param` lanes) in the
+    kernel's fp32 order, from exact partials; tokens in blocks of at most 64M partials (256 MB)."""
+    m = q.shape[0]
+    block = max(1, min(m, (64 << 20) // max(1, codes.shape[0] * math.ceil(k / 128))))
+    for start in range(0, m, block):
+        stop = min(m, start + block)
+        partials = exact_partials(codes, q[start:stop])
+        oracle.finish(order, param, epi, partials, scale_bits, sx[start:stop], bias, out[start:stop], k, out_stride)
+    return out

@@ -14,8 +14,8 @@ import numpy as np
 import pytest
 
 import ternary_oracle as T
-from _util import (ATOL, RTOL, assert_bits_equal, assert_within, device_matrix, make_layer, reference_lanes,
-                   to_np)
+from _util import (ATOL, RTOL, assert_bits_equal, assert_within, device_matrix, finish_all_rows, make_layer,
+                   reference_lanes, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -26,6 +26,16 @@ def _t(array, device):
     import torch
 
     return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+def _every_row(oracle, codes, x, k, scale_bits, bias, splits, epi=None, out=None, stride=None):
+    """The token GEMM's expected output for every token and row, in the kernel's split order."""
+    m, rows = x.shape[0], codes.shape[0]
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    epi = T.EPI_STORE if epi is None else epi
+    out = np.zeros((m, rows), np.float32) if out is None else out
+    return finish_all_rows(oracle, 1, splits, epi, codes, T.q8_linear(eq8, k), scale_bits, esx, bias, out, k,
+                           rows if stride is None else stride)
 
 
 # ------------------------------------------------------------------ quantizer
@@ -412,9 +422,9 @@ def test_invalid_arguments_raise(cuda):
 
 
 @pytest.mark.parametrize("m,k,rows", [(2048, 1024, 4096), (2048, 4096, 1024), (512, 1100, 4096), (300, 4096, 2048)])
-def test_gemm_large_tiles_on_sampled_tokens(cuda, oracle, m, k, rows):
-    """The large block shapes are chosen only at big M: check every row of a sample of tokens bit for bit
-    (each output depends only on its own token row), and the whole output against the fp64 truth."""
+def test_gemm_large_tiles_every_token(cuda, oracle, m, k, rows):
+    """The large block shapes are chosen only at big M: every output bit for bit against the oracle's
+    split order, from exact partials."""
     from ivonar_amd import ops, runtime
 
     rng = np.random.default_rng(m + k + rows)
@@ -423,13 +433,9 @@ def test_gemm_large_tiles_on_sampled_tokens(cuda, oracle, m, k, rows):
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
-    sample = np.unique(np.array([0, 1, 63, 64, 127, 128, 255, 256, m // 2, m - 1]) % m)
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     splits = runtime.gemm_plan(m, rows, k)
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), splits)
-    assert_bits_equal(y[sample], expected, f"sampled tokens ({splits} splits)")
-    assert np.isfinite(y).all()
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, splits)
+    assert_bits_equal(y, expected, f"every token ({splits} splits)")
 
 
 @pytest.mark.parametrize("m", [1, 3, 16, 32])
@@ -457,7 +463,7 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
 # The two skinny kernels (M <= 32): the token bytes staged in LDS per wave (8, 4, 2 or 1 K-splits by
 # group count; one row tile per wave, two or four from 768 row tiles on) and, when a wave's share does not
 # fit there, the token operand read per wave from the caches (one or two row tiles per wave).  Odd
-# chunk counts with several groups, ragged rows, bias; sampled tokens against the oracle's split
+# chunk counts with several groups, ragged rows, bias; every token against the oracle's split
 # order.
 @pytest.mark.parametrize("m,k,rows,bias,splits", [(7, 4160, 1000, True, 8), (32, 2112, 1000, False, 8),
                                                   (20, 1088, 8200, True, 8), (1, 8192, 8192, False, 8),
@@ -474,12 +480,7 @@ def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     assert runtime.gemm_plan(m, rows, k) == splits
-    sample = np.unique(np.array([0, 3, 15, 16, m - 1]) % m)
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), splits)
-    assert_bits_equal(y[sample], expected, f"sampled tokens ({splits} splits)")
-    assert np.isfinite(y).all()
+    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, splits), f"every token ({splits} splits)")
 
 
 # Prompts of 33..512 tokens that neither long-prompt tiling takes (few row blocks, few groups) run the
@@ -497,12 +498,7 @@ def test_gemm_sliced_skinny(cuda, oracle, m, k, rows, bias, splits):
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     assert runtime.gemm_plan(m, rows, k) == splits
-    sample = np.unique(np.array([0, 15, 16, 31, 32, 33, 63, 64, m // 2, m - 2, m - 1]) % m)
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), splits)
-    assert_bits_equal(y[sample], expected, f"sampled tokens ({splits} splits)")
-    assert np.isfinite(y).all()
+    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, splits), f"every token ({splits} splits)")
 
 
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
@@ -569,13 +565,8 @@ def test_gemm_wide_tiles_edges(cuda, oracle, m, k, rows, bias):
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
-    sample = np.unique(np.array([0, 1, 15, 16, 127, 128, 129, 255, m // 2, m - 2, m - 1]) % m)
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     assert runtime.gemm_plan(m, rows, k) == 1
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), 1)
-    assert_bits_equal(y[sample], expected, "sampled tokens")
-    assert np.isfinite(y).all()
+    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, 1), "every token")
 
 
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
@@ -594,16 +585,13 @@ def test_gemm_wide_tiles_epilogues(cuda, oracle, epilogue):
     base = rng.standard_normal((m, stride)).astype(np.float32)
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
-    sample = np.array([0, 5, 127, 128, 255, 256, 299])
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
-    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
-                                 len(sample), 1)
-    assert_bits_equal(to_np(out)[sample], expected, epilogue)
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, 1, epi, base.copy(), stride)
+    assert_bits_equal(to_np(out), expected, epilogue)
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
-# 128-token tiles (2048 inputs and more) with both epilogues, on sampled tokens: 192 blocks of 128
+# 128-token tiles (2048 inputs and more) with both epilogues, every token: 192 blocks of 128
 # tokens x 256 rows.
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
 def test_gemm_wide_128_token_tiles_epilogues(cuda, oracle, epilogue):
@@ -622,12 +610,9 @@ def test_gemm_wide_128_token_tiles_epilogues(cuda, oracle, epilogue):
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
     assert runtime.gemm_plan(m, rows, k) == 1
-    sample = np.array([0, 1, 127, 128, 500, 1023])
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
-    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
-                                 len(sample), 1)
-    assert_bits_equal(to_np(out)[sample], expected, epilogue)
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, 1, epi, base.copy(), stride)
+    assert_bits_equal(to_np(out), expected, epilogue)
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
@@ -648,15 +633,12 @@ def test_gemm_split_k_edges(cuda, oracle, m, k, rows, bias):
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     assert runtime.gemm_plan(m, rows, k) == 4
+    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, 4), "every token (4 splits)")
     sample = np.unique(np.array([0, 1, 31, 32, 95, 127, 128, 129, m // 2, m - 2, m - 1]) % m)
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                                 np.zeros((len(sample), rows), np.float32), k, rows, len(sample), 4)
-    assert_bits_equal(y[sample], expected, "sampled tokens (4 splits)")
     ref = oracle.reforder(T.EPI_STORE, True, eq8, exsum, esx, packed, scale_bits, b,
                           np.zeros((len(sample), rows), np.float32), k, reference_lanes(k, rows), rows, len(sample))
     assert_within(y[sample], ref, what="split-K GEMM vs reference-kernel order")
-    assert np.isfinite(y).all()
 
 
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
@@ -676,10 +658,7 @@ def test_gemm_split_k_epilogues(cuda, oracle, epilogue):
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
     assert runtime.gemm_plan(m, rows, k) == 4
-    sample = np.array([0, 7, 127, 128, 200, 255])
-    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     epi = T.EPI_RESIDUAL if epilogue == "residual" else T.EPI_SILU_PAIR
-    expected = oracle.gemm_split(epi, eq8, exsum, esx, packed, scale_bits, b, base[sample].copy(), k, stride,
-                                 len(sample), 4)
-    assert_bits_equal(to_np(out)[sample], expected, epilogue)
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, 4, epi, base.copy(), stride)
+    assert_bits_equal(to_np(out), expected, epilogue)
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
