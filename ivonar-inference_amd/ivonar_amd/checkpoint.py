@@ -3,10 +3,12 @@ config.py:6-74 the configuration contract, kernel_decoder.py:53-142 and :230-262
 
 ``load_checkpoint(path)`` reads an Ivonar packed checkpoint with ``torch.load(weights_only=True)``
 (nothing in the file is executed), checks its format, schema, tokenizer hash and configuration contract,
-that every state entry is a tensor of the right dtype and that the key set is exactly the model's, and
-returns the ternary linear path on the host.  ``LinearPath.matrices(device)`` uploads it as device
-``Matrix`` groups fused the way the reference decoder launches them, and validates every operand on the
-device (``ivonar_validate_ternary``: reserved code 3, non-finite or non-positive scales):
+every state entry (a tensor of the right dtype; packed buffers free of the reserved code 3, scales finite
+and positive) and that the key set is exactly the model's, and returns the ternary linear path on the
+host.  ``LinearPath.matrices(device)`` uploads it as device
+``Matrix`` groups fused the way the reference decoder launches them, and checks every uploaded operand
+again on the device (``ivonar_validate_ternary``), so operands built from host tensors that never went
+through the loader are covered too:
 
 * token matrix: ``token_io.projection`` (4 lanes, the LM head and the embedding);
 * per ``mamba`` block: ``entry`` = [in_proj, bc_dt_proj], ``out`` = [out_proj];
@@ -53,9 +55,35 @@ REQUIRED_CONTRACT = {
 FLAG_RESERVED_CODE, FLAG_NONFINITE_SCALE, FLAG_NONPOSITIVE_SCALE = 1, 2, 4
 
 
+def _dense_width(config: dict[str, Any], hidden: int) -> int:
+    return int(config.get("dense_intermediate_dim", 0) or max(int(config.get("intermediate_dim", 0)), 4 * hidden))
+
+
+def _latent_width(config: dict[str, Any], hidden: int) -> int:
+    return int(config.get("mla_latent_dim", 0) or max(128, hidden // 4))
+
+
+# The configuration fields (config.py:20-74): field name, payload key, type, and the default when the key
+# is optional (None: required).  Widths that depend on others are filled in afterwards.
+_CONFIG_FIELDS = (
+    ("name", "name", str, ""),
+    ("vocab_size", "vocab_size", int, None),
+    ("seq_len", "seq_len", int, None),
+    ("hidden_dim", "hidden_dim", int, None),
+    ("num_layers", "num_layers", int, None),
+    ("num_heads", "num_heads", int, None),
+    ("state_dim", "state_dim", int, None),
+    ("base_context", "base_context", int, 8192),
+    ("final_context", "final_context", int, 8192),
+    ("rope_base", "rope_base", float, 10000.0),
+    ("longrope_scaling", "longrope_scaling", str, "linear"),
+)
+_LAYER_KINDS = ("mamba", "mla")
+
+
 @dataclass(frozen=True)
 class CheckpointConfig:
-    """config.py:20-74: the configuration fields running the model needs."""
+    """The configuration fields running the model needs (semantics of config.py:20-74)."""
 
     name: str
     vocab_size: int
@@ -74,87 +102,131 @@ class CheckpointConfig:
 
     @classmethod
     def from_payload(cls, config: Any) -> "CheckpointConfig":
+        """Parse and check a payload's ``config`` dict: the contract, no experts, one known kind per layer."""
         if not isinstance(config, dict):
             raise ValueError("checkpoint config is invalid")
-        mismatches = [f"{key}={config.get(key)!r}" for key, expected in REQUIRED_CONTRACT.items()
-                      if config.get(key) != expected]
-        if mismatches:
-            raise ValueError("incompatible Ivonar checkpoint: " + ", ".join(mismatches))
+        wrong = [f"{key}={config.get(key)!r}" for key in REQUIRED_CONTRACT if config.get(key) != REQUIRED_CONTRACT[key]]
+        if wrong:
+            raise ValueError("incompatible Ivonar checkpoint: " + ", ".join(wrong))
         if int(config.get("num_experts", 0)) > 0:
             raise ValueError("mixture-of-experts checkpoints are not supported")
-        hidden = int(config["hidden_dim"])
-        layers = int(config["num_layers"])
-        kinds = tuple(str(kind) for kind in config.get("layer_types") or ())
-        if not kinds:
-            kinds = tuple("mamba" for _ in range(layers))
-        if len(kinds) != layers or any(kind not in {"mamba", "mla"} for kind in kinds):
+        values = {name: kind(config[key] if default is None else config.get(key, default))
+                  for name, key, kind, default in _CONFIG_FIELDS}
+        kinds = tuple(map(str, config.get("layer_types") or ())) or ("mamba",) * values["num_layers"]
+        if len(kinds) != values["num_layers"] or not set(kinds) <= set(_LAYER_KINDS):
             raise ValueError("layer_types must name mamba or mla for every layer")
-        return cls(
-            name=str(config.get("name", "")),
-            vocab_size=int(config["vocab_size"]),
-            seq_len=int(config["seq_len"]),
-            hidden_dim=hidden,
-            num_layers=layers,
-            num_heads=int(config["num_heads"]),
-            state_dim=int(config["state_dim"]),
-            layer_types=kinds,
-            dense_dim=int(config.get("dense_intermediate_dim", 0)
-                          or max(int(config.get("intermediate_dim", 0)), 4 * hidden)),
-            latent_dim=int(config.get("mla_latent_dim", 0) or max(128, hidden // 4)),
-            base_context=int(config.get("base_context", 8192)),
-            final_context=int(config.get("final_context", 8192)),
-            rope_base=float(config.get("rope_base", 10000.0)),
-            longrope_scaling=str(config.get("longrope_scaling", "linear")),
-        )
+        hidden = values["hidden_dim"]
+        return cls(layer_types=kinds, dense_dim=_dense_width(config, hidden), latent_dim=_latent_width(config, hidden),
+                   **values)
+
+    def width(self, source: str) -> int:
+        """Input width of a projection by the name of its source: hidden, latent or dense."""
+        return {"hidden": self.hidden_dim, "latent": self.latent_dim, "dense": self.dense_dim}[source]
+
+
+# Reserved-code test per byte value: a byte holds code 3 when both bits of one of its four fields are set.
+_RESERVED_BYTES = torch.tensor([any((value >> shift) & 3 == 3 for shift in (0, 2, 4, 6)) for value in range(256)])
+
+
+def _holds_reserved_code(packed: Tensor) -> bool:
+    """Whether any byte of a packed buffer carries code 3 (one histogram of the byte values)."""
+    if packed.numel() == 0:
+        return False
+    counts = torch.bincount(packed.reshape(-1).to(torch.int64) if packed.device.type != "cpu"
+                            else packed.reshape(-1), minlength=256)
+    return bool(counts.cpu()[_RESERVED_BYTES].any())
 
 
 def _check_entries(state: dict[str, Any]) -> None:
-    """loader.py:94-112, the host part: every entry a tensor, packed buffers uint8, scales float16."""
+    """The reference's per-entry checks (loader.py:94-112), in the state's order: every entry a tensor; packed
+    buffers uint8 with no reserved code; g128 scales float16, finite and positive."""
     for key, value in state.items():
         if not isinstance(value, Tensor):
             raise RuntimeError(f"model_state entry is not a tensor: {key}")
-        if key.endswith(".packed_weight") and value.dtype != torch.uint8:
-            raise RuntimeError(f"packed ternary buffer must be uint8: {key}")
-        if key.endswith(".weight_scales") and value.dtype != torch.float16:
-            raise RuntimeError(f"g128 scale buffer must be float16: {key}")
+        if key.endswith(".packed_weight"):
+            if value.dtype != torch.uint8:
+                raise RuntimeError(f"packed ternary buffer must be uint8: {key}")
+            if _holds_reserved_code(value):
+                raise RuntimeError(f"packed ternary buffer contains the reserved code 3: {key}")
+        elif key.endswith(".weight_scales"):
+            if value.dtype != torch.float16:
+                raise RuntimeError(f"g128 scale buffer must be float16: {key}")
+            if value.numel() and not bool(torch.isfinite(value).all()):
+                raise RuntimeError(f"g128 scale buffer must contain only finite values: {key}")
+            if value.numel() and not bool((value > 0).all()):
+                raise RuntimeError(f"g128 scale buffer must contain only positive values: {key}")
 
 
-class _StateReader:
-    """Hands out state tensors by key and reports what was never asked for (loader.py:115-145)."""
-
-    def __init__(self, state: dict[str, Tensor]) -> None:
-        self.state = state
-        self.used: set[str] = set()
-
-    def take(self, key: str) -> Tensor:
-        if key not in self.state:
-            raise RuntimeError(f"model_state is missing {key}")
-        self.used.add(key)
-        return self.state[key]
-
-    def take_optional(self, key: str) -> Tensor | None:
-        if key not in self.state:
-            return None
-        self.used.add(key)
-        return self.state[key]
-
-    def linear(self, prefix: str, in_features: int) -> TernaryLinear:
-        return TernaryLinear(self.take(f"{prefix}.packed_weight"), self.take(f"{prefix}.weight_scales"), in_features,
-                             bias=self.take_optional(f"{prefix}.bias"))
-
-    def unused(self) -> list[str]:
-        return sorted(set(self.state) - self.used)
-
-
-_MAMBA_TENSORS = ("log_decay", "theta", "skip", "conv_weight", "conv_bias")
+# The ternary projections of a block, by module name and the width of their input, in the order the
+# reference builds its modules (loader.py:156-190); then the mixer's own tensors and the norms.
+_MIXER_PROJECTIONS = {
+    "mamba": (("in_proj", "hidden"), ("bc_dt_proj", "hidden"), ("out_proj", "hidden")),
+    "mla": (("q_proj", "hidden"), ("kv_down_proj", "hidden"), ("k_nope_up_proj", "latent"),
+            ("k_rope_proj", "hidden"), ("v_up_proj", "latent"), ("out_proj", "hidden")),
+}
+_FFN_PROJECTIONS = (("gate_proj", "hidden"), ("up_proj", "hidden"), ("down_proj", "dense"))
+_MIXER_TENSORS = {"mamba": ("log_decay", "theta", "skip", "conv_weight", "conv_bias"), "mla": ()}
 
 # The fused operand groups of a block and their projections, in launch order (kernel_decoder.py:236-262).
-_FFN = (("gate_up", ("gate_proj", "up_proj")), ("down", ("down_proj",)))
+_FFN_GROUPS = (("gate_up", ("gate_proj", "up_proj")), ("down", ("down_proj",)))
 GROUPS = {
-    "mamba": (("entry", ("in_proj", "bc_dt_proj")), ("out", ("out_proj",))) + _FFN,
+    "mamba": (("entry", ("in_proj", "bc_dt_proj")), ("out", ("out_proj",))) + _FFN_GROUPS,
     "mla": (("entry", ("q_proj", "kv_down_proj", "k_rope_proj")), ("up", ("k_nope_up_proj", "v_up_proj")),
-            ("out", ("out_proj",))) + _FFN,
+            ("out", ("out_proj",))) + _FFN_GROUPS,
 }
+
+
+@dataclass(frozen=True)
+class _Entry:
+    """One state key the model reads: a projection's part, a mixer tensor or a norm."""
+
+    key: str
+    required: bool = True
+
+
+def _projection_entries(prefix: str) -> list[_Entry]:
+    return [_Entry(f"{prefix}.packed_weight"), _Entry(f"{prefix}.weight_scales"), _Entry(f"{prefix}.bias", False)]
+
+
+def _block_layout(kind: str, index: int) -> list[tuple[str, str, str]]:
+    """(state prefix, projection name, input source) of every projection of block `index`."""
+    prefix = f"blocks.{index}"
+    return ([(f"{prefix}.mixer.{name}", name, source) for name, source in _MIXER_PROJECTIONS[kind]]
+            + [(f"{prefix}.ffn.{name}", name, source) for name, source in _FFN_PROJECTIONS])
+
+
+def _expected_entries(config: CheckpointConfig) -> list[_Entry]:
+    """Every key the model reads, in the order the reference's builder takes them: the token matrix; per
+    block the mixer's projections and tensors, the feed-forward projections and the two norms; the final
+    norm."""
+    entries = _projection_entries("token_io.projection")
+    for index, kind in enumerate(config.layer_types):
+        prefix = f"blocks.{index}"
+        for name, _ in _MIXER_PROJECTIONS[kind]:
+            entries += _projection_entries(f"{prefix}.mixer.{name}")
+        entries += [_Entry(f"{prefix}.mixer.{name}") for name in _MIXER_TENSORS[kind]]
+        for name, _ in _FFN_PROJECTIONS:
+            entries += _projection_entries(f"{prefix}.ffn.{name}")
+        entries += [_Entry(f"{prefix}.mixer_norm.weight"), _Entry(f"{prefix}.ffn_norm.weight")]
+    entries.append(_Entry("final_norm.weight"))
+    return entries
+
+
+def _check_keys(config: CheckpointConfig, state: dict[str, Tensor]) -> None:
+    """The key set must be exactly the model's: nothing required missing, nothing left over."""
+    expected = _expected_entries(config)
+    for entry in expected:
+        if entry.required and entry.key not in state:
+            raise RuntimeError(f"model_state is missing {entry.key}")
+    known = {entry.key for entry in expected}
+    unused = sorted(key for key in state if key not in known)
+    if unused:
+        raise RuntimeError(f"model_state has entries the model does not use: {', '.join(unused[:5])}")
+
+
+def _linear(state: dict[str, Tensor], prefix: str, in_features: int) -> TernaryLinear:
+    return TernaryLinear(state[f"{prefix}.packed_weight"], state[f"{prefix}.weight_scales"], in_features,
+                         bias=state.get(f"{prefix}.bias"))
 
 
 @dataclass
@@ -186,17 +258,16 @@ class LinearPath:
     def matrices(self, device: torch.device | str, validate: bool = True):
         """(token matrix, per-block dict of Matrix) on `device`, fused as the reference decoder's
         launches are (kernel_decoder.py:230-262); with `validate`, every uploaded operand is checked
-        on the device first."""
+        on the device as well."""
         device = torch.device(device)
         token = Matrix([self.token], device, lanes=HEAD_LANES)
         named = [("token_io.projection", token)]
         groups = []
         for index, block in enumerate(self.blocks):
-            p = block.projections
             layer = {}
             for group, members in GROUPS[block.kind]:
                 interleave = group == "gate_up"
-                layer[group] = Matrix([p[name] for name in members], device, interleave=interleave,
+                layer[group] = Matrix([block.projections[name] for name in members], device, interleave=interleave,
                                       max_lanes=16 if interleave else 32)
                 named.append((f"blocks.{index} {group} ({', '.join(members)})", layer[group]))
             groups.append(layer)
@@ -206,69 +277,64 @@ class LinearPath:
 
 
 def build_linear_path(config: CheckpointConfig, state: dict[str, Any]) -> LinearPath:
-    """loader.py:148-219 for the ternary linear path: the same keys, shapes and unused-entry check."""
+    """The ternary linear path of a packed state dict (loader.py:146-203 for these modules): the
+    entry checks, the exact key set, then every projection with its shape checks."""
     _check_entries(state)
-    reader = _StateReader(state)
-    hidden = config.hidden_dim
-    token = reader.linear("token_io.projection", hidden)
+    _check_keys(config, state)
+    token = _linear(state, "token_io.projection", config.hidden_dim)
     if token.out_features != config.vocab_size:
         raise RuntimeError(f"token weight has {token.out_features} rows, config says {config.vocab_size}")
     blocks = []
     for index, kind in enumerate(config.layer_types):
-        prefix = f"blocks.{index}"
-        projections: dict[str, TernaryLinear] = {}
-        mixer_tensors: dict[str, Tensor] = {}
-        if kind == "mamba":
-            projections["in_proj"] = reader.linear(f"{prefix}.mixer.in_proj", hidden)
-            projections["bc_dt_proj"] = reader.linear(f"{prefix}.mixer.bc_dt_proj", hidden)
-            projections["out_proj"] = reader.linear(f"{prefix}.mixer.out_proj", hidden)
-            for name in _MAMBA_TENSORS:
-                mixer_tensors[name] = reader.take(f"{prefix}.mixer.{name}")
-        else:
-            projections["q_proj"] = reader.linear(f"{prefix}.mixer.q_proj", hidden)
-            projections["kv_down_proj"] = reader.linear(f"{prefix}.mixer.kv_down_proj", hidden)
-            projections["k_nope_up_proj"] = reader.linear(f"{prefix}.mixer.k_nope_up_proj", config.latent_dim)
-            projections["k_rope_proj"] = reader.linear(f"{prefix}.mixer.k_rope_proj", hidden)
-            projections["v_up_proj"] = reader.linear(f"{prefix}.mixer.v_up_proj", config.latent_dim)
-            projections["out_proj"] = reader.linear(f"{prefix}.mixer.out_proj", hidden)
-        projections["gate_proj"] = reader.linear(f"{prefix}.ffn.gate_proj", hidden)
-        projections["up_proj"] = reader.linear(f"{prefix}.ffn.up_proj", hidden)
-        projections["down_proj"] = reader.linear(f"{prefix}.ffn.down_proj", config.dense_dim)
-        blocks.append(BlockLinears(kind, projections, reader.take(f"{prefix}.mixer_norm.weight"),
-                                   reader.take(f"{prefix}.ffn_norm.weight"), mixer_tensors))
-    final_norm = reader.take("final_norm.weight")
-    unused = reader.unused()
-    if unused:
-        raise RuntimeError(f"model_state has entries the model does not use: {', '.join(unused[:5])}")
-    return LinearPath(config, token, blocks, final_norm)
+        projections = {name: _linear(state, prefix, config.width(source))
+                       for prefix, name, source in _block_layout(kind, index)}
+        mixer = {name: state[f"blocks.{index}.mixer.{name}"] for name in _MIXER_TENSORS[kind]}
+        blocks.append(BlockLinears(kind, projections, state[f"blocks.{index}.mixer_norm.weight"],
+                                   state[f"blocks.{index}.ffn_norm.weight"], mixer))
+    return LinearPath(config, token, blocks, state["final_norm.weight"])
 
 
-def load_checkpoint(path: str | Path, expected_tokenizer_sha256: str | None = None) -> LinearPath:
-    """loader.py:222-258 up to the model build: the payload checks, then ``build_linear_path``."""
-    model_file = Path(path)
+def _read_payload(model_file: Path) -> dict[str, Any]:
+    """The checkpoint dict, loaded without executing anything from the file, with its format checked."""
     payload = torch.load(model_file, map_location="cpu", weights_only=True)
     if not isinstance(payload, dict):
         raise RuntimeError(f"invalid Ivonar checkpoint: {model_file}")
-    if payload.get("format") != PACKED_FORMAT or payload.get("schema_version") != PACKED_SCHEMA_VERSION:
+    if (payload.get("format"), payload.get("schema_version")) != (PACKED_FORMAT, PACKED_SCHEMA_VERSION):
         raise RuntimeError(f"unsupported checkpoint format; expected {PACKED_FORMAT} schema {PACKED_SCHEMA_VERSION}")
+    return payload
+
+
+def _check_tokenizer(found: str | None, expected: str | None) -> None:
+    if expected is None:
+        return
+    if found is None:
+        raise RuntimeError("checkpoint is missing tokenizer_sha256")
+    if found != str(expected):
+        raise RuntimeError(f"tokenizer SHA-256 mismatch: expected {expected}, found {found}")
+
+
+def _optional_text(payload: dict[str, Any], key: str) -> str | None:
+    value = payload.get(key)
+    return None if value is None else str(value)
+
+
+def load_checkpoint(path: str | Path, expected_tokenizer_sha256: str | None = None) -> LinearPath:
+    """Read a packed checkpoint (the checks of loader.py:222-242 with the reference's messages) and
+    return its ternary linear path with the payload's metadata."""
+    model_file = Path(path)
+    payload = _read_payload(model_file)
     config = CheckpointConfig.from_payload(payload.get("config"))
-    tokenizer_sha256 = str(payload["tokenizer_sha256"]) if payload.get("tokenizer_sha256") else None
-    if expected_tokenizer_sha256 is not None:
-        if tokenizer_sha256 is None:
-            raise RuntimeError("checkpoint is missing tokenizer_sha256")
-        if tokenizer_sha256 != str(expected_tokenizer_sha256):
-            raise RuntimeError(
-                f"tokenizer SHA-256 mismatch: expected {expected_tokenizer_sha256}, found {tokenizer_sha256}")
+    tokenizer = str(payload["tokenizer_sha256"]) if payload.get("tokenizer_sha256") else None
+    _check_tokenizer(tokenizer, expected_tokenizer_sha256)
     state = payload.get("model_state")
     if not isinstance(state, dict):
         raise RuntimeError("checkpoint model_state is invalid")
     linear_path = build_linear_path(config, state)
     linear_path.path = model_file
-    linear_path.lineup = str(payload["lineup"]) if payload.get("lineup") is not None else None
-    linear_path.stage = str(payload["stage"]) if payload.get("stage") is not None else None
-    linear_path.phase = str(payload["phase"]) if payload.get("phase") is not None else None
+    linear_path.lineup, linear_path.stage, linear_path.phase = (
+        _optional_text(payload, key) for key in ("lineup", "stage", "phase"))
     linear_path.step = int(payload.get("step", 0) or 0)
-    linear_path.tokenizer_sha256 = tokenizer_sha256
+    linear_path.tokenizer_sha256 = tokenizer
     return linear_path
 
 

@@ -14,8 +14,6 @@ It has no CPU path; calling it on a non-ROCm tensor raises ``KernelError``.
 
 from __future__ import annotations
 
-import math
-
 import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
@@ -42,22 +40,27 @@ def pack_ternary_codes(values: Tensor) -> Tensor:
 
 
 def dequantize_ternary_codes(codes: Tensor, scales: Tensor, group_size: int, dtype: torch.dtype) -> Tensor:
-    """values * per-group scale, as ``dtype`` (quantization.py:21-32)."""
-    in_features = int(codes.shape[-1])
-    groups = math.ceil(in_features / group_size)
-    pad = groups * group_size - in_features
-    values = codes.float()
-    if pad:
-        values = F.pad(values, (0, pad))
-    values = values.reshape(*codes.shape[:-1], groups, group_size) * scales.float().unsqueeze(-1)
-    values = values.reshape(*codes.shape[:-1], -1)
-    if pad:
-        values = values[..., :in_features]
-    return values.to(dtype)
+    """values * per-group scale, as ``dtype`` (semantics of quantization.py:21-32).
+
+    Each input's scale is its group's, repeated ``group_size`` times along the
+    row and cut to the row's width; the product is formed in fp32."""
+    width = int(codes.shape[-1])
+    per_input = scales.float().repeat_interleave(int(group_size), dim=-1)[..., :width]
+    return (codes.float() * per_input).to(dtype)
+
+
+def _require_shape(what: str, tensor: Tensor, expected: tuple[int, ...]) -> None:
+    if tuple(tensor.shape) != expected:
+        raise ValueError(f"invalid {what} shape: expected {expected}, got {tuple(tensor.shape)}")
 
 
 class TernaryLinear(nn.Module):
-    """Packed ternary linear layer with the reference's constructor contract (quantization.py:119-147)."""
+    """Packed ternary linear layer with the reference's constructor contract (quantization.py:119-147).
+
+    ``packed_weight`` uint8 [out_features, ceil(in_features/4)], ``weight_scales``
+    [out_features, ceil(in_features/group_size)], ``bias`` [out_features] or
+    None; the shapes are checked with the reference's messages and the
+    tensors kept as buffers (bias in fp32)."""
 
     def __init__(
         self,
@@ -69,23 +72,23 @@ class TernaryLinear(nn.Module):
         group_size: int = TERNARY_GROUP_SIZE,
     ) -> None:
         super().__init__()
-        if packed_weight.ndim != 2 or packed_weight.dtype != torch.uint8:
+        if packed_weight.dtype != torch.uint8 or packed_weight.dim() != 2:
             raise ValueError("packed_weight must be a two-dimensional uint8 tensor")
-        self.in_features = int(in_features)
-        self.out_features = int(packed_weight.shape[0])
-        self.group_size = int(group_size)
-        self.eps = float(eps)
-        expected_packed = (self.out_features, math.ceil(self.in_features / 4))
-        expected_scales = (self.out_features, math.ceil(self.in_features / self.group_size))
-        if tuple(packed_weight.shape) != expected_packed:
-            raise ValueError(f"invalid packed shape: expected {expected_packed}, got {tuple(packed_weight.shape)}")
-        if tuple(weight_scales.shape) != expected_scales:
-            raise ValueError(f"invalid scale shape: expected {expected_scales}, got {tuple(weight_scales.shape)}")
-        if bias is not None and tuple(bias.shape) != (self.out_features,):
-            raise ValueError(f"invalid bias shape: expected ({self.out_features},), got {tuple(bias.shape)}")
-        self.register_buffer("packed_weight", packed_weight.contiguous())
-        self.register_buffer("weight_scales", weight_scales.contiguous())
-        self.register_buffer("bias", None if bias is None else bias.detach().clone().float())
+        rows = int(packed_weight.shape[0])
+        width, groups = int(in_features), -(-int(in_features) // int(group_size))
+        _require_shape("packed", packed_weight, (rows, -(-width // 4)))
+        _require_shape("scale", weight_scales, (rows, groups))
+        if bias is not None:
+            _require_shape("bias", bias, (rows,))
+        self.in_features, self.out_features = width, rows
+        self.group_size, self.eps = int(group_size), float(eps)
+        buffers = {
+            "packed_weight": packed_weight.contiguous(),
+            "weight_scales": weight_scales.contiguous(),
+            "bias": None if bias is None else bias.detach().float().clone(),
+        }
+        for name, tensor in buffers.items():
+            self.register_buffer(name, tensor)
         self._matrix = None
 
     def unpacked_weight(self, dtype: torch.dtype = torch.float32) -> Tensor:

@@ -135,3 +135,36 @@ def test_device_groups_need_a_rocm_device():
     linear = _build(_state())
     with pytest.raises(KernelError):
         linear.matrices("cpu")
+
+
+@pytest.mark.parametrize("where", [0, "middle", -1])
+def test_reserved_code_and_bad_scales_are_refused_at_load(where):
+    """loader.py:94-112 runs at load time: a byte carrying code 3 anywhere, an infinite, NaN, zero or
+    negative scale is refused with the reference's message."""
+    key = "blocks.1.ffn.down_proj"
+    for field, value, message in [
+        ("packed_weight", 0b11_01_01_01, "contains the reserved code 3"),
+        ("packed_weight", 0b01_11_01_01, "contains the reserved code 3"),
+        ("packed_weight", 0b11_10_10_10, "contains the reserved code 3"),
+        ("weight_scales", float("inf"), "must contain only finite values"),
+        ("weight_scales", float("nan"), "must contain only finite values"),
+        ("weight_scales", 0.0, "must contain only positive values"),
+        ("weight_scales", -0.01, "must contain only positive values"),
+    ]:
+        state = _state()
+        tensor = state[f"{key}.{field}"].clone()
+        flat = tensor.view(-1)
+        index = flat.numel() // 2 if where == "middle" else where
+        flat[index] = value
+        state[f"{key}.{field}"] = tensor
+        with pytest.raises(RuntimeError, match=f"{message}: {key}.{field}"):
+            _build(state)
+
+
+def test_reserved_byte_table_matches_the_field_decoding():
+    from ivonar_amd.quantization import unpack_ternary_codes
+
+    every_byte = torch.arange(256, dtype=torch.uint8).reshape(256, 1)
+    fields = unpack_ternary_codes(every_byte, 4) + 1  # codes 0..3 of each byte's four inputs
+    assert torch.equal(C._RESERVED_BYTES, (fields == 3).any(dim=1))
+    assert int(C._RESERVED_BYTES.sum()) == 256 - 81  # 3**4 bytes use codes 0..2 only

@@ -93,6 +93,8 @@ def test_loaded_groups_match_the_oracle(cuda, oracle, tmp_path):
 
 
 def test_reserved_code_in_a_checkpoint_is_refused(cuda, tmp_path):
+    """The loader refuses a corrupt checkpoint on the host (loader.py:94-112); operands corrupted after
+    loading are refused by the device check when they are uploaded."""
     import torch
 
     from ivonar_amd import checkpoint as C
@@ -104,14 +106,15 @@ def test_reserved_code_in_a_checkpoint_is_refused(cuda, tmp_path):
     state[key] = state[key].clone()
     state[key][3, 5] |= 0xC0
     synthetic.write_checkpoint(tmp_path / "bad.pt", config=config, state=state)
-    linear = C.load_checkpoint(tmp_path / "bad.pt")
+    with pytest.raises(RuntimeError, match=f"reserved code 3: {key}"):
+        C.load_checkpoint(tmp_path / "bad.pt")
+    synthetic.write_checkpoint(tmp_path / "good.pt", config=config, state=synthetic.checkpoint_state(config, seed=2))
+    linear = C.load_checkpoint(tmp_path / "good.pt")
+    linear.blocks[1].projections["kv_down_proj"].packed_weight[3, 5] |= 0xC0
     with pytest.raises(RuntimeError, match=r"reserved code 3: blocks.1 entry \(q_proj, kv_down_proj, k_rope_proj\)"):
         linear.matrices(cuda)
-    state = synthetic.checkpoint_state(config, seed=2)
-    key = "blocks.0.ffn.down_proj.weight_scales"
-    state[key] = state[key].clone()
-    state[key][0, 0] = float("inf")
-    synthetic.write_checkpoint(tmp_path / "bad2.pt", config=config, state=state)
+    linear = C.load_checkpoint(tmp_path / "good.pt")
+    linear.blocks[0].projections["down_proj"].weight_scales[0, 0] = float("inf")
     with pytest.raises(RuntimeError, match="only finite values: blocks.0 down"):
-        C.load_checkpoint(tmp_path / "bad2.pt").matrices(cuda)
+        linear.matrices(cuda)
     assert torch.cuda.is_available()
