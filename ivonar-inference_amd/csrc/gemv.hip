@@ -193,7 +193,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   // Loads are never predicated (rows past the matrix are clamped inside
   // load_step), so the wait counts before each use stay exact.
   Step<NJ> a, b;
-  int it = first;
+  int it = __builtin_amdgcn_readfirstlane(first);  // wave-uniform: the per-item branches are scalar
   load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
                                                           it * rows_per_iter + slot * kRows, 0, sub, chunks);
 
@@ -281,50 +281,36 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   // With q8 in registers an item is a whole row (NJ == steps, the host's
   // layouts): jb stays 0, and saying so lets the step offsets fold into the
   // loads' immediate offsets.
+  // The wave's last item prefetches nothing (no loads go out for rows past the end).
   const int blocks_per_row = QREG ? 1 : (steps + NJ - 1) / NJ;
   int jb = 0;
   float acc = 0.0f;
-  while (it < sh.iters) {
-    {
-      int it_next = it, jb_next = jb + 1;
-      if (jb_next == blocks_per_row) {
-        jb_next = 0;
-        it_next = it + waves;
-      }
-      const int row0 = it * rows_per_iter + slot * kRows;
-      const int j_next = QREG ? 0 : jb_next * NJ;
-      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(b, packed, scales, output, sh,
-                                                                     it_next * rows_per_iter + slot * kRows, j_next,
-                                                                     sub, chunks);
-      compute_step<EPI, NJ, QREG, LANES, EXACT>(a, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
-                                                QREG ? 0 : jb * NJ, sub, chunks);
-      if (jb == blocks_per_row - 1) {
-        finish(acc, row0, a.base);
-        acc = 0.0f;
-      }
-      it = it_next;
-      jb = jb_next;
+  auto item = [&](Step<NJ>& current, Step<NJ>& next) -> bool {
+    int it_next = it, jb_next = jb + 1;
+    if (jb_next == blocks_per_row) {
+      jb_next = 0;
+      it_next = it + waves;
     }
-    if (it >= sh.iters) break;
-    {
-      int it_next = it, jb_next = jb + 1;
-      if (jb_next == blocks_per_row) {
-        jb_next = 0;
-        it_next = it + waves;
-      }
-      const int row0 = it * rows_per_iter + slot * kRows;
+    const int row0 = it * rows_per_iter + slot * kRows;
+    const bool more = it_next < sh.iters;
+    if (more) {
       const int j_next = QREG ? 0 : jb_next * NJ;
-      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
+      load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(next, packed, scales, output, sh,
                                                                      it_next * rows_per_iter + slot * kRows, j_next,
                                                                      sub, chunks);
-      compute_step<EPI, NJ, QREG, LANES, EXACT>(b, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
-                                                QREG ? 0 : jb * NJ, sub, chunks);
-      if (jb == blocks_per_row - 1) {
-        finish(acc, row0, b.base);
-        acc = 0.0f;
-      }
-      it = it_next;
-      jb = jb_next;
+    }
+    compute_step<EPI, NJ, QREG, LANES, EXACT>(current, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
+                                              QREG ? 0 : jb * NJ, sub, chunks);
+    if (jb == blocks_per_row - 1) {
+      finish(acc, row0, current.base);
+      acc = 0.0f;
+    }
+    it = it_next;
+    jb = jb_next;
+    return more;
+  };
+  if (it < sh.iters) {
+    while (item(a, b) && item(b, a)) {
     }
   }
 }
@@ -397,7 +383,9 @@ struct RowStep {
 // loaded at the top of its own iteration, after its steps' weights, and
 // consumed at its end: vmcnt(3*(STEPS-1) + 2) before every step (younger:
 // the pair's later steps, its two side loads, the refills issued so far),
-// vmcnt(3*STEPS) before the epilogue (younger: the STEPS refills).  No value
+// vmcnt(3*STEPS) before the epilogue (younger: the STEPS refills).  A
+// wave's last row pair issues no refills (its waits count only the pair's
+// later steps and side loads), so no loads go out for rows past the end.  No value
 // an asm load writes is carried across the loop's back edge except the
 // step registers, which are rewritten in place (the compiler has no copy to
 // make of them); a value carried across the edge can be copied by the
@@ -485,7 +473,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   int xv = load_b32(in.xsum_in + min(tid, chunks - 1));
 
   RowStep st[STEPS];
-  int it = blockIdx.x * (kBlock / 64) + (tid >> 6);
+  int it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));  // wave-uniform
   PairBase pb = pair_base(it);
   static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
 
@@ -504,30 +492,15 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
 
   const int4 qr_unused[1][4] = {};
   const int xr_unused[1] = {0};
-  while (it < sh.iters) {
-    const int row0 = it * kRows;
-    const int it_next = it + waves;
-    // This row pair's bias and residual base, younger than its steps' weights.
-    int b_side, base_side;
-    issue_side(it, b_side, base_side);
-    pb = pair_base(it_next);
-    float acc = 0.0f;
-    static_for<STEPS>([&](auto s) {
-      asm volatile("s_waitcnt vmcnt(%3)"
-                   : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
-                   : "n"(3 * (STEPS - 1) + kSide)
-                   : "memory");
-      Step<1> view;
-      view.w[0][0] = __builtin_bit_cast(uint4, st[s].w0);
-      view.w[0][1] = __builtin_bit_cast(uint4, st[s].w1);
-      view.s[0] = (uint16_t)st[s].s;
-      compute_step<EPI, 1, false, 64, EXACT, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0, s,
-                                             sub, chunks);
-      issue_step(st[s], pb, it_next, s);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    // Younger than the side loads: the STEPS refills of the next row pair.
-    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b_side), "+v"(base_side) : "n"(3 * STEPS) : "memory");
+  auto compute = [&](const RowStep& step, float& acc, int row0, auto step_c) {
+    Step<1> view;
+    view.w[0][0] = __builtin_bit_cast(uint4, step.w0);
+    view.w[0][1] = __builtin_bit_cast(uint4, step.w1);
+    view.s[0] = (uint16_t)step.s;
+    compute_step<EPI, 1, false, 64, EXACT, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0,
+                                                 decltype(step_c)::value, sub, chunks);
+  };
+  auto epilogue = [&](float acc, int row0, int b_side, int base_side) {
     if constexpr (EPI != kPartials) {
       acc = pair_tree_sum(acc, 64);
       const int row = row0 + (sub & 1);
@@ -541,9 +514,48 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
         else output[row] = __int_as_float(base_side) + y;
       }
     }
-    it = it_next;
+  };
+  if (it < sh.iters) {
+    // Steady state: each computed step is refilled with the same step of the wave's next row pair.
+    while (it + waves < sh.iters) {
+      const int row0 = it * kRows;
+      const int it_next = it + waves;
+      // This row pair's bias and residual base, younger than its steps' weights.
+      int b_side, base_side;
+      issue_side(it, b_side, base_side);
+      pb = pair_base(it_next);
+      float acc = 0.0f;
+      static_for<STEPS>([&](auto s) {
+        asm volatile("s_waitcnt vmcnt(%3)"
+                     : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
+                     : "n"(3 * (STEPS - 1) + kSide)
+                     : "memory");
+        compute(st[s], acc, row0, s);
+        issue_step(st[s], pb, it_next, s);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // Younger than the side loads: the STEPS refills of the next row pair.
+      asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b_side), "+v"(base_side) : "n"(3 * STEPS) : "memory");
+      epilogue(acc, row0, b_side, base_side);
+      it = it_next;
+    }
+    // The wave's last row pair: no refills, so fewer loads are younger than each step.
+    const int row0 = it * kRows;
+    int b_side, base_side;
+    issue_side(it, b_side, base_side);
+    float acc = 0.0f;
+    static_for<STEPS>([&](auto s) {
+      asm volatile("s_waitcnt vmcnt(%3)"
+                   : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
+                   : "n"(3 * (STEPS - 1 - decltype(s)::value) + kSide)
+                   : "memory");
+      compute(st[s], acc, row0, s);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(b_side), "+v"(base_side)::"memory");
+    epilogue(acc, row0, b_side, base_side);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the refills of the pass past the end
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // a wave with no row pair still has its first loads out
 }
 
 int device_cus() {
