@@ -97,6 +97,19 @@ hipError_t gemv_norm_store_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
 hipError_t gemv_norm_silu_pair_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
 hipError_t gemv_attn_residual_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
 
+/* No reference counterpart; for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  gemv_plain_store with the same arguments and results, except
+ * that a row longer than 4096 inputs is quantized into a fixed 35,072-byte
+ * array of the library's device code (one per device, set up on the first
+ * call on each device) instead of the scratch gemv_plain_store allocates:
+ * nothing is allocated or freed, by this call or the library.  n above
+ * 32768 returns hipErrorInvalidValue.  Every call on a device shares that
+ * array, so calls that overlap on one device race (their outputs are
+ * undefined); calls in one stream order are safe.  Nothing in the array
+ * needs to start at zero: each call writes all of it that it reads. */
+hipError_t ivonar_gemv_plain_store_noalloc(hipStream_t stream, IVONAR_GEMV_ARGS);
+
 /* Test export (no reference counterpart; requested by the decode-path parity
  * checks): the exact int32 partials P[r, g] of the GEMV's integer core, from
  * pre-quantized activations, into partials int32 [rows, groups]. */

@@ -58,7 +58,7 @@ hipError_t check_matrix(const uint8_t* packed, const uint16_t* scales, int rows,
 hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, const float* input, const float* aux,
                       const int8_t* q8_in, const int32_t* xsum_in, const float* scale_in, const uint8_t* packed,
                       const uint16_t* scales, const float* bias, float* output, int rows, int n, int row_bytes,
-                      int groups, int splits, float eps) {
+                      int groups, int splits, float eps, Scratch* work = nullptr) {
   hipError_t status = check_matrix(packed, scales, rows, n, row_bytes, groups);
   if (status != hipSuccess) return status;
   if (output == nullptr) return hipErrorInvalidValue;
@@ -84,6 +84,7 @@ hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, cons
   a.bias = bias;
   a.output = output;
   a.partials = nullptr;
+  a.work = work;
   a.rows = rows;
   a.n = n;
   a.row_bytes = row_bytes;
@@ -92,6 +93,40 @@ hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, cons
   a.eps = eps;
   a.head_dim = defines().head_dim;
   return launch_gemv(stream, a);
+}
+
+// ------------------------------------------------ no-allocation GEMV scratch
+// Rows longer than the fused limit are quantized before the GEMV; the
+// no-allocation entry point quantizes them into this array (q8, chunk sums,
+// token scale) instead of the scratch the library allocates.  Each device
+// holds its own copy at its own address, looked up once per device with
+// hipGetSymbolAddress; host code uses only that address.
+constexpr int kStaticChunks = 512;  // rows up to 32768 inputs
+constexpr size_t kStaticQ8Bytes = (size_t)kStaticChunks * kChunk;
+constexpr size_t kStaticBytes = kStaticQ8Bytes + (size_t)kStaticChunks * sizeof(int32_t) + 256;
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+std::mutex g_static_lock;
+Scratch g_static[kMaxDevices];
+
+hipError_t static_scratch(Scratch** out) {
+  int device = 0;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) return status;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> guard(g_static_lock);
+  Scratch& s = g_static[device];
+  if (s.q8 == nullptr) {
+    void* base = nullptr;
+    status = hipGetSymbolAddress(&base, HIP_SYMBOL(scratch));
+    if (status != hipSuccess) return status;
+    unsigned char* bytes = static_cast<unsigned char*>(base);
+    s.xsum = reinterpret_cast<int32_t*>(bytes + kStaticQ8Bytes);
+    s.scale = reinterpret_cast<float*>(bytes + kStaticQ8Bytes + (size_t)kStaticChunks * sizeof(int32_t));
+    s.capacity_chunks = kStaticChunks;
+    s.q8 = reinterpret_cast<int8_t*>(bytes);
+  }
+  *out = &s;
+  return hipSuccess;
 }
 
 hipError_t quant_entry(hipStream_t stream, int mode, const float* input, int in_stride, const float* aux, int n,
@@ -195,6 +230,17 @@ int ivonar_gemm_plan(int m, int rows, int n) { return gemm_splits(m, rows, n); }
 hipError_t gemv_plain_store(hipStream_t stream, IVONAR_GEMV_ARGS) {
   GEMV_UNUSED;
   return GEMV_PASS_ENTRY(kPlain, kStore, false);
+}
+hipError_t ivonar_gemv_plain_store_noalloc(hipStream_t stream, IVONAR_GEMV_ARGS) {
+  GEMV_UNUSED;
+  if (n > kStaticChunks * kChunk) return hipErrorInvalidValue;  // beyond the static scratch
+  Scratch* work = nullptr;
+  if (n > gemv_fused_limit()) {
+    hipError_t status = static_scratch(&work);
+    if (status != hipSuccess) return status;
+  }
+  return gemv_entry(stream, kPlain, kStore, false, input, aux, q8_in, xsum_in, scale_in, packed, scales, bias, output,
+                    rows, n, row_bytes, groups, splits, eps, work);
 }
 hipError_t gemv_plain_residual(hipStream_t stream, IVONAR_GEMV_ARGS) {
   GEMV_UNUSED;

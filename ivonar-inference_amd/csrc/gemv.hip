@@ -713,10 +713,13 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
     }
   }
   if (a.q8_in == nullptr) {
-    Scratch* scratch = nullptr;
-    hipError_t status = scratch_for_stream(stream, &scratch);
-    if (status != hipSuccess) return status;
+    Scratch* scratch = a.work;
+    if (scratch == nullptr) {
+      hipError_t status = scratch_for_stream(stream, &scratch);
+      if (status != hipSuccess) return status;
+    }
     if (chunks > scratch->capacity_chunks) return hipErrorInvalidValue;
+    hipError_t status;
     QuantArgs q{a.mode, a.input, a.n, a.aux, a.n, a.eps, a.splits, a.head_dim, 1, scratch->q8, scratch->xsum,
                 scratch->scale};
     status = launch_quantize(stream, q);

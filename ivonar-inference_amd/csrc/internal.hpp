@@ -60,6 +60,10 @@ struct GemvArgs {
   const float* bias;
   float* output;
   int32_t* partials;  // kPartials only: int32 [rows, groups]
+  // Where a row longer than the fused limit is quantized to when q8_in is
+  // null: this buffer if set (capacity work_chunks chunks), else the device
+  // scratch allocated by the library.
+  Scratch* work;
   int rows;
   int n;
   int row_bytes;

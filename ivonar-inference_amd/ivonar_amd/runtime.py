@@ -50,7 +50,7 @@ SIGNATURES: dict[str, list] = {
     **{name: _GEMV for name in (
         "gemv_plain_store", "gemv_plain_residual", "gemv_norm_store", "gemv_norm_silu_pair", "gemv_attn_residual",
         "gemv_prequant_store", "gemv_plain_store_wide", "gemv_plain_residual_wide", "gemv_norm_store_wide",
-        "gemv_norm_silu_pair_wide", "gemv_attn_residual_wide",
+        "gemv_norm_silu_pair_wide", "gemv_attn_residual_wide", "ivonar_gemv_plain_store_noalloc",
     )},
     "quantize_norm": _QUANT,
     "quantize_norm_wide": _QUANT,
