@@ -5,12 +5,15 @@ K=28672 -> N=8192, fp16 scales |N(0,0.01)|, x ~ N(0,1)), each matrix in 8
 rotating device copies (about 500 MB, more than the 256 MB Infinity Cache),
 so every call streams its weights from HBM.  One step is one cold GEMV of
 each shape through the reference-named entry point ``gemv_plain_store``
-(quantize + GEMV); the step sequence is recorded once into a HIP graph and
-replayed.  ``value`` is algorithmic bytes / second over the timed steps:
+(quantize + GEMV).  W warmup steps run untimed; then exactly K steps are
+recorded into one HIP graph, which is replayed 20 times with events on the
+launch stream around each replay: ``ms_per_step`` is the median replay / K.
+``value`` is algorithmic bytes / second over the timed steps:
 bytes(M,N,K) = N*ceil(K/4) + 2*N*ceil(K/128) + 4*M*K + 4*M*N.
 
 Also reported on the same line: the GEMV kernel alone (pre-quantized
-activations, HIP events on the launch stream) as the roofline figure, the
+activations, each launch bracketed by HIP events on the launch stream) as
+the roofline figure, the
 single-linear case (K=1024 -> N=4096), the 32-token prefill tile GEMM TOPS,
 and the CPU baseline (the reference's numba GEMV restated in C++/OpenMP)
 on a bounded sample of the same workload.
@@ -33,6 +36,7 @@ sys.path.insert(0, str(ROOT / "ivonar-inference_amd"))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 ROTATING_COPIES = 8
+HEADLINE_REPLAYS = 20
 PROBE_GEMM_SHAPES = [(1024, 4096), (4096, 1024), (4096, 14336)]  # (K, N) of the GEMM probe, in order
 PROBE_GEMM_M = (2048, 32)
 
@@ -293,6 +297,49 @@ def measure_traffic(calls: int = 8) -> dict:
             "per_launch": [round(v) for v in per_launch]}
 
 
+def measure_trace(calls: int = 32) -> dict:
+    """Dispatch durations of the GEMV kernels alone: one `rocprofv3 --kernel-trace --stats` pass over the GEMV
+    probe (pre-quantized input, `calls` launches per stress shape cycling the 8 copies), as a child process;
+    the average duration per kernel and the bandwidth it implies for one stress GEMV."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    tool = shutil.which("rocprofv3")
+    if tool is None:
+        return {"error": "rocprofv3 not found"}
+    out = tempfile.mkdtemp(prefix="ivonar_trace_", dir="/tmp")
+    command = [tool, "--kernel-trace", "--stats", "--output-format", "csv", "-d", out, "-o", "trace", "--",
+               sys.executable, str(ROOT / "bench.py"), "--probe", "gemv-stress", "--probe-calls", str(calls)]
+    print("bench: kernel-trace pass over gemv-stress", file=sys.stderr, flush=True)
+    try:
+        subprocess.run(command, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, timeout=240,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    except subprocess.TimeoutExpired:
+        shutil.rmtree(out, ignore_errors=True)
+        return {"error": "kernel-trace pass timed out"}
+    files = sorted(Path(out).rglob("*kernel_stats.csv"))
+    if not files:
+        shutil.rmtree(out, ignore_errors=True)
+        return {"error": "kernel-trace pass wrote no kernel_stats.csv"}
+    kernels = {}
+    with open(files[0]) as handle:
+        reader = csv.DictReader(handle)
+        if not {"Name", "Calls", "AverageNs"} <= set(reader.fieldnames or []):
+            shutil.rmtree(out, ignore_errors=True)
+            return {"error": f"unexpected kernel_stats.csv columns {reader.fieldnames}"}
+        for row in reader:
+            if "gemv" in row["Name"]:
+                name = row["Name"].replace("void ivo::(anonymous namespace)::", "").split("(")[0]
+                kernels[name] = {"calls": int(row["Calls"]), "average_us": round(float(row["AverageNs"]) / 1e3, 3)}
+    shutil.rmtree(out, ignore_errors=True)
+    per_launch = 62537728
+    return {"kernels": kernels,
+            "GBps_from_average": {k: round(per_launch / (v["average_us"] * 1e3), 1) for k, v in kernels.items()},
+            "note": "dispatch durations from the trace exclude the gap between back-to-back launches"}
+
+
 def measure_mfma(calls: int = 16, cus: int = 256, xcds: int = 8) -> dict:
     """MFMA-busy share of the token GEMM from one counter pass over the GEMM probe, per case: rocprofv3's
     derived MfmaUtil (SQ_VALU_MFMA_BUSY_CYCLES summed over SIMDs / (GRBM_GUI_ACTIVE max over XCDs x SIMDs)),
@@ -376,6 +423,7 @@ def main() -> None:
     from ivonar_amd import ops, runtime, synthetic
 
     traffic = None if args.no_traffic else measure_traffic()
+    trace = None if args.no_traffic else measure_trace()
     mfma = None if args.no_traffic else measure_mfma()
     device = torch.device("cuda", 0)
     runtime.initialise(0)
@@ -391,26 +439,33 @@ def main() -> None:
         outputs.append(torch.empty(layer.rows, dtype=torch.float32, device=device))
         bytes_per_step += gemv_bytes(1, layer.rows, layer.in_features)
 
-    def stress_steps(count: int):
+    def stress_steps(count: int, first: int = 0):
         def run():
-            for step in range(count):
+            for step in range(first, first + count):
                 copy = step % ROTATING_COPIES
                 for shape in range(len(stress)):
                     ops.gemv(matrices[shape][copy], inputs[shape], out=outputs[shape])
         return run
 
-    per_graph = ROTATING_COPIES
-    graph = graph_of(stress_steps(per_graph), stream)
-    replays = max(1, args.steps // per_graph)
-    seconds = time_graph(graph, replays, max(1, args.warmup // per_graph))
-    steps = replays * per_graph
-    step_seconds = seconds / per_graph
+    # W untimed warmup steps, then HEADLINE_REPLAYS replays of one HIP graph of exactly K steps, each
+    # replay bracketed by events on the launch stream; the median replay is the timed K steps.
+    steps = args.steps
+    with torch.cuda.stream(stream):
+        stress_steps(args.warmup)()
+    torch.cuda.synchronize()
+    graph = graph_of(stress_steps(steps), stream)
+    seconds = time_graph(graph, HEADLINE_REPLAYS, 1, median=True)
+    step_seconds = seconds / steps
     value = bytes_per_step / step_seconds / 1e9
 
     # ---- dominant kernel alone: GEMV on pre-quantized activations ----------------------------
+    # Per call inside a HIP graph of 8 back-to-back calls (one per rotating copy), events on the launch
+    # stream around each replay; the inter-launch gap a decode sequence also pays is included.  The
+    # kernel-trace pass below gives the dispatch durations alone.
     kernel = {}
     for shape, (layer, x) in enumerate(stress):
         q8, xsum, sx = ops.quantize_rows(inputs[shape].reshape(1, -1))
+        b = gemv_bytes(1, layer.rows, layer.in_features)
 
         def prequant(shape=shape, q8=q8, xsum=xsum, sx=sx):
             for copy in range(ROTATING_COPIES):
@@ -418,7 +473,6 @@ def main() -> None:
 
         g = graph_of(prequant, stream)
         t = time_graph(g, max(20, args.steps // ROTATING_COPIES), 2, median=True) / ROTATING_COPIES
-        b = gemv_bytes(1, layer.rows, layer.in_features)
         kernel[f"{layer.in_features}x{layer.rows}"] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
     # the same shapes through the K-split MFMA kernel (gemm_tile_store with one token)
     skinny = {}
@@ -495,6 +549,7 @@ def main() -> None:
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
+        "replays": HEADLINE_REPLAYS,
         "ms_per_step": round(step_seconds * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -520,9 +575,11 @@ def main() -> None:
             "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 4),
             "copy_bandwidth": copy,
             "frac_of_copy_bandwidth": round(achieved / copy["GBps"], 4),
-            "timing": "median of >= 20 HIP-graph replays of 8 calls (one per rotating copy), events on the "
-                      "launch stream",
+            "timing": "achieved = algorithmic bytes / time per call: median of >= 20 replays of a HIP graph of 8 "
+                      "back-to-back calls (one per rotating copy), events on the launch stream, inter-launch gaps "
+                      "included",
             "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)} for k, v in kernel.items()},
+            "kernel_trace": trace,
         },
         "cpu_baseline": cpu,
         "extra": results,
@@ -646,7 +703,7 @@ def cpu_baseline(stress, budget_seconds: float):
     sys.path.insert(0, str(ROOT / "oracle"))
     import ternary_oracle as T
 
-    cb = T.CpuBaseline()
+    cb = T.CpuBaseline(native=True)
     allowed = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else set(range(os.cpu_count() or 1))
     threads = max(1, min(physical_cores(allowed), 16))
     prepared = []
@@ -682,6 +739,7 @@ def cpu_baseline(stress, budget_seconds: float):
         "sample_1_thread": f"{single_calls} calls (~{budget_seconds / 4:.0f} s)",
         "cpu_model": cpu_model(),
         "cpus_allowed": len(allowed),
+        "march": cb.march,
     }
 
 

@@ -327,10 +327,22 @@ class Oracle:
 
 
 class CpuBaseline:
-    """ctypes view of libcpubaseline.so (the numba kernels restated with OpenMP)."""
+    """ctypes view of libcpubaseline.so (the numba kernels restated with OpenMP).  With ``native`` the
+    library is rebuilt on this host with -march=native (libcpubaseline_native.so, make target ``native``);
+    if that build fails the portable x86-64-v3 library is used and ``march`` says so."""
 
-    def __init__(self) -> None:
-        lib = _load("libcpubaseline.so")
+    def __init__(self, native: bool = False) -> None:
+        self.march = "x86-64-v3"
+        lib = None
+        if native:
+            done = subprocess.run(["make", "-s", "-B", "-C", str(HERE), "native"], capture_output=True, text=True)
+            if done.returncode == 0:
+                lib = ctypes.CDLL(str(HERE / "libcpubaseline_native.so"))
+                self.march = "native"
+            else:
+                self.march = f"x86-64-v3 (native build failed: {done.stderr.strip()[-200:]})"
+        if lib is None:
+            lib = _load("libcpubaseline.so")
         lib.cb_planes_of.argtypes = [c_void_p, c_int, c_int, c_int, c_void_p]
         lib.cb_set_threads.argtypes = [c_int]
         lib.cb_max_threads.restype = c_int
