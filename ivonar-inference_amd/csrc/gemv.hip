@@ -558,19 +558,6 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // a wave with no row pair still has its first loads out
 }
 
-int device_cus() {
-  static int cached[64] = {0};
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
-  if (cached[device] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
-      cus = 256;
-    cached[device] = cus;
-  }
-  return cached[device];
-}
-
 template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
 void launch_one(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                 size_t lds) {
@@ -661,6 +648,19 @@ hipError_t launch_fused(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a
 }
 
 }  // namespace
+
+int device_cus() {
+  static int cached[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+  if (cached[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[device] = cus;
+  }
+  return cached[device];
+}
 
 int gemv_fused_limit() { return kFusedLimit; }
 

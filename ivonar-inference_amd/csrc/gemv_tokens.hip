@@ -1,0 +1,302 @@
+// Token GEMV: M = 1..16 tokens against one packed matrix, each weight byte
+// streamed once for all tokens, on v_mfma_i32_16x16x64_i8 (the gemm_tile_*
+// entry points with m <= 16; reference: kernels/ternary.cu:688-765, the
+// 32-token tile it replaces for short prompts and decode batches).
+//
+// Work split.  A wave owns one tile of 16 weight rows and the contiguous span
+// range [p*PART, (p+1)*PART) of its row, a span being 64 packed bytes (two
+// 128-input groups).  The PARTS waves of a row tile sit in one block, with up
+// to 16/PARTS tiles per block.  Per span a lane (c = lane % 16, kb = lane / 16)
+// loads the 16 bytes [64s + 16kb, +16) of row c: one wave instruction reads
+// 16 rows x 64 contiguous bytes.  Two v_permlane32_swap exchanges give every
+// lane 8 bytes of the span's first group (group bytes 0-7, 16-23, 8-15, 24-31
+// for kb = 0..3) and 8 of its second, so that one MFMA's 64-input sum never
+// mixes groups.  The 2-bit fields of those 8 bytes, shifted to bit 0 and
+// masked (codes 0..2 as int8), are the B operands of two chained MFMAs per
+// group; the A operands are the q8 bytes of the same inputs for token c (the
+// token slots past M read token M-1 and are not stored).  The chain starts
+// from minus the group's q sum of the lane's four output tokens, so the int32
+// result is the exact group partial sum((code - 1) * q) for tokens 4kb..4kb+3
+// of row c.
+//
+// Activations.  The block copies the whole q8 rows of the M tokens (the
+// quantizer's layout, 8-byte pieces gathered into MFMA operand order) and the
+// group q sums into LDS once, after its waves have issued their first weight
+// loads; all waves then read their operands from LDS.  Weights stream through
+// a register ring UW spans deep; all scales of the wave's range are loaded up
+// front.
+//
+// fp32 order (the CPU oracle's orc_gemm_split with S = PARTS): each wave folds
+// its groups' partials into one fmaf chain per output in ascending group
+// order; the PARTS chains of a row tile are added in wave order, then the
+// token scale, the bias and the epilogue follow.
+#include <type_traits>
+
+#include "internal.hpp"
+#include "ternary_device.hpp"
+
+namespace ivo {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxTokens = 16;
+constexpr int kMaxWaves = 16;
+constexpr int kRing = 8;            // spans of weights in flight per wave
+constexpr int kSeedsPerThread = 4;  // group q sums each thread copies
+constexpr int kSpanBytes = 64;
+
+struct TokenShape {
+  int rows, n, row_bytes, groups, m, parts, tiles_per_block, out_stride;
+};
+
+// 2-bit field f of each byte of w, as an int8 code 0..2.
+template <int F>
+__device__ __forceinline__ int field(unsigned w) {
+  return (int)((w >> (2 * F)) & kLow2);
+}
+
+template <int EPI, int PART, int FILL>
+__global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t* __restrict__ q8,
+                                                                     const int32_t* __restrict__ xsum,
+                                                                     const float* __restrict__ scale_in,
+                                                                     const uint8_t* __restrict__ packed,
+                                                                     const uint16_t* __restrict__ scales,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ output, TokenShape sh) {
+  constexpr int UW = PART < kRing ? PART : kRing;
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, kb = lane >> 4;
+  const int m = sh.m;
+  const int tile = blockIdx.x * sh.tiles_per_block + wave / sh.parts;
+  const int part = wave % sh.parts;
+  const int span0 = part * PART;
+  const int chunks = sh.n / kChunk;
+  // LDS: A operands [group][o][kb][m][16 B], then the negated group q sums
+  // [group][4*sq] (tokens 4*sq and up zero), then the wave partials
+  // [wave][16 tokens][16 rows], then a 16-byte dump slot for fill pieces past the end.
+  const int abytes = sh.groups * 128 * m;
+  const int sq = (m + 3) >> 2;
+  const int seeds = sh.groups * 4 * sq;
+  int* lseed = reinterpret_cast<int*>(lds + abytes);
+  float* partial = reinterpret_cast<float*>(lds + abytes + 4 * seeds);
+  unsigned char* dump = lds + abytes + 4 * seeds + nthr / 64 * 1024;
+
+  // Token operand first (it is waited for before the weights), then the group
+  // q sums, the scales and the first UW spans of weights.  Fill item p is q8
+  // quad p of the block's tokens (token p / (8G), 16 contiguous bytes: the four
+  // fields of one packed word W of a group); its fields (0, 1) and (2, 3) are
+  // the halves W & 1 of the operands o = 0, 1 of lane group kb = 0, 0, 2, 2,
+  // 1, 1, 3, 3 (W = 0..7).
+  const int quads = abytes / 16;  // m * 8 * groups
+  v4u fill[FILL];
+#pragma unroll
+  for (int j = 0; j < FILL; ++j) {
+    const int p = min(j * nthr + tid, quads - 1);
+    fill[j] = *reinterpret_cast<const v4u*>(q8 + (size_t)p * 16);
+  }
+  int seed_value[kSeedsPerThread];
+#pragma unroll
+  for (int j = 0; j < kSeedsPerThread; ++j) {
+    const int p = min(j * nthr + tid, seeds - 1);
+    const int g = p / (4 * sq), t = p % (4 * sq);
+    const int2 xs = *reinterpret_cast<const int2*>(xsum + (size_t)min(t, m - 1) * chunks + 2 * g);
+    seed_value[j] = t < m ? -(xs.x + xs.y) : 0;
+  }
+  const int row = min(tile * 16 + c, sh.rows - 1);
+  const uint8_t* wrow = packed + (size_t)row * sh.row_bytes + (size_t)span0 * kSpanBytes + kb * 16;
+  const uint16_t* srow = scales + (size_t)row * sh.groups + span0 * 2;
+  unsigned sc[PART];  // the two fp16 group scales of each span
+#pragma unroll
+  for (int i = 0; i < PART; i += 2) {
+    if (i + 1 < PART) {
+      const uint2 v = *reinterpret_cast<const uint2*>(srow + 2 * i);
+      sc[i] = v.x;
+      sc[i + 1] = v.y;
+    } else {
+      sc[i] = *reinterpret_cast<const unsigned*>(srow + 2 * i);
+    }
+  }
+  v4u w[UW];
+#pragma unroll
+  for (int i = 0; i < UW; ++i) w[i] = *reinterpret_cast<const v4u*>(wrow + i * kSpanBytes);
+
+#pragma unroll
+  for (int j = 0; j < FILL; ++j) {
+    const int p = j * nthr + tid;
+    const int t = p / (8 * sh.groups), quad = p % (8 * sh.groups);
+    const int g = quad >> 3, word = quad & 7;
+    const int k = (0x33112200 >> (4 * word)) & 15;  // lane group of packed word `word`
+    unsigned char* piece = lds + (((g * 2) * 4 + k) * m + t) * 16 + 8 * (word & 1);
+    const bool live = p < quads;
+    *reinterpret_cast<uint2*>(live ? piece : dump) = uint2{fill[j][0], fill[j][1]};
+    *reinterpret_cast<uint2*>(live ? piece + 64 * m : dump) = uint2{fill[j][2], fill[j][3]};
+  }
+#pragma unroll
+  for (int j = 0; j < kSeedsPerThread; ++j) {
+    const int p = j * nthr + tid;
+    *(p < seeds ? lseed + p : reinterpret_cast<int*>(dump)) = seed_value[j];
+  }
+  // Only the LDS stores are waited for: the weight loads stay in flight.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  const unsigned char* abase = lds + (size_t)span0 * 2 * 128 * m + kb * 16 * m + min(c, m - 1) * 16;
+  const int* sbase = lseed + span0 * 2 * 4 * sq + min(kb, sq - 1) * 4;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < PART; ++i) {
+    v4i a[2][2], seed[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int o = 0; o < 2; ++o)
+        a[h][o] = *reinterpret_cast<const v4i*>(abase + (size_t)((2 * i + h) * 2 + o) * 64 * m);
+      seed[h] = *reinterpret_cast<const v4i*>(sbase + (2 * i + h) * 4 * sq);
+    }
+    const v4u wk = w[i % UW];
+    if (i + UW < PART) w[i % UW] = *reinterpret_cast<const v4u*>(wrow + (i + UW) * kSpanBytes);
+    // Lanes kb = 0, 1 keep their first 8 bytes and take the first 8 of lane
+    // kb + 2 for the span's first group; lanes kb = 2, 3 the reverse.
+    const auto s0 = __builtin_amdgcn_permlane32_swap(wk[0], wk[2], false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(wk[1], wk[3], false, false);
+    const unsigned x0[2] = {s0[0], s0[1]}, x1[2] = {s1[0], s1[1]};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const v4i b0 = {field<0>(x0[h]), field<1>(x0[h]), field<0>(x1[h]), field<1>(x1[h])};
+      const v4i b1 = {field<2>(x0[h]), field<3>(x0[h]), field<2>(x1[h]), field<3>(x1[h])};
+      v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[h][0], b0, seed[h], 0, 0, 0);
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[h][1], b1, d, 0, 0, 0);
+      const float s = h2f((uint16_t)(h ? sc[i] >> 16 : sc[i] & 0xffffu));
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf((float)d[v], s, acc[v]);
+    }
+    // One span per step: the accumulators and the memory operations stay in
+    // program order, which keeps the ring's registers from piling up.
+#pragma unroll
+    for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(acc[v]));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Partials of lane (c, kb): tokens 4kb + v of row c.
+#pragma unroll
+  for (int v = 0; v < 4; ++v) partial[(wave * 16 + 4 * kb + v) * 16 + c] = acc[v];
+  __syncthreads();
+
+  const int tiles = sh.tiles_per_block;
+  if constexpr (EPI == kSiluPair) {
+    // Output j of a token pairs gate row 2j and up row 2j + 1 of the tile.
+    for (int o = tid; o < tiles * 16 * 8; o += nthr) {
+      const int pair = o & 7, t = (o >> 3) & 15, tl = o >> 7;
+      const int r0 = (blockIdx.x * tiles + tl) * 16 + 2 * pair;
+      float y[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float* src = partial + ((tl * sh.parts) * 16 + t) * 16 + 2 * pair + e;
+        float total = src[0];
+        for (int p = 1; p < sh.parts; ++p) total = total + src[p * 256];
+        y[e] = total * scale_in[min(t, m - 1)];
+        if (bias != nullptr) y[e] = y[e] + bias[min(r0 + e, sh.rows - 1)];
+      }
+      if (t < m && r0 + 1 < sh.rows) output[(size_t)t * sh.out_stride + (r0 >> 1)] = ivo_silu(y[0]) * y[1];
+    }
+  } else {
+    for (int o = tid; o < tiles * 256; o += nthr) {
+      const int r = o & 15, t = (o >> 4) & 15, tl = o >> 8;
+      const int out_row = (blockIdx.x * tiles + tl) * 16 + r;
+      const float* src = partial + ((tl * sh.parts) * 16 + t) * 16 + r;
+      float total = src[0];
+      for (int p = 1; p < sh.parts; ++p) total = total + src[p * 256];
+      float y = total * scale_in[min(t, m - 1)];
+      if (bias != nullptr) y = y + bias[min(out_row, sh.rows - 1)];
+      if (t < m && out_row < sh.rows) {
+        float* dst = output + (size_t)t * sh.out_stride + out_row;
+        if constexpr (EPI == kResidual) *dst = *dst + y;
+        else *dst = y;
+      }
+    }
+  }
+}
+
+constexpr int kPartSpans[] = {16, 14, 8, 4, 2, 1};
+
+template <int EPI, int PART>
+hipError_t launch_part(hipStream_t stream, const GemmArgs& a, const TokenShape& sh, int fill, int blocks, int threads,
+                       size_t lds) {
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), lds, stream, a.q8_in, a.xsum_in, a.scale_in, a.packed,
+                       a.scales, a.bias, a.output, sh);
+    return hipGetLastError();
+  };
+  if (fill <= 2) return go(token_gemv_kernel<EPI, PART, 2>);
+  if (fill <= 4) return go(token_gemv_kernel<EPI, PART, 4>);
+  if (fill <= 8) return go(token_gemv_kernel<EPI, PART, 8>);
+  if (fill <= 12) return go(token_gemv_kernel<EPI, PART, 12>);
+  return go(token_gemv_kernel<EPI, PART, 16>);
+}
+
+template <int EPI>
+hipError_t launch_epi(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan) {
+  TokenShape sh{a.rows, a.n, a.row_bytes, a.groups, a.m, plan.parts, plan.tiles_per_block, a.out_stride};
+  const int threads = 64 * plan.parts * plan.tiles_per_block;
+  const int blocks = ceil_div(ceil_div(a.rows, 16), plan.tiles_per_block);
+  switch (plan.part_spans) {
+    case 16: return launch_part<EPI, 16>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    case 14: return launch_part<EPI, 14>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    case 8: return launch_part<EPI, 8>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    case 4: return launch_part<EPI, 4>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    case 2: return launch_part<EPI, 2>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    case 1: return launch_part<EPI, 1>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+TokenPlan token_gemv_plan(int m, int rows, int n, int cus, size_t max_lds) {
+  TokenPlan plan{0, 0, 0, 0, 0};
+  if (m < 1 || m > kMaxTokens || rows < 1 || n < 256 || n % 256 != 0) return plan;
+  const int spans = n / 256, groups = n / kGroup, tiles = ceil_div(rows, 16);
+  // Spans per wave: the longest range that still gives every CU eight waves,
+  // else the shortest available; at most 16 waves per row tile.
+  int part_spans = 0;
+  for (int candidate : kPartSpans) {
+    if (spans % candidate != 0 || spans / candidate > kMaxWaves) continue;
+    part_spans = candidate;
+    if ((long long)tiles * (spans / candidate) >= 8LL * cus) break;
+  }
+  if (part_spans == 0) return plan;
+  const int parts = spans / part_spans;
+  int tiles_per_block = ceil_div(tiles, cus);
+  if (tiles_per_block > kMaxWaves / parts) tiles_per_block = kMaxWaves / parts;
+  if (tiles_per_block < 1) tiles_per_block = 1;
+  const int threads = 64 * parts * tiles_per_block;
+  const size_t abytes = (size_t)groups * 128 * m;
+  const size_t seeds = (size_t)groups * 4 * ((m + 3) / 4);
+  const size_t lds = abytes + 4 * seeds + (size_t)threads / 64 * 1024 + 16;
+  const int fill = (int)((abytes / 16 + threads - 1) / threads);
+  // (Sixteen fill pieces per thread on top of a 16-span ring would spill.)
+  if (lds > max_lds || fill > (part_spans == 16 ? 12 : 16) || seeds > (size_t)kSeedsPerThread * threads) return plan;
+  plan.parts = parts;
+  plan.part_spans = part_spans;
+  plan.tiles_per_block = tiles_per_block;
+  plan.fill = fill;
+  plan.lds = lds;
+  return plan;
+}
+
+hipError_t launch_token_gemv(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan) {
+  if (plan.parts == 0) return hipErrorInvalidValue;
+  switch (a.epi) {
+    case kStore: return launch_epi<kStore>(stream, a, plan);
+    case kResidual: return launch_epi<kResidual>(stream, a, plan);
+    case kSiluPair: return launch_epi<kSiluPair>(stream, a, plan);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ivo

@@ -121,6 +121,21 @@ struct SkinnyPlan {
 };
 SkinnyPlan skinny_plan(int m, int rows, int n, size_t max_lds);
 hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan);
+// Token GEMV (1..16 tokens, K a multiple of 256, the tokens' q8 rows resident
+// in LDS): K-split into `parts` contiguous ranges of `part_spans` 256-input
+// spans (its fp32 order, as the GEMM's splits); parts == 0 means it does not
+// apply.
+struct TokenPlan {
+  int parts;
+  int part_spans;
+  int tiles_per_block;
+  int fill;
+  size_t lds;
+};
+TokenPlan token_gemv_plan(int m, int rows, int n, int cus, size_t max_lds);
+hipError_t launch_token_gemv(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan);
+// Compute units of the current device.
+int device_cus();
 
 hipError_t launch_embed(hipStream_t stream, const int64_t* tokens, int m, const uint8_t* packed,
                         const uint16_t* scales, float* output, int n, int row_bytes, int groups);

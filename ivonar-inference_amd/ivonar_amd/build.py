@@ -29,7 +29,7 @@ CSRC = PACKAGE.parent / "csrc"
 INCLUDE = PACKAGE.parent.parent / "include"
 LIBRARY = PACKAGE / "_lib" / "libivonar_ternary.so"
 ARCH = "gfx950"
-SOURCES = ("quantize.hip", "gemv.hip", "gemm.hip", "gemm_wide.hip", "gemm_skinny.hip", "embed.hip", "sample.hip", "stream_read.hip",
+SOURCES = ("quantize.hip", "gemv.hip", "gemv_tokens.hip", "gemm.hip", "gemm_wide.hip", "gemm_skinny.hip", "embed.hip", "sample.hip", "stream_read.hip",
            "validate.hip", "capi.hip")
 HIP_FLAGS = (
     f"--offload-arch={ARCH}",

@@ -1,0 +1,95 @@
+"""GPU parity of the token GEMV: 1..16 tokens against one packed matrix with K a multiple of 256 and the
+tokens' q8 rows within the LDS budget (the gemm_tile_* entry points route those calls to it).
+
+Every output of every token is checked bit for bit against the oracle's split order (S = the library's
+plan, contiguous group ranges folded in order and added in order), and token 0 within rel 1e-5 / abs 1e-6
+of the fp64 truth.  Cases: the planner's span choices (1, 2, 4, 8, 14 and 16 spans per wave), ragged row
+counts, a bias, both epilogues with a padded output stride, token counts that are not a multiple of four
+(the last lane group's slots past M), and the fallback to the skinny kernel above the LDS budget."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import ternary_oracle as T
+from _util import assert_bits_equal, assert_within, device_matrix, finish_all_rows, make_layer, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(array, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+def _case(oracle, cuda, m, k, rows, bias, seed, epilogue="store", pad=0):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    print(f"token gemv m={m} k={k} rows={rows} bias={bias} {epilogue}", flush=True)
+    rng = np.random.default_rng(seed)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=bias)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[:, :: max(1, k // 50)] *= 20.0  # outlier channels set the absmax
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    assert_bits_equal(to_np(q8), eq8, "q8")
+    width = rows // 2 if epilogue == "silu_pair" else rows
+    stride = width + pad
+    base = rng.standard_normal((m, stride)).astype(np.float32) if epilogue == "residual" else np.zeros(
+        (m, stride), np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    splits = runtime.gemm_plan(m, rows, k)
+    epi = {"store": T.EPI_STORE, "residual": T.EPI_RESIDUAL, "silu_pair": T.EPI_SILU_PAIR}[epilogue]
+    q = T.q8_linear(eq8, k)
+    expected = finish_all_rows(oracle, 1, splits, epi, codes, q, scale_bits, esx, b, base.copy(), k, stride)
+    got = to_np(out)
+    assert_bits_equal(got, expected, f"token gemv m={m} k={k} rows={rows} ({splits} splits)")
+    if pad:
+        assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "wrote past the output width"
+    if epilogue == "store":
+        truth = T.truth_fp64(oracle.group_partials(eq8[0], exsum[0], packed, rows, k), T.half_bits_to_float(scale_bits),
+                             esx[0], b)
+        assert_within(got[0, :rows], truth, what="token 0 vs fp64 truth")
+    return splits
+
+
+# (m, k, rows, bias, K-splits of the plan on a 256-CU device): the plan takes the longest span range
+# per wave that still gives every CU eight waves, else one span per wave.
+@pytest.mark.parametrize("m,k,rows,bias,splits", [
+    (1, 1024, 4096, False, 4),     # 4 spans, 1 per wave
+    (5, 4096, 1000, True, 16),     # ragged rows, 16 waves per row tile
+    (3, 8192, 8200, True, 4),      # 8 spans per wave, ragged rows
+    (8, 2048, 16384, False, 2),    # 4 spans per wave
+    (2, 28672, 8192, False, 7),    # the long-row stress shape, 16 spans per wave
+    (16, 8192, 2000, False, 16),   # 2 spans per wave, 128 KB of token bytes
+    (4, 28672, 1000, True, 14),    # 8 spans per wave (no range reaches eight waves per CU)
+    (4, 7168, 16384, False, 2),    # 14 spans per wave
+    (16, 256, 40, True, 1),        # one span, one wave per row tile
+    (13, 3584, 4100, False, 14),   # 14 spans, one per wave
+])
+def test_token_gemv_store(cuda, oracle, m, k, rows, bias, splits):
+    got = _case(oracle, cuda, m, k, rows, bias, seed=m * 1009 + k + rows)
+    assert got == splits
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+@pytest.mark.parametrize("m,k,rows", [(7, 2048, 1000), (16, 4096, 514), (1, 8192, 3000)])
+def test_token_gemv_epilogues(cuda, oracle, epilogue, m, k, rows):
+    _case(oracle, cuda, m, k, rows, True, seed=m * 31 + k + rows + (7 if epilogue == "residual" else 0),
+          epilogue=epilogue, pad=3)
+
+
+def test_token_gemv_stress_shape_sixteen_tokens(cuda, oracle):
+    """K=8192 -> N=28672 with 16 tokens: 128 KB of token bytes in LDS, the planner's largest fill."""
+    assert _case(oracle, cuda, 16, 8192, 28672, False, seed=5) == 2
+
+
+def test_token_gemv_falls_back_above_lds(cuda, oracle):
+    """16 tokens of 28672 inputs (448 KB of q8) do not fit: the skinny kernel runs, in its own split order."""
+    splits = _case(oracle, cuda, 16, 28672, 512, True, seed=6)
+    assert splits == 4
