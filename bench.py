@@ -402,7 +402,48 @@ def m_sweep(device, stream) -> dict:
                 crossover = m
         table[str(m)] = entry
     return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover,
-            "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph"}
+            "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph; gemm_us for M <= 16 "
+                    "is the token GEMV (K a multiple of 256)"}
+
+
+def stress_tokens(matrices, stress, stream, replays: int) -> dict:
+    """Cold-cache GEMM with M = 1..16 tokens on the two stress shapes (8 rotating copies per shape, one
+    HIP graph of 8 calls, median of `replays` replays): the token GEMV where the tokens' q8 rows fit in
+    LDS, the skinny kernel otherwise; beside it the M = 1 GEMV on pre-quantized input."""
+    import numpy as np
+    import torch
+
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(11)
+    table = {}
+    for shape, (layer, _) in enumerate(stress):
+        k, n = layer.in_features, layer.rows
+        out = torch.empty((16, n), dtype=torch.float32, device=matrices[shape][0].packed.device)
+        entry = {}
+        for m in (1, 2, 4, 8, 16):
+            x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(out.device)
+            q8, xsum, sx = ops.quantize_rows(x)
+
+            def run(q8=q8, xsum=xsum, sx=sx, m=m):
+                for mat in matrices[shape]:
+                    ops.gemm(mat, q8, xsum, sx, out=out[:m])
+
+            t = time_graph(graph_of(run, stream), replays, 2, median=True) / len(matrices[shape])
+            entry[str(m)] = {"us": round(t * 1e6, 3), "GBps": round(gemv_bytes(m, n, k) / t / 1e9, 1),
+                             "splits": runtime.gemm_plan(m, n, k)}
+        q8, xsum, sx = ops.quantize_rows(torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32)).to(out.device))
+
+        def gemv(q8=q8, xsum=xsum, sx=sx):
+            for mat in matrices[shape]:
+                ops.gemv_prequant(mat, q8, xsum, sx, out=out[0])
+
+        t1 = time_graph(graph_of(gemv, stream), replays, 2, median=True) / len(matrices[shape])
+        entry["gemv_m1_us"] = round(t1 * 1e6, 3)
+        entry["m16_over_gemv_m1"] = round(entry["16"]["us"] / entry["gemv_m1_us"], 3)
+        entry["m16_over_m1"] = round(entry["16"]["us"] / entry["1"]["us"], 3)
+        table[f"{k}x{n}"] = entry
+    return {"by_shape": table, "timing": "median of HIP-graph replays of 8 calls (one per rotating copy), per call"}
 
 
 def main() -> None:
@@ -474,21 +515,8 @@ def main() -> None:
         g = graph_of(prequant, stream)
         t = time_graph(g, max(20, args.steps // ROTATING_COPIES), 2, median=True) / ROTATING_COPIES
         kernel[f"{layer.in_features}x{layer.rows}"] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
-    # the same shapes through the K-split MFMA kernel (gemm_tile_store with one token)
-    skinny = {}
-    for shape, (layer, x) in enumerate(stress):
-        q8, xsum, sx = ops.quantize_rows(inputs[shape].reshape(1, -1))
-        out2 = torch.empty((1, layer.rows), dtype=torch.float32, device=device)
-
-        def mfma_m1(shape=shape, q8=q8, xsum=xsum, sx=sx, out2=out2):
-            for copy in range(ROTATING_COPIES):
-                ops.gemm(matrices[shape][copy], q8, xsum, sx, out=out2)
-
-        g = graph_of(mfma_m1, stream)
-        t = time_graph(g, max(1, args.steps // ROTATING_COPIES), 2) / ROTATING_COPIES
-        b = gemv_bytes(1, layer.rows, layer.in_features)
-        skinny[f"{layer.in_features}x{layer.rows}"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1)}
-    results["mfma_m1_stress"] = skinny
+    # the same shapes with 1..16 tokens through the gemm_tile_store path (token GEMV / skinny kernel)
+    results["stress_tokens"] = stress_tokens(matrices, stress, stream, max(20, args.steps // ROTATING_COPIES))
     kernel_bytes = sum(v["bytes"] for v in kernel.values())
     kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
     achieved = kernel_bytes / kernel_seconds / 1e9
