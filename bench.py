@@ -12,8 +12,9 @@ launch stream around each replay: ``ms_per_step`` is the median replay / K.
 bytes(M,N,K) = N*ceil(K/4) + 2*N*ceil(K/128) + 4*M*K + 4*M*N.
 
 Also reported on the same line: the GEMV kernel alone (pre-quantized
-activations, each launch bracketed by HIP events on the launch stream) as
-the roofline figure, the
+activations) as the roofline figure, from the dispatch durations of a
+rocprofv3 kernel-trace pass the bench runs itself, with the HIP-event time
+per call inside a graph of 8 back-to-back calls beside it; the
 single-linear case (K=1024 -> N=4096), the 32-token prefill tile GEMM TOPS,
 and the CPU baseline (the reference's numba GEMV restated in C++/OpenMP)
 on a bounded sample of the same workload.
@@ -39,6 +40,8 @@ ROTATING_COPIES = 8
 HEADLINE_REPLAYS = 20
 PROBE_GEMM_SHAPES = [(1024, 4096), (4096, 1024), (4096, 14336)]  # (K, N) of the GEMM probe, in order
 PROBE_GEMM_M = (2048, 32)
+PROBE_BIG_READ_BYTES = 1 << 30
+PROBE_BIG_READS = 4
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
@@ -52,7 +55,7 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     parser.add_argument("--skip-cpu", action="store_true")
-    parser.add_argument("--probe", choices=["gemv-stress", "gemm-prefill"], default=None,
+    parser.add_argument("--probe", choices=["gemv-stress", "gemm-prefill", "tokens"], default=None,
                         help="profiling mode: only the named kernel workload, no JSON line")
     parser.add_argument("--probe-calls", type=int, default=16)
     parser.add_argument("--no-traffic", action="store_true", help="skip the three rocprofv3 counter passes")
@@ -60,14 +63,24 @@ def parse() -> argparse.Namespace:
 
 
 def probe_gemv_stress(calls: int) -> None:
-    """GEMV kernel alone (pre-quantized input) on both stress shapes, cycling 8 copies; then a
-    512 MiB device copy of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    """GEMV kernel alone (pre-quantized input) on both stress shapes, cycling 8 copies, then the
+    streaming-read kernel once over each copy's packed bytes (58.7 MB launches); then PROBE_BIG_READS
+    streaming reads of one 1 GiB buffer; then a 512 MiB device copy of known size that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters."""
     import torch
 
     from ivonar_amd import ops, runtime, synthetic
 
     device = torch.device("cuda", 0)
     runtime.initialise(0)
+    lib = runtime.library()
+    sink = torch.empty(lib.ivonar_stream_read_sink_words(), dtype=torch.int32, device=device)
+    stream_id = runtime.current_stream()
+
+    def stream_read(tensor):
+        runtime.check(lib.ivonar_stream_read(stream_id, runtime.pointer(tensor), tensor.numel(), runtime.pointer(sink)),
+                      "ivonar_stream_read")
+
     for layer, x in synthetic.stress_layers(seed=3):
         mats = device_copies(layer, device, ROTATING_COPIES)
         q8, xsum, sx = ops.quantize_rows(torch.from_numpy(x).to(device))
@@ -76,12 +89,49 @@ def probe_gemv_stress(calls: int) -> None:
         for call in range(calls):
             ops.gemv_prequant(mats[call % ROTATING_COPIES], q8, xsum, sx, out=out)
         torch.cuda.synchronize()
-        print(f"probe: gemv {layer.in_features}->{layer.rows} x{calls} done", flush=True)
+        for mat in mats:
+            stream_read(mat.packed)
+        torch.cuda.synchronize()
+        print(f"probe: gemv {layer.in_features}->{layer.rows} x{calls}, {len(mats)} reads done", flush=True)
+        del mats
+    big = torch.empty(PROBE_BIG_READ_BYTES, dtype=torch.uint8, device=device)  # contents unused: no fill dispatch
+    torch.cuda.synchronize()
+    for _ in range(PROBE_BIG_READS):
+        stream_read(big)
+    torch.cuda.synchronize()
+    del big
+    print(f"probe: {PROBE_BIG_READS} reads of 1 GiB done", flush=True)
     src = torch.empty(512 * 2**20, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
     print("probe: 512 MiB copy done", flush=True)
+
+
+def probe_tokens(calls: int) -> None:
+    """GEMM with M = 1, 2, 4, 8, 16 tokens on both stress shapes (pre-quantized activations), `calls`
+    launches per M cycling the 8 rotating copies: the token GEMV, or the skinny kernel where the tokens'
+    q8 rows do not fit in LDS."""
+    import numpy as np
+    import torch
+
+    from ivonar_amd import ops, runtime, synthetic
+
+    device = torch.device("cuda", 0)
+    runtime.initialise(0)
+    rng = np.random.default_rng(11)
+    for layer, _ in synthetic.stress_layers(seed=3):
+        mats = device_copies(layer, device, ROTATING_COPIES)
+        for m in (1, 2, 4, 8, 16):
+            x = torch.from_numpy(rng.standard_normal((m, layer.in_features)).astype(np.float32)).to(device)
+            q8, xsum, sx = ops.quantize_rows(x)
+            out = torch.empty((m, layer.rows), dtype=torch.float32, device=device)
+            torch.cuda.synchronize()
+            for call in range(calls):
+                ops.gemm(mats[call % ROTATING_COPIES], q8, xsum, sx, out=out)
+            torch.cuda.synchronize()
+            print(f"probe: tokens m={m} {layer.in_features}->{layer.rows} x{calls} done", flush=True)
+        del mats
 
 
 def probe_gemm_prefill(calls: int) -> None:
@@ -173,25 +223,34 @@ def copy_bandwidth(device, stream, size: int = 1 << 30) -> dict:
 def read_ceiling(matrices, stream) -> dict:
     """Streaming-read bandwidth over the packed weights the GEMV streams (8 rotating copies of both stress
     matrices, 58.7 MB each), one launch per matrix, timed like the GEMV: the best a kernel that only reads
-    achieves per launch at this size."""
+    achieves per launch at this size; and the same kernel over one 1 GiB buffer in one launch (the sustained
+    rate, without the per-launch ramp and drain)."""
     import torch
 
     from ivonar_amd import runtime
 
     lib = runtime.library()
-    sink = torch.empty(lib.ivonar_stream_read_sink_words(), dtype=torch.int32, device=matrices[0][0].packed.device)
+    device = matrices[0][0].packed.device
+    sink = torch.empty(lib.ivonar_stream_read_sink_words(), dtype=torch.int32, device=device)
     buffers = [(m.packed, m.packed.numel()) for shape in matrices for m in shape]
     total = sum(size for _, size in buffers)
 
-    def run():
-        stream_id = runtime.current_stream()
-        for tensor, size in buffers:
-            runtime.check(lib.ivonar_stream_read(stream_id, runtime.pointer(tensor), size, runtime.pointer(sink)),
-                          "ivonar_stream_read")
+    def read(items):
+        def run():
+            stream_id = runtime.current_stream()
+            for tensor, size in items:
+                runtime.check(lib.ivonar_stream_read(stream_id, runtime.pointer(tensor), size, runtime.pointer(sink)),
+                              "ivonar_stream_read")
+        return run
 
-    seconds = time_graph(graph_of(run, stream), 20, 2, median=True)
-    return {"GBps": round(total / seconds / 1e9, 1), "bytes": total,
-            "kernel": "ivonar_stream_read (16-byte loads, 4 in flight per thread, 1024 blocks)"}
+    seconds = time_graph(graph_of(read(buffers), stream), 20, 2, median=True)
+    big = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    big.fill_(1)
+    big_seconds = time_graph(graph_of(read([(big, big.numel())]), stream), 20, 2, median=True)
+    del big
+    return {"GBps": round(total / seconds / 1e9, 1), "bytes": total, "us_per_launch": round(seconds / len(buffers) * 1e6, 3),
+            "one_GiB_launch": {"GBps": round((1 << 30) / big_seconds / 1e9, 1), "us": round(big_seconds * 1e6, 2)},
+            "kernel": "ivonar_stream_read (non-temporal 16-byte loads, 4 in flight per thread, 1024 blocks)"}
 
 
 def validate_throughput(matrices, stream) -> dict:
@@ -277,24 +336,34 @@ def measure_traffic(calls: int = 8) -> dict:
         rows = counter_pass([counter], "gemv-stress", calls)
         if isinstance(rows, str):
             return {"error": rows}
-        gemv, other = {}, []
+        gemv, reads, other = {}, [], []
         for row in rows:
             if counter not in row:
                 continue
-            if "gemv_kernel" in row["kernel"]:
+            if "gemv_kernel" in row["kernel"] or "gemv_rows_kernel" in row["kernel"]:
                 gemv.setdefault(row["grid"], []).append(row[counter])
+            elif "stream_read" in row["kernel"]:
+                reads.append(row[counter])
             else:
                 other.append(row[counter])
         if not gemv or not other:
             return {"error": f"{counter} pass found no GEMV or copy dispatch"}
         readings[counter] = {"factor": (512 * 1024) / max(other),
-                             "per_grid": {grid: sum(v) / len(v) for grid, v in gemv.items()}}
+                             "per_grid": {grid: sum(v) / len(v) for grid, v in gemv.items()}, "reads": reads}
     fetch, write = readings["FETCH_SIZE"], readings["WRITE_SIZE"]
     per_launch = [fetch["per_grid"][grid] * fetch["factor"] * 1024 + write["per_grid"].get(grid, 0.0) * write["factor"] * 1024
                   for grid in fetch["per_grid"]]
+    # streaming-read launches: the last PROBE_BIG_READS read the 1 GiB buffer, the others one packed copy each
+    reads = [v * fetch["factor"] * 1024 for v in fetch["reads"]]
+    read_fetch = None
+    if len(reads) > PROBE_BIG_READS:
+        small, big = reads[:-PROBE_BIG_READS], reads[-PROBE_BIG_READS:]
+        read_fetch = {"copy_launch_bytes": round(sum(small) / len(small)), "one_GiB_launch_bytes": round(sum(big) / len(big)),
+                      "note": "FETCH_SIZE x factor per streaming-read dispatch: 58.7 MB packed-copy launches and "
+                              "1 GiB launches (1,073,741,824 bytes read)"}
     return {"bytes_per_launch": sum(per_launch) / len(per_launch),
             "fetch_factor": round(fetch["factor"], 4), "write_factor": round(write["factor"], 4),
-            "per_launch": [round(v) for v in per_launch]}
+            "per_launch": [round(v) for v in per_launch], "stream_read_fetch": read_fetch}
 
 
 def measure_trace(calls: int = 32) -> dict:
@@ -333,11 +402,33 @@ def measure_trace(calls: int = 32) -> dict:
             if "gemv" in row["Name"]:
                 name = row["Name"].replace("void ivo::(anonymous namespace)::", "").split("(")[0]
                 kernels[name] = {"calls": int(row["Calls"]), "average_us": round(float(row["AverageNs"]) / 1e3, 3)}
+    # streaming reads, per dispatch in launch order: one per packed copy of each shape, then the 1 GiB reads
+    reads = []
+    for path in sorted(Path(out).rglob("*kernel_trace.csv")):
+        with open(path) as handle:
+            reader = csv.DictReader(handle)
+            if not {"Kernel_Name", "Start_Timestamp", "End_Timestamp"} <= set(reader.fieldnames or []):
+                continue
+            rows = [row for row in reader if "stream_read" in row["Kernel_Name"]]
+        rows.sort(key=lambda row: int(row["Start_Timestamp"]))
+        reads = [(int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3 for row in rows]
     shutil.rmtree(out, ignore_errors=True)
     per_launch = 62537728
-    return {"kernels": kernels,
-            "GBps_from_average": {k: round(per_launch / (v["average_us"] * 1e3), 1) for k, v in kernels.items()},
-            "note": "dispatch durations from the trace exclude the gap between back-to-back launches"}
+    result = {"kernels": kernels,
+              "GBps_from_average": {k: round(per_launch / (v["average_us"] * 1e3), 1) for k, v in kernels.items()},
+              "note": "dispatch durations from the trace exclude the gap between back-to-back launches"}
+    if len(reads) == 2 * ROTATING_COPIES + PROBE_BIG_READS:
+        small, big = reads[:2 * ROTATING_COPIES], reads[2 * ROTATING_COPIES:]
+        copy_bytes = 28672 * 8192 // 4  # the packed bytes of either stress shape: 58,720,256
+        result["stream_read"] = {
+            "copy_launch_us": round(sum(small) / len(small), 3),
+            "copy_launch_GBps": round(copy_bytes / (sum(small) / len(small) * 1e3), 1),
+            "one_GiB_launch_us": round(sum(big) / len(big), 2),
+            "one_GiB_launch_GBps": round(PROBE_BIG_READ_BYTES / (sum(big) / len(big) * 1e3), 1)}
+    else:
+        result["stream_read"] = {"error": f"expected {2 * ROTATING_COPIES + PROBE_BIG_READS} streaming-read dispatches, "
+                                          f"found {len(reads)}"}
+    return result
 
 
 def measure_mfma(calls: int = 16, cus: int = 256, xcds: int = 8) -> dict:
@@ -458,6 +549,9 @@ def main() -> None:
     if args.probe == "gemm-prefill":
         probe_gemm_prefill(args.probe_calls)
         return
+    if args.probe == "tokens":
+        probe_tokens(args.probe_calls)
+        return
     import numpy as np
     import torch
 
@@ -519,7 +613,17 @@ def main() -> None:
     results["stress_tokens"] = stress_tokens(matrices, stress, stream, max(20, args.steps // ROTATING_COPIES))
     kernel_bytes = sum(v["bytes"] for v in kernel.values())
     kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
-    achieved = kernel_bytes / kernel_seconds / 1e9
+    achieved_graph = kernel_bytes / kernel_seconds / 1e9
+    achieved, timing = achieved_graph, ("algorithmic bytes / time per call: median of >= 20 replays of a HIP graph "
+                                        "of 8 back-to-back calls (one per rotating copy), events on the launch "
+                                        "stream, inter-launch gaps included (the kernel-trace pass failed)")
+    if trace and trace.get("kernels"):
+        calls = sum(v["calls"] for v in trace["kernels"].values())
+        mean_us = sum(v["calls"] * v["average_us"] for v in trace["kernels"].values()) / calls
+        achieved = (kernel_bytes / len(kernel)) / (mean_us * 1e-6) / 1e9
+        timing = ("algorithmic bytes per launch / mean dispatch duration of the GEMV kernels in the rocprofv3 "
+                  "kernel-trace pass (kernel_trace); achieved_graph is the HIP-event time per call inside a graph "
+                  "of 8 back-to-back calls, median of >= 20 replays, inter-launch gaps included")
     ceiling = read_ceiling(matrices, stream)
     results["checkpoint_validate"] = validate_throughput(matrices, stream)
     copy = copy_bandwidth(device, stream)
@@ -595,17 +699,19 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "achieved_graph": round(achieved_graph, 2),
+            "frac_graph": round(achieved_graph / HBM_PEAK_GBS, 4),
             "traffic": None if not traffic or "error" in traffic else round(traffic["bytes_per_launch"]),
             "traffic_detail": traffic,
             "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
             "kernel": "gemv_kernel at K=8192, gemv_rows_kernel at K=28672 (pre-quantized activations)",
             "read_ceiling": ceiling,
-            "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 4),
+            "graph_frac_of_read_ceiling": round(achieved_graph / ceiling["GBps"], 4),
+            "frac_of_read_ceiling_trace": (round(achieved / trace["stream_read"]["copy_launch_GBps"], 4)
+                                           if trace and "copy_launch_GBps" in trace.get("stream_read", {}) else None),
             "copy_bandwidth": copy,
             "frac_of_copy_bandwidth": round(achieved / copy["GBps"], 4),
-            "timing": "achieved = algorithmic bytes / time per call: median of >= 20 replays of a HIP graph of 8 "
-                      "back-to-back calls (one per rotating copy), events on the launch stream, inter-launch gaps "
-                      "included",
+            "timing": timing,
             "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)} for k, v in kernel.items()},
             "kernel_trace": trace,
         },

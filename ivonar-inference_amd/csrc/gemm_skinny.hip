@@ -227,10 +227,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 // loads, 16 bytes per lane, XOR-swizzled pieces) and the fp16 scales of the
 // block's rows from its first group on, and loads the packed bytes of its
 // groups into registers, group by group, so that group j's loads are complete
-// once no more than (NG-1-j) groups' loads are outstanding: step j waits for
-// that count and a barrier (measured on MI355X: a wave that reads the bytes of
-// its own direct-to-LDS load right after the counter reaches them sometimes
-// reads the half of the 64 lanes that is still being written; with the barrier
+// once no more than (NG-1-j) groups' loads are outstanding (vector loads,
+// direct-to-LDS ones included, retire in issue order on the counter): step j
+// waits for that count and then a barrier.  The counter is what the ISA
+// documents; the barrier is a measured guard (on MI355X a wave that read its
+// own direct-to-LDS bytes right after the counter reached them sometimes read
+// the half of the 64 lanes that was still being written, and with the barrier
 // it never did).  The token fragments of a group feed all R row tiles.  Prompts
 // of more than 32 tokens run as slices of 32 tokens (grid dimension y).  Tokens
 // past the slice and the missing second chunk of an odd chunk count read as
@@ -324,8 +326,8 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
       for (int i = 0; i < 4; ++i) acc[mt][r][i] = 0.0f;
   static_for<NG>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    // A direct-to-LDS load may still be writing LDS when the counter says it is complete: the
-    // reads of its bytes wait for the counter and then a barrier (every wave passes all NG).
+    // The reads of a direct-to-LDS load's bytes wait for the counter and then a barrier (a load
+    // was seen still writing LDS after the counter alone; every wave passes all NG barriers).
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"((NG - 1 - j) * T::kLoadsPerGroup)
                  : "memory");
     if (j >= count) return;  // wave-uniform

@@ -134,8 +134,12 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
       xs = lds_x[u];
     }
     const int seed = XNEG ? xs : -xs;  // XNEG: the LDS copy holds minus the chunk sums
-    // The partner's row first: its sum crosses the pair by DPP, which must not
-    // read a register the instruction just before it wrote.
+    // The partner's row first: its sum crosses the pair by DPP, and a DPP read
+    // of a VGPR needs two wait states after the VALU instruction that wrote it
+    // (gfx9 family).  The compiler pads that gap with s_nop where nothing
+    // independent fills it; computing the partner's sum first puts the own
+    // row's dot products in the gap.  The order saves issue cycles only: the
+    // result does not depend on it.
     int d1 = chunk_code_dot(st.w[j][1], q0, q1, q2, q3, seed);
     int d0 = chunk_code_dot(st.w[j][0], q0, q1, q2, q3, seed);
     if constexpr (!EXACT) {

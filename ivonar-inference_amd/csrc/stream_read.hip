@@ -1,9 +1,12 @@
 // Streaming-read reference kernel (no counterpart in the reference): reads a
-// buffer once with 16-byte loads, four per thread in flight, and folds the
-// words into an XOR that is stored only when it equals a fixed constant (so
-// the loads are kept and nothing is written in practice).  Its bandwidth over
-// the same rotating buffers the GEMV streams is the read ceiling the GEMV's
-// roofline fraction is compared with.
+// buffer once with non-temporal 16-byte loads, four per thread in flight,
+// grid-stride over 1024 blocks, and folds the words into an XOR that is stored
+// only when it equals a fixed constant (so the loads are kept and nothing is
+// written in practice).  Its bandwidth over the same rotating buffers the GEMV
+// streams is the per-launch read ceiling the GEMV's roofline fraction is
+// compared with.  (Measured on MI355X: non-temporal loads read 58.7 MB per
+// launch in 10.1 us and 1 GiB in 161 us, plain loads in 10.7 and 180 us;
+// other depths, block counts and per-block slices were no faster.)
 #include "internal.hpp"
 #include "ternary_device.hpp"
 
@@ -22,7 +25,9 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint4* __re
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       long long i = base + (long long)u * kThreads + threadIdx.x;
-      v[u] = data[i < words ? i : words - 1];
+      typedef unsigned v4u __attribute__((ext_vector_type(4)));
+      const v4u w = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(data) + (i < words ? i : words - 1));
+      v[u] = make_uint4(w[0], w[1], w[2], w[3]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) fold ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
