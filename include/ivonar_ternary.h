@@ -39,10 +39,12 @@ extern "C" {
 
 /* ---------------------------------------------------------------- set-up */
 
-/* Allocates the per-device activation scratch used when a GEMV quantizes
- * rows longer than the fused limit.  Call once per device outside graph
- * capture; replaces the reference's compile_module set-up step
- * (kernels/runtime.py:301-324).  Calls with the device current. */
+/* Allocates the per-device scratch: the activation row a GEMV quantizes when
+ * its rows are longer than the fused limit, and the 16 MB of fp32 wave
+ * chains of a K-sliced token GEMM (1..16 tokens whose q8 rows exceed LDS).
+ * Call once per device outside graph capture; replaces the reference's
+ * compile_module set-up step (kernels/runtime.py:301-324).  Calls with the
+ * device current. */
 hipError_t ivonar_init(int device);
 
 /* Process-wide values the reference passes as -D defines to NVRTC
@@ -148,7 +150,9 @@ hipError_t ivonar_quantize_rows(hipStream_t stream, int mode, const float* input
 /* ---------------------------------------------------------- token GEMM
  * GEMM_ARGS of ternary.cu:671-674 (gemm_tile_* :767-784): m token rows of
  * pre-quantized activations against `rows` weight rows on int8 MFMA; output
- * row t at output + t*out_stride. */
+ * row t at output + t*out_stride.  For 1..16 tokens with n a multiple of 256
+ * whose q8 rows exceed LDS, the call is two launches sharing the device
+ * scratch (see ivonar_init): concurrent such calls on one device race. */
 #define IVONAR_GEMM_ARGS                                                                                      \
   const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, const uint8_t *packed,              \
       const uint16_t *scales, const float *bias, float *output, int rows, int n, int row_bytes, int groups, \

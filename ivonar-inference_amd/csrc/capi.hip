@@ -31,17 +31,21 @@ hipError_t allocate_scratch(int device) {
   void* q8 = nullptr;
   void* xsum = nullptr;
   void* scale = nullptr;
+  void* partials = nullptr;
   hipError_t status = hipMalloc(&q8, (size_t)kScratchChunks * kChunk);
   if (status == hipSuccess) status = hipMalloc(&xsum, (size_t)kScratchChunks * sizeof(int32_t));
   if (status == hipSuccess) status = hipMalloc(&scale, 256);
+  if (status == hipSuccess) status = hipMalloc(&partials, (size_t)kTokenPartialFloats * sizeof(float));
   if (status != hipSuccess) {
     if (q8) (void)hipFree(q8);
     if (xsum) (void)hipFree(xsum);
+    if (scale) (void)hipFree(scale);
     return status;
   }
   s.q8 = static_cast<int8_t*>(q8);
   s.xsum = static_cast<int32_t*>(xsum);
   s.scale = static_cast<float*>(scale);
+  s.token_partials = static_cast<float*>(partials);
   s.capacity_chunks = kScratchChunks;
   return hipSuccess;
 }

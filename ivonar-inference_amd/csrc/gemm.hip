@@ -370,14 +370,15 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 
 }  // namespace
 
-// Kernel choice: the token GEMV for up to 16 tokens whose q8 rows fit in LDS
-// (K a multiple of 256); the skinny kernels up to 32 tokens; then the long-prompt
+// Kernel choice: the token GEMV for up to 16 tokens (K a multiple of 256; K
+// sliced across blocks where the tokens' q8 rows do not fit in LDS whole);
+// the skinny kernels up to 32 tokens; then the long-prompt
 // tilings; then the LDS-staged skinny kernel in 32-token slices up to
 // kSlicedTokens; otherwise the tiled kernel.
 int gemm_splits(int m, int rows, int n) {
   const size_t lds = (size_t)max_lds_per_block();
   const TokenPlan tokens = token_gemv_plan(m, rows, n, device_cus(), lds);
-  if (tokens.parts > 0) return tokens.parts;
+  if (tokens.parts > 0) return tokens.parts * tokens.slices;
   if (gemm_wide_tokens(m, rows, n) > 0) return 1;
   if (gemm_split_applies(m, rows, n)) return 4;
   const SkinnyPlan plan = skinny_plan(m, rows, n, lds);

@@ -26,10 +26,17 @@
 // a register ring UW spans deep; all scales of the wave's range are loaded up
 // front.
 //
-// fp32 order (the CPU oracle's orc_gemm_split with S = PARTS): each wave folds
-// its groups' partials into one fmaf chain per output in ascending group
-// order; the PARTS chains of a row tile are added in wave order, then the
-// token scale, the bias and the epilogue follow.
+// Long rows.  Where the tokens' whole q8 rows do not fit in LDS, K is cut
+// into `slices` equal span ranges, one per block row of the grid (grid y):
+// a block then copies and reads only its slice's q8 bytes and q sums, and
+// its waves write their fp32 chains to the scratch ([slice * parts + part]
+// [token][row]) instead of adding them; token_finish_kernel adds them.
+//
+// fp32 order (the CPU oracle's orc_gemm_split with S = PARTS * slices): each
+// wave folds its groups' partials into one fmaf chain per output in ascending
+// group order; the S chains of an output are added in wave order (slice
+// first, then the part within it), then the token scale, the bias and the
+// epilogue follow.
 #include <type_traits>
 
 #include "internal.hpp"
@@ -46,9 +53,12 @@ constexpr int kMaxWaves = 16;
 constexpr int kRing = 8;            // spans of weights in flight per wave
 constexpr int kSeedsPerThread = 4;  // group q sums each thread copies
 constexpr int kSpanBytes = 64;
+constexpr int kMaxSlices = 16;
+constexpr int kSlicePartials = 100;  // EPI of a sliced launch: wave chains to the scratch
 
 struct TokenShape {
   int rows, n, row_bytes, groups, m, parts, tiles_per_block, out_stride;
+  int slice_groups;  // groups per K slice (= groups when the grid has one slice)
 };
 
 // 2-bit field f of each byte of w, as an int8 code 0..2.
@@ -64,7 +74,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
                                                                      const uint8_t* __restrict__ packed,
                                                                      const uint16_t* __restrict__ scales,
                                                                      const float* __restrict__ bias,
-                                                                     float* __restrict__ output, TokenShape sh) {
+                                                                     float* __restrict__ output,
+                                                                     float* __restrict__ chains, TokenShape sh) {
   constexpr int UW = PART < kRing ? PART : kRing;
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x;
@@ -74,17 +85,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   const int m = sh.m;
   const int tile = blockIdx.x * sh.tiles_per_block + wave / sh.parts;
   const int part = wave % sh.parts;
-  const int span0 = part * PART;
+  const int span0 = part * PART;  // within the slice
   const int chunks = sh.n / kChunk;
-  // LDS: A operands [group][o][kb][m][16 B], then the negated group q sums
-  // [group][4*sq] (tokens 4*sq and up zero), then the wave partials
-  // [wave][16 tokens][16 rows], then a 16-byte dump slot for fill pieces past the end.
-  const int abytes = sh.groups * 128 * m;
+  const int sg = sh.slice_groups;
+  const int g_first = blockIdx.y * sg;  // the slice's first group
+  // LDS: A operands [group][o][kb][m][16 B] of the slice's groups, then their
+  // negated q sums [group][4*sq] (tokens 4*sq and up zero), then (one slice
+  // only) the wave partials [wave][16 tokens][16 rows], then a 16-byte dump
+  // slot for fill pieces past the end.
+  const int abytes = sg * 128 * m;
   const int sq = (m + 3) >> 2;
-  const int seeds = sh.groups * 4 * sq;
+  const int seeds = sg * 4 * sq;
   int* lseed = reinterpret_cast<int*>(lds + abytes);
   float* partial = reinterpret_cast<float*>(lds + abytes + 4 * seeds);
-  unsigned char* dump = lds + abytes + 4 * seeds + nthr / 64 * 1024;
+  unsigned char* dump = lds + abytes + 4 * seeds + (EPI == kSlicePartials ? 0 : nthr / 64 * 1024);
 
   // Token operand first (it is waited for before the weights), then the group
   // q sums, the scales and the first UW spans of weights.  Fill item p is q8
@@ -92,24 +106,25 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   // fields of one packed word W of a group); its fields (0, 1) and (2, 3) are
   // the halves W & 1 of the operands o = 0, 1 of lane group kb = 0, 0, 2, 2,
   // 1, 1, 3, 3 (W = 0..7).
-  const int quads = abytes / 16;  // m * 8 * groups
+  const int quads = abytes / 16;  // m * 8 * sg
   v4u fill[FILL];
 #pragma unroll
   for (int j = 0; j < FILL; ++j) {
     const int p = min(j * nthr + tid, quads - 1);
-    fill[j] = *reinterpret_cast<const v4u*>(q8 + (size_t)p * 16);
+    const int t = p / (8 * sg), quad = p - t * (8 * sg);
+    fill[j] = *reinterpret_cast<const v4u*>(q8 + ((size_t)t * 8 * sh.groups + 8 * g_first + quad) * 16);
   }
   int seed_value[kSeedsPerThread];
 #pragma unroll
   for (int j = 0; j < kSeedsPerThread; ++j) {
     const int p = min(j * nthr + tid, seeds - 1);
     const int g = p / (4 * sq), t = p % (4 * sq);
-    const int2 xs = *reinterpret_cast<const int2*>(xsum + (size_t)min(t, m - 1) * chunks + 2 * g);
+    const int2 xs = *reinterpret_cast<const int2*>(xsum + (size_t)min(t, m - 1) * chunks + 2 * (g_first + g));
     seed_value[j] = t < m ? -(xs.x + xs.y) : 0;
   }
   const int row = min(tile * 16 + c, sh.rows - 1);
-  const uint8_t* wrow = packed + (size_t)row * sh.row_bytes + (size_t)span0 * kSpanBytes + kb * 16;
-  const uint16_t* srow = scales + (size_t)row * sh.groups + span0 * 2;
+  const uint8_t* wrow = packed + (size_t)row * sh.row_bytes + (size_t)(g_first / 2 + span0) * kSpanBytes + kb * 16;
+  const uint16_t* srow = scales + (size_t)row * sh.groups + g_first + span0 * 2;
   unsigned sc[PART];  // the two fp16 group scales of each span
 #pragma unroll
   for (int i = 0; i < PART; i += 2) {
@@ -128,7 +143,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
 #pragma unroll
   for (int j = 0; j < FILL; ++j) {
     const int p = j * nthr + tid;
-    const int t = p / (8 * sh.groups), quad = p % (8 * sh.groups);
+    const int t = p / (8 * sg), quad = p % (8 * sg);
     const int g = quad >> 3, word = quad & 7;
     const int k = (0x33112200 >> (4 * word)) & 15;  // lane group of packed word `word`
     unsigned char* piece = lds + (((g * 2) * 4 + k) * m + t) * 16 + 8 * (word & 1);
@@ -182,6 +197,18 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  if constexpr (EPI == kSlicePartials) {
+    // Chain of lane (c, kb) for tokens 4kb + v of row c, to [slice * parts + part][token][row].
+    const int out_row = tile * 16 + c;
+    const int chain = blockIdx.y * sh.parts + part;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int t = 4 * kb + v;
+      if (t < m && out_row < sh.rows) chains[((size_t)chain * m + t) * sh.rows + out_row] = acc[v];
+    }
+    return;
+  }
+
   // Partials of lane (c, kb): tokens 4kb + v of row c.
 #pragma unroll
   for (int v = 0; v < 4; ++v) partial[(wave * 16 + 4 * kb + v) * 16 + c] = acc[v];
@@ -222,14 +249,47 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   }
 }
 
+// Finish of a sliced launch: output (token t, row r) = the `chains` fp32
+// chains of (t, r) added in chain order, times the token scale, plus the bias,
+// then the epilogue (a SiLU pair takes rows 2j and 2j + 1).  One thread per
+// output.
+template <int EPI>
+__global__ __launch_bounds__(256) void token_finish_kernel(const float* __restrict__ partials, int chains,
+                                                           const float* __restrict__ scale_in,
+                                                           const float* __restrict__ bias, float* __restrict__ output,
+                                                           int m, int rows, int out_stride) {
+  const int width = EPI == kSiluPair ? rows / 2 : rows;
+  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (o >= (long long)m * width) return;
+  const int t = (int)(o / width), j = (int)(o - (long long)t * width);
+  const size_t stride = (size_t)m * rows;
+  auto finish = [&](int r) {
+    const float* src = partials + (size_t)t * rows + r;
+    float total = src[0];
+    for (int c = 1; c < chains; ++c) total = total + src[c * stride];
+    float y = total * scale_in[t];
+    if (bias != nullptr) y = y + bias[r];
+    return y;
+  };
+  float* dst = output + (size_t)t * out_stride + j;
+  if constexpr (EPI == kSiluPair) {
+    const float gate = finish(2 * j);
+    *dst = ivo_silu(gate) * finish(2 * j + 1);
+  } else if constexpr (EPI == kResidual) {
+    *dst = *dst + finish(j);
+  } else {
+    *dst = finish(j);
+  }
+}
+
 constexpr int kPartSpans[] = {16, 14, 8, 4, 2, 1};
 
 template <int EPI, int PART>
-hipError_t launch_part(hipStream_t stream, const GemmArgs& a, const TokenShape& sh, int fill, int blocks, int threads,
-                       size_t lds) {
+hipError_t launch_part(hipStream_t stream, const GemmArgs& a, const TokenShape& sh, int fill, dim3 blocks, int threads,
+                       size_t lds, float* chains) {
   auto go = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), lds, stream, a.q8_in, a.xsum_in, a.scale_in, a.packed,
-                       a.scales, a.bias, a.output, sh);
+    hipLaunchKernelGGL(kernel, blocks, dim3(threads), lds, stream, a.q8_in, a.xsum_in, a.scale_in, a.packed,
+                       a.scales, a.bias, a.output, chains, sh);
     return hipGetLastError();
   };
   if (fill <= 2) return go(token_gemv_kernel<EPI, PART, 2>);
@@ -240,62 +300,98 @@ hipError_t launch_part(hipStream_t stream, const GemmArgs& a, const TokenShape& 
 }
 
 template <int EPI>
-hipError_t launch_epi(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan) {
-  TokenShape sh{a.rows, a.n, a.row_bytes, a.groups, a.m, plan.parts, plan.tiles_per_block, a.out_stride};
+hipError_t launch_epi(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan, float* chains) {
+  const int groups = a.n / kGroup;
+  TokenShape sh{a.rows, a.n, a.row_bytes, a.groups, a.m, plan.parts, plan.tiles_per_block, a.out_stride,
+                groups / plan.slices};
   const int threads = 64 * plan.parts * plan.tiles_per_block;
-  const int blocks = ceil_div(ceil_div(a.rows, 16), plan.tiles_per_block);
+  const dim3 blocks(ceil_div(ceil_div(a.rows, 16), plan.tiles_per_block), plan.slices);
   switch (plan.part_spans) {
-    case 16: return launch_part<EPI, 16>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
-    case 14: return launch_part<EPI, 14>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
-    case 8: return launch_part<EPI, 8>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
-    case 4: return launch_part<EPI, 4>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
-    case 2: return launch_part<EPI, 2>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
-    case 1: return launch_part<EPI, 1>(stream, a, sh, plan.fill, blocks, threads, plan.lds);
+    case 16: return launch_part<EPI, 16>(stream, a, sh, plan.fill, blocks, threads, plan.lds, chains);
+    case 14: return launch_part<EPI, 14>(stream, a, sh, plan.fill, blocks, threads, plan.lds, chains);
+    case 8: return launch_part<EPI, 8>(stream, a, sh, plan.fill, blocks, threads, plan.lds, chains);
+    case 4: return launch_part<EPI, 4>(stream, a, sh, plan.fill, blocks, threads, plan.lds, chains);
+    case 2: return launch_part<EPI, 2>(stream, a, sh, plan.fill, blocks, threads, plan.lds, chains);
+    case 1: return launch_part<EPI, 1>(stream, a, sh, plan.fill, blocks, threads, plan.lds, chains);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <int EPI>
+hipError_t launch_finish(hipStream_t stream, const GemmArgs& a, int chains, const float* partials) {
+  const int width = EPI == kSiluPair ? a.rows / 2 : a.rows;
+  const long long outputs = (long long)a.m * width;
+  if (outputs == 0) return hipSuccess;
+  hipLaunchKernelGGL(token_finish_kernel<EPI>, dim3((unsigned)((outputs + 255) / 256)), dim3(256), 0, stream,
+                     partials, chains, a.scale_in, a.bias, a.output, a.m, a.rows, a.out_stride);
+  return hipGetLastError();
 }
 
 }  // namespace
 
 TokenPlan token_gemv_plan(int m, int rows, int n, int cus, size_t max_lds) {
-  TokenPlan plan{0, 0, 0, 0, 0};
+  TokenPlan plan{0, 0, 0, 0, 0, 1};
   if (m < 1 || m > kMaxTokens || rows < 1 || n < 256 || n % 256 != 0) return plan;
-  const int spans = n / 256, groups = n / kGroup, tiles = ceil_div(rows, 16);
-  // Spans per wave: the longest range that still gives every CU eight waves,
-  // else the shortest available; at most 16 waves per row tile.
-  int part_spans = 0;
-  for (int candidate : kPartSpans) {
-    if (spans % candidate != 0 || spans / candidate > kMaxWaves) continue;
-    part_spans = candidate;
-    if ((long long)tiles * (spans / candidate) >= 8LL * cus) break;
+  const int spans = n / 256, tiles = ceil_div(rows, 16);
+  const int sq = (m + 3) / 4;
+  // The fewest K slices whose q8 bytes fit in LDS (one slice: the whole rows).
+  for (int slices = 1; slices <= kMaxSlices; ++slices) {
+    if (spans % slices != 0) continue;
+    const int slice_spans = spans / slices, slice_groups = 2 * slice_spans;
+    // Spans per wave: the longest range that still gives every CU eight
+    // waves, else the shortest available; at most 16 waves per row tile.
+    int part_spans = 0;
+    for (int candidate : kPartSpans) {
+      if (slice_spans % candidate != 0 || slice_spans / candidate > kMaxWaves) continue;
+      part_spans = candidate;
+      if ((long long)tiles * (slice_spans / candidate) * slices >= 8LL * cus) break;
+    }
+    if (part_spans == 0) continue;
+    const int parts = slice_spans / part_spans;
+    int tiles_per_block = ceil_div(tiles * slices, cus);
+    if (tiles_per_block > kMaxWaves / parts) tiles_per_block = kMaxWaves / parts;
+    if (tiles_per_block < 1) tiles_per_block = 1;
+    const int threads = 64 * parts * tiles_per_block;
+    const size_t abytes = (size_t)slice_groups * 128 * m;
+    const size_t seeds = (size_t)slice_groups * 4 * sq;
+    const size_t partials = slices == 1 ? (size_t)threads / 64 * 1024 : 0;
+    const size_t lds = abytes + 4 * seeds + partials + 16;
+    const int fill = (int)((abytes / 16 + threads - 1) / threads);
+    // (Sixteen fill pieces per thread on top of a 16-span ring would spill.)
+    if (lds > max_lds || fill > (part_spans == 16 ? 12 : 16) || seeds > (size_t)kSeedsPerThread * threads) continue;
+    if (slices > 1 && (long long)slices * parts * m * rows > kTokenPartialFloats) return plan;
+    plan.parts = parts;
+    plan.part_spans = part_spans;
+    plan.tiles_per_block = tiles_per_block;
+    plan.fill = fill;
+    plan.lds = lds;
+    plan.slices = slices;
+    return plan;
   }
-  if (part_spans == 0) return plan;
-  const int parts = spans / part_spans;
-  int tiles_per_block = ceil_div(tiles, cus);
-  if (tiles_per_block > kMaxWaves / parts) tiles_per_block = kMaxWaves / parts;
-  if (tiles_per_block < 1) tiles_per_block = 1;
-  const int threads = 64 * parts * tiles_per_block;
-  const size_t abytes = (size_t)groups * 128 * m;
-  const size_t seeds = (size_t)groups * 4 * ((m + 3) / 4);
-  const size_t lds = abytes + 4 * seeds + (size_t)threads / 64 * 1024 + 16;
-  const int fill = (int)((abytes / 16 + threads - 1) / threads);
-  // (Sixteen fill pieces per thread on top of a 16-span ring would spill.)
-  if (lds > max_lds || fill > (part_spans == 16 ? 12 : 16) || seeds > (size_t)kSeedsPerThread * threads) return plan;
-  plan.parts = parts;
-  plan.part_spans = part_spans;
-  plan.tiles_per_block = tiles_per_block;
-  plan.fill = fill;
-  plan.lds = lds;
   return plan;
 }
 
 hipError_t launch_token_gemv(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan) {
   if (plan.parts == 0) return hipErrorInvalidValue;
+  if (plan.slices == 1) {
+    switch (a.epi) {
+      case kStore: return launch_epi<kStore>(stream, a, plan, nullptr);
+      case kResidual: return launch_epi<kResidual>(stream, a, plan, nullptr);
+      case kSiluPair: return launch_epi<kSiluPair>(stream, a, plan, nullptr);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (a.epi != kStore && a.epi != kResidual && a.epi != kSiluPair) return hipErrorInvalidValue;
+  Scratch* work = nullptr;
+  hipError_t status = scratch_for_stream(stream, &work);
+  if (status != hipSuccess) return status;
+  status = launch_epi<kSlicePartials>(stream, a, plan, work->token_partials);
+  if (status != hipSuccess) return status;
+  const int chains = plan.parts * plan.slices;
   switch (a.epi) {
-    case kStore: return launch_epi<kStore>(stream, a, plan);
-    case kResidual: return launch_epi<kResidual>(stream, a, plan);
-    case kSiluPair: return launch_epi<kSiluPair>(stream, a, plan);
-    default: return hipErrorInvalidValue;
+    case kStore: return launch_finish<kStore>(stream, a, chains, work->token_partials);
+    case kResidual: return launch_finish<kResidual>(stream, a, chains, work->token_partials);
+    default: return launch_finish<kSiluPair>(stream, a, chains, work->token_partials);
   }
 }
 

@@ -27,7 +27,10 @@ struct Scratch {
   int32_t* xsum = nullptr;
   float* scale = nullptr;
   int capacity_chunks = 0;
+  float* token_partials = nullptr;  // fp32 wave partials of the K-sliced token GEMV
 };
+// Capacity of Scratch::token_partials (floats; 16 MB per device).
+constexpr long long kTokenPartialFloats = 4LL << 20;
 hipError_t scratch_for_stream(hipStream_t stream, Scratch** out);
 hipError_t init_device(int device);
 
@@ -126,11 +129,12 @@ hipError_t launch_skinny(hipStream_t stream, const GemmArgs& a, SkinnyPlan plan)
 // spans (its fp32 order, as the GEMM's splits); parts == 0 means it does not
 // apply.
 struct TokenPlan {
-  int parts;
+  int parts;  // waves per row tile within one K slice
   int part_spans;
   int tiles_per_block;
   int fill;
   size_t lds;
+  int slices;  // K slices (blocks along grid y); above 1 the wave partials go through the scratch
 };
 TokenPlan token_gemv_plan(int m, int rows, int n, int cus, size_t max_lds);
 hipError_t launch_token_gemv(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan);

@@ -5,7 +5,8 @@ Every output of every token is checked bit for bit against the oracle's split or
 plan, contiguous group ranges folded in order and added in order), and token 0 within rel 1e-5 / abs 1e-6
 of the fp64 truth.  Cases: the planner's span choices (1, 2, 4, 8, 14 and 16 spans per wave), ragged row
 counts, a bias, both epilogues with a padded output stride, token counts that are not a multiple of four
-(the last lane group's slots past M), and the fallback to the skinny kernel above the LDS budget."""
+(the last lane group's slots past M), and rows too long for the tokens' q8 bytes in LDS, where K is cut
+into 2, 4 or 8 slices across blocks and a second kernel adds the wave chains in order."""
 
 from __future__ import annotations
 
@@ -89,7 +90,28 @@ def test_token_gemv_stress_shape_sixteen_tokens(cuda, oracle):
     assert _case(oracle, cuda, 16, 8192, 28672, False, seed=5) == 2
 
 
-def test_token_gemv_falls_back_above_lds(cuda, oracle):
-    """16 tokens of 28672 inputs (448 KB of q8) do not fit: the skinny kernel runs, in its own split order."""
-    splits = _case(oracle, cuda, 16, 28672, 512, True, seed=6)
-    assert splits == 4
+# (m, k, rows, bias, K-splits = slices x waves per row tile): the tokens' whole q8 rows exceed the LDS budget.
+@pytest.mark.parametrize("m,k,rows,bias,splits", [
+    (16, 28672, 512, True, 56),    # 4 slices x 14 waves (448 KB of q8 in all)
+    (5, 28672, 1000, True, 28),    # 2 slices x 14
+    (12, 28672, 4100, False, 8),   # 4 slices x 2, ragged rows
+    (9, 20480, 3000, True, 20),    # 2 slices x 10
+    (3, 65536, 700, False, 32),    # 2 slices x 16
+    (16, 65536, 1024, False, 32),  # 8 slices x 4, sixteen fill pieces per thread
+    (13, 28672, 130, True, 56),    # fewer row tiles than blocks of one slice
+    (11, 28672, 8192, False, 8),   # 2 slices, LDS within 1 KB of the budget
+])
+def test_token_gemv_sliced(cuda, oracle, m, k, rows, bias, splits):
+    assert _case(oracle, cuda, m, k, rows, bias, seed=m * 7 + k + rows) == splits
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+def test_token_gemv_sliced_epilogues(cuda, oracle, epilogue):
+    assert _case(oracle, cuda, 16, 28672, 514, True, seed=61 if epilogue == "residual" else 62, epilogue=epilogue,
+                 pad=3) == 56
+
+
+def test_token_gemv_sliced_stress_shapes(cuda, oracle):
+    """K=28672 -> N=8192 with 8 and 16 tokens: two and four slices of two or four waves per row tile."""
+    assert _case(oracle, cuda, 8, 28672, 8192, False, seed=7) == 8
+    assert _case(oracle, cuda, 16, 28672, 8192, False, seed=8) == 8
