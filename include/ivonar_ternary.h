@@ -74,7 +74,12 @@ int ivonar_gemm_plan(int m, int rows, int n);
  * (eps, clip +-8, weight `aux`) first, ATTN merges split-softmax partials
  * [heads, splits, HEAD_DIM+2] first; prequant reads q8_in/xsum_in/scale_in.
  * Epilogue: store, residual (output[r] += y), silu pair (interleaved
- * gate/up rows; output[r/2] = silu(y[r]) * y[r+1], rows even). */
+ * gate/up rows; output[r/2] = silu(y[r]) * y[r+1], rows even).
+ * A row longer than 4096 inputs (PLAIN, NORM, ATTN) is quantized by a
+ * separate launch into the device scratch (see ivonar_init) and then read
+ * by the GEMV: concurrent such calls on one device, from different streams
+ * or from graphs replayed at once, race on it; calls in one stream order
+ * are safe. */
 #define IVONAR_GEMV_ARGS                                                                                    \
   const float *input, const float *aux, const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, \
       const uint8_t *packed, const uint16_t *scales, const float *bias, float *output, int rows, int n,      \
