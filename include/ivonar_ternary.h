@@ -39,12 +39,15 @@ extern "C" {
 
 /* ---------------------------------------------------------------- set-up */
 
-/* Allocates the per-device scratch: the activation row a GEMV quantizes when
+/* Allocates the device's scratch: the activation row a GEMV quantizes when
  * its rows are longer than the fused limit, and the 16 MB of fp32 wave
  * chains of a K-sliced token GEMM (1..16 tokens whose q8 rows exceed LDS).
- * Call once per device outside graph capture; replaces the reference's
- * compile_module set-up step (kernels/runtime.py:301-324).  Calls with the
- * device current. */
+ * Besides it, every stream (up to 32 per device) that makes such a call
+ * outside graph capture gets a scratch of its own on its first call, so
+ * eager calls on different streams never share one; a call under capture
+ * uses its stream's scratch if it has one, else the device's.  Call once per
+ * device outside graph capture; replaces the reference's compile_module
+ * set-up step (kernels/runtime.py:301-324).  Calls with the device current. */
 hipError_t ivonar_init(int device);
 
 /* Process-wide values the reference passes as -D defines to NVRTC
@@ -76,10 +79,10 @@ int ivonar_gemm_plan(int m, int rows, int n);
  * Epilogue: store, residual (output[r] += y), silu pair (interleaved
  * gate/up rows; output[r/2] = silu(y[r]) * y[r+1], rows even).
  * A row longer than 4096 inputs (PLAIN, NORM, ATTN) is quantized by a
- * separate launch into the device scratch (see ivonar_init) and then read
- * by the GEMV: concurrent such calls on one device, from different streams
- * or from graphs replayed at once, race on it; calls in one stream order
- * are safe. */
+ * separate launch into the stream's scratch (see ivonar_init) and then read
+ * by the GEMV: calls in one stream order are safe, and so are eager calls on
+ * different streams; graphs whose captured calls share a scratch (captured
+ * on one stream, or on streams that had none) race when replayed at once. */
 #define IVONAR_GEMV_ARGS                                                                                    \
   const float *input, const float *aux, const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, \
       const uint8_t *packed, const uint16_t *scales, const float *bias, float *output, int rows, int n,      \
@@ -156,8 +159,8 @@ hipError_t ivonar_quantize_rows(hipStream_t stream, int mode, const float* input
  * GEMM_ARGS of ternary.cu:671-674 (gemm_tile_* :767-784): m token rows of
  * pre-quantized activations against `rows` weight rows on int8 MFMA; output
  * row t at output + t*out_stride.  For 1..16 tokens with n a multiple of 256
- * whose q8 rows exceed LDS, the call is two launches sharing the device
- * scratch (see ivonar_init): concurrent such calls on one device race. */
+ * whose q8 rows exceed LDS, the call is two launches through the stream's
+ * scratch (see ivonar_init), with the same concurrency rule as the GEMV's. */
 #define IVONAR_GEMM_ARGS                                                                                      \
   const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, const uint8_t *packed,              \
       const uint16_t *scales, const float *bias, float *output, int rows, int n, int row_bytes, int groups, \

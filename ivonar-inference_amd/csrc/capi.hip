@@ -20,13 +20,23 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 constexpr int kScratchChunks = 16384;  // rows up to 1,048,576 inputs
+// Scratch per (device, stream): the device's own (set up by ivonar_init, used
+// by the null stream, by calls under graph capture on a stream that has none
+// yet, and past kMaxStreamScratch streams), and one per stream that calls
+// outside capture, so that eager calls on different streams never share one.
+constexpr int kMaxStreamScratch = 32;
+struct StreamScratch {
+  hipStream_t stream = nullptr;
+  Scratch scratch;
+};
 std::mutex g_scratch_lock;
 Scratch g_scratch[kMaxDevices];
+StreamScratch g_stream_scratch[kMaxDevices][kMaxStreamScratch];
+int g_stream_scratch_count[kMaxDevices] = {0};
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-hipError_t allocate_scratch(int device) {
-  Scratch& s = g_scratch[device];
+hipError_t allocate_scratch(Scratch& s) {
   if (s.q8 != nullptr) return hipSuccess;
   void* q8 = nullptr;
   void* xsum = nullptr;
@@ -67,13 +77,14 @@ hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, cons
   if (status != hipSuccess) return status;
   if (output == nullptr) return hipErrorInvalidValue;
   if (epi == kSiluPair && (rows & 1) != 0) return hipErrorInvalidValue;
+  const int head_dim = defines().head_dim;  // read once: checked and used with the same value
   if (prequant) {
     if (q8_in == nullptr || xsum_in == nullptr || scale_in == nullptr || !aligned16(q8_in))
       return hipErrorInvalidValue;
   } else {
     if (input == nullptr) return hipErrorInvalidValue;
     if (mode == kNorm && aux == nullptr) return hipErrorInvalidValue;
-    if (mode == kAttn && (splits <= 0 || n % defines().head_dim != 0)) return hipErrorInvalidValue;
+    if (mode == kAttn && (splits <= 0 || n % head_dim != 0)) return hipErrorInvalidValue;
   }
   GemvArgs a{};
   a.mode = mode;
@@ -95,7 +106,7 @@ hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, cons
   a.groups = groups;
   a.splits = splits > 0 ? splits : 1;
   a.eps = eps;
-  a.head_dim = defines().head_dim;
+  a.head_dim = head_dim;
   return launch_gemv(stream, a);
 }
 
@@ -139,10 +150,11 @@ hipError_t quant_entry(hipStream_t stream, int mode, const float* input, int in_
     return hipErrorInvalidValue;
   if (!aligned16(q8_out) || ((uintptr_t)xsum_out & 3u) != 0) return hipErrorInvalidValue;
   if (mode == kNorm && aux == nullptr) return hipErrorInvalidValue;
-  if (mode == kAttn && (splits <= 0 || n % defines().head_dim != 0)) return hipErrorInvalidValue;
+  const int head_dim = defines().head_dim;  // read once: checked and used with the same value
+  if (mode == kAttn && (splits <= 0 || n % head_dim != 0)) return hipErrorInvalidValue;
   if (mode < kPlain || mode > kAttn) return hipErrorInvalidValue;
   if (m > 1 && in_stride < (mode == kAttn ? 1 : n)) return hipErrorInvalidValue;
-  QuantArgs q{mode, input, in_stride, aux, n, eps, splits > 0 ? splits : 1, defines().head_dim, m,
+  QuantArgs q{mode, input, in_stride, aux, n, eps, splits > 0 ? splits : 1, head_dim, m,
               q8_out, xsum_out, scale_out};
   return launch_quantize(stream, q);
 }
@@ -174,7 +186,7 @@ hipError_t init_device(int device) {
     status = hipSetDevice(device);
     if (status != hipSuccess) return status;
   }
-  status = allocate_scratch(device);
+  status = allocate_scratch(g_scratch[device]);
   if (current != device) (void)hipSetDevice(current);
   return status;
 }
@@ -184,13 +196,32 @@ hipError_t scratch_for_stream(hipStream_t stream, Scratch** out) {
   hipError_t status = hipGetDevice(&device);
   if (status != hipSuccess) return status;
   if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  status = hipStreamIsCapturing(stream, &capture);
+  if (status != hipSuccess) return status;
+  const bool capturing = capture != hipStreamCaptureStatusNone;
   std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (stream != nullptr) {
+    StreamScratch* table = g_stream_scratch[device];
+    const int count = g_stream_scratch_count[device];
+    for (int i = 0; i < count; ++i) {
+      if (table[i].stream == stream) {
+        *out = &table[i].scratch;
+        return hipSuccess;
+      }
+    }
+    if (!capturing && count < kMaxStreamScratch) {
+      status = allocate_scratch(table[count].scratch);
+      if (status != hipSuccess) return status;
+      table[count].stream = stream;
+      g_stream_scratch_count[device] = count + 1;
+      *out = &table[count].scratch;
+      return hipSuccess;
+    }
+  }
   if (g_scratch[device].q8 == nullptr) {
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    status = hipStreamIsCapturing(stream, &capture);
-    if (status != hipSuccess) return status;
-    if (capture != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-    status = allocate_scratch(device);
+    if (capturing) return hipErrorStreamCaptureUnsupported;
+    status = allocate_scratch(g_scratch[device]);
     if (status != hipSuccess) return status;
   }
   *out = &g_scratch[device];

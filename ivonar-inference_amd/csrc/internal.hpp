@@ -4,20 +4,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace ivo {
 
 // Process-wide values the reference passes as compile-time defines
 // (kernel_decoder.py:215): HEAD_DIM for the ATTN prologue, TILE for the
 // token count of the quantize_tile_* entry points, MAX_CHUNKS (capacity of
 // the caller's q8 buffers, used only for argument checks), MAX_TOPK (largest
-// top-k of the sampler, ternary.cu:8).
+// top-k of the sampler, ternary.cu:8).  Atomic, so that ivonar_define on one
+// thread and a launch on another never race (a launch reads each value once).
 constexpr int kMaxTopK = 1024;
 constexpr int kMaxSampleVocab = 1 << 18;
 struct Defines {
-  int head_dim = 64;
-  int tile = 32;
-  int max_chunks = 70;
-  int max_topk = 256;
+  std::atomic<int> head_dim{64};
+  std::atomic<int> tile{32};
+  std::atomic<int> max_chunks{70};
+  std::atomic<int> max_topk{256};
 };
 Defines& defines();
 
