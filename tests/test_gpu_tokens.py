@@ -115,3 +115,55 @@ def test_token_gemv_sliced_stress_shapes(cuda, oracle):
     """K=28672 -> N=8192 with 8 and 16 tokens: two and four slices of two or four waves per row tile."""
     assert _case(oracle, cuda, 8, 28672, 8192, False, seed=7) == 8
     assert _case(oracle, cuda, 16, 28672, 8192, False, seed=8) == 8
+
+
+def test_token_gemv_graph_replays(cuda, oracle):
+    """One-slice and sliced token GEMVs captured in a HIP graph replay bit-identically to the eager calls,
+    with eager calls of the same kernels (on the default stream) between the replays."""
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(77)
+    cases = []
+    for m, k, rows in ((5, 4096, 1000), (16, 28672, 512)):
+        codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+        matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+        q8, xsum, sx = ops.quantize_rows(_t(rng.standard_normal((m, k)).astype(np.float32), cuda))
+        other = ops.quantize_rows(_t(rng.standard_normal((m, k)).astype(np.float32), cuda))
+        cases.append((matrix, (q8, xsum, sx), other, torch.empty((m, rows), dtype=torch.float32, device=cuda),
+                      torch.empty((m, rows), dtype=torch.float32, device=cuda)))
+    assert runtime.gemm_plan(16, 512, 28672) == 56
+
+    def step():
+        for matrix, (q8, xsum, sx), _, out, _ in cases:
+            ops.gemm(matrix, q8, xsum, sx, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    eager = [case[3].clone() for case in cases]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    other_expected = []
+    for matrix, _, (q8, xsum, sx), _, side in cases:
+        ops.gemm(matrix, q8, xsum, sx, out=side)
+    torch.cuda.synchronize()
+    other_expected = [case[4].clone() for case in cases]
+    for replay in range(4):
+        for case in cases:
+            case[3].zero_()
+            case[4].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        for matrix, _, (q8, xsum, sx), _, side in cases:  # eager work between and during the replays
+            ops.gemm(matrix, q8, xsum, sx, out=side)
+        torch.cuda.synchronize()
+        for i, case in enumerate(cases):
+            assert torch.equal(case[3], eager[i]), f"replay {replay}, case {i}"
+            assert torch.equal(case[4], other_expected[i]), f"eager call after replay {replay}, case {i}"
