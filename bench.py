@@ -805,13 +805,23 @@ def decoder_bytes(config) -> int:
 
 
 def cpu_model() -> str:
+    """The host CPU's model name with its family/model numbers and vector extensions (a virtualised host
+    may report only the brand)."""
+    fields: dict[str, str] = {}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" not in line:
+                if fields:
+                    break  # the first processor's block is enough
+                continue
+            key, value = (part.strip() for part in line.split(":", 1))
+            fields.setdefault(key, value)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    flags = set(fields.get("flags", "").split())
+    vector = [f for f in ("avx2", "avx512f", "avx512_vnni", "avx512_bf16") if f in flags]
+    return f"{name} (family {fields.get('cpu family', '?')}, model {fields.get('model', '?')}; {' '.join(vector) or 'no avx2'})"
 
 
 def physical_cores(allowed: set[int]) -> int:
