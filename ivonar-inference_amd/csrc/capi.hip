@@ -1,5 +1,5 @@
 // C-ABI entry points (declared in include/ivonar_ternary.h): argument checks,
-// process defines, the per-device scratch, and dispatch to the launchers.
+// process defines, the per-device and per-stream scratch, and dispatch to the launchers.
 #include <stdint.h>
 #include <string.h>
 

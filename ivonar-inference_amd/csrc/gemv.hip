@@ -27,7 +27,7 @@
 // fp32 input itself into LDS (the fused prologue of gemv_plain_*,
 // gemv_norm_*, gemv_attn_*), quad-planar (quad w of chunk u at int4 index
 // w*C + u), and each lane then keeps its chunks' quads in registers.  Longer
-// rows are quantized once by the quantizer into the device scratch, and
+// rows are quantized once by the quantizer into the stream's scratch, and
 // pre-quantized activations are read by each lane straight from global
 // memory: once for the whole kernel when a row needs at most two steps per
 // lane, else with every step's weights.  That path has no LDS and no
