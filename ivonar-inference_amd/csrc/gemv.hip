@@ -32,6 +32,14 @@
 // memory: once for the whole kernel when a row needs at most two steps per
 // lane, else with every step's weights.  That path has no LDS and no
 // barrier: the q8 row is small and stays in the caches for every block.
+//
+// Integer core.  The fused kernels take 8-bit dot products on q8 quads
+// (chunk_code_dot, 9 VALU per packed word).  Pre-quantized activations take
+// 4-bit dot products on nibble-split quads (chunk_split_dot, 7 VALU per
+// word): the quantizer writes the scratch row split, and a caller's q8 quads
+// are split as they are loaded (split_quad, once per quad and lane in
+// registers, once per block in the LDS copies).  Both return the same exact
+// int32 sums, so the fp32 order and the outputs do not depend on the form.
 #include <type_traits>
 
 #include "internal.hpp"
@@ -51,6 +59,7 @@ struct GemvShape {
   float eps;
   int lanes, lane_shift, iters;
   int exact;  // every lane's chunks exist (C is a multiple of lanes): no per-chunk masks
+  int split;  // the activations are nibble-split quads (the two-pass path's own scratch)
 };
 
 struct GemvPtrs {
@@ -103,7 +112,7 @@ __device__ __forceinline__ void load_step(Step<NJ>& st, const uint8_t* __restric
 // forms both rows' chunk sums (its own row's first), sends the partner's row
 // across the pair (one DPP swap) and adds the partner's sum for its own row:
 // the exact group partial P[own row, g].
-template <int EPI, int NJ, bool QREG, int LANES, bool EXACT, bool XNEG = false>
+template <int EPI, int NJ, bool QREG, int LANES, bool EXACT, bool XNEG = false, bool SPLIT = false>
 __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr)[QREG ? NJ : 1][4],
                                              const int (&xr)[QREG ? NJ : 1], const int4* __restrict__ lds_q,
                                              const int* __restrict__ lds_x, float& acc,
@@ -140,8 +149,9 @@ __device__ __forceinline__ void compute_step(const Step<NJ>& st, const int4 (&qr
     // independent fills it; computing the partner's sum first puts the own
     // row's dot products in the gap.  The order saves issue cycles only: the
     // result does not depend on it.
-    int d1 = chunk_code_dot(st.w[j][1], q0, q1, q2, q3, seed);
-    int d0 = chunk_code_dot(st.w[j][0], q0, q1, q2, q3, seed);
+    // SPLIT: the activations are nibble-split quads (4-bit dot products).
+    int d1 = SPLIT ? chunk_split_dot(st.w[j][1], q0, q1, q2, q3, seed) : chunk_code_dot(st.w[j][1], q0, q1, q2, q3, seed);
+    int d0 = SPLIT ? chunk_split_dot(st.w[j][0], q0, q1, q2, q3, seed) : chunk_code_dot(st.w[j][0], q0, q1, q2, q3, seed);
     if constexpr (!EXACT) {
       d0 = live ? d0 : 0;
       d1 = live ? d1 : 0;
@@ -175,6 +185,9 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   // from the block's LDS copy at every step.
   constexpr bool QREG = !ROLL;
   static_assert(!(FUSED && ROLL), "the fused prologue keeps q8 in registers");
+  // Pre-quantized activations take the 4-bit dot products: quads arrive split
+  // (sh.split, the two-pass path's scratch) or are split as they are loaded.
+  constexpr bool SPLIT = !FUSED;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ float slots[64];
   const int chunks = (sh.n + kChunk - 1) / kChunk;
@@ -242,6 +255,12 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
       for (int w = 0; w < 4; ++w) qr[j][w] = gq[u * 4 + w];
       xr[j] = in.xsum_in[u];
     }
+    if (!sh.split) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) qr[j][w] = split_quad(qr[j][w]);
+    }
   } else {
     // Rolling over a long row: the block copies the q8 row to LDS.  All of a
     // thread's loads go out before its LDS stores.
@@ -254,7 +273,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
 #pragma unroll
       for (int k = 0; k < kCopyBatch; ++k) {
         const int e = base + k * kBlock + threadIdx.x;
-        if (e < words) lds_q[(e & 3) * chunks + (e >> 2)] = v[k];
+        if (e < words) lds_q[(e & 3) * chunks + (e >> 2)] = sh.split ? v[k] : split_quad(v[k]);
       }
     }
     for (int u = threadIdx.x; u < chunks; u += kBlock) lds_x[u] = in.xsum_in[u];
@@ -303,7 +322,7 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
                                                                      it_next * rows_per_iter + slot * kRows, j_next,
                                                                      sub, chunks);
     }
-    compute_step<EPI, NJ, QREG, LANES, EXACT>(current, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
+    compute_step<EPI, NJ, QREG, LANES, EXACT, false, SPLIT>(current, qr, xr, lds_q, lds_x, acc, partials, sh, row0,
                                               QREG ? 0 : jb * NJ, sub, chunks);
     if (jb == blocks_per_row - 1) {
       finish(acc, row0, current.base);
@@ -376,7 +395,7 @@ struct RowStep {
 };
 
 // Pre-quantized rows of 3..8 steps (8193 <= K <= 32768 inputs), 64 lanes per
-// row, q8 row in LDS.  Every lane keeps all STEPS steps of its row pair in
+// row, activation row in LDS (nibble-split).  Every lane keeps all STEPS steps of its row pair in
 // flight (3*STEPS loads: 14 KB per wave at K=28672, 8 waves and 112 KB per
 // CU) instead of the rolling pipeline's one or two, and refills a step with
 // the same step of the wave's next row pair as soon as it is computed.
@@ -397,7 +416,7 @@ struct RowStep {
 // order, so a count that leaves only younger loads outstanding proves the
 // step complete; stores only make the waits longer.  (Compiled loads would
 // get compiler-placed waits, which at this depth drain every load in flight
-// at loop joins.)  The q8 copy's loads go out first and are waited for with
+// at loop joins.)  The activation copy's loads go out first and are waited for with
 // the first row pair's weights still in flight.  The build disassembles
 // these kernels and checks every VGPR access against the loads in flight
 // (asmcheck.py).  Lane layout and fp32 order are those of gemv_kernel
@@ -489,7 +508,10 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
 #pragma unroll
   for (int k = 0; k < kCopy; ++k) {
     const int e = k * kBlock + tid;
-    *reinterpret_cast<v4i32*>(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = qv[k];
+    // Caller q8 quads are split here, once per block (the scratch's arrive split).
+    const int4 quad = __builtin_bit_cast(int4, qv[k]);
+    const int4 stored = sh.split ? quad : split_quad(quad);
+    *(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = stored;
   }
   *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = -xv;  // minus the chunk sums
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -501,7 +523,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     view.w[0][0] = __builtin_bit_cast(uint4, step.w0);
     view.w[0][1] = __builtin_bit_cast(uint4, step.w1);
     view.s[0] = (uint16_t)step.s;
-    compute_step<EPI, 1, false, 64, EXACT, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0,
+    compute_step<EPI, 1, false, 64, EXACT, true, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0,
                                                  decltype(step_c)::value, sub, chunks);
   };
   auto epilogue = [&](float acc, int row0, int b_side, int base_side) {
@@ -700,6 +722,7 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   const int steps = ceil_div(chunks, lanes);
   // Dead lanes exist when the last step is partial (items never hold dead steps).
   sh.exact = chunks % lanes == 0;
+  sh.split = 0;
   const int cus = device_cus();
   const bool roll = !fused && steps > 2;  // the layouts launch_nj picks
   int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);
@@ -724,13 +747,16 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
     }
     if (chunks > scratch->capacity_chunks) return hipErrorInvalidValue;
     hipError_t status;
+    // The scratch row is the GEMV's alone: the quantizer writes it nibble-split for the 4-bit dots.
+    const bool split = true;
     QuantArgs q{a.mode, a.input, a.n, a.aux, a.n, a.eps, a.splits, a.head_dim, 1, scratch->q8, scratch->xsum,
-                scratch->scale};
+                scratch->scale, split};
     status = launch_quantize(stream, q);
     if (status != hipSuccess) return status;
     a.q8_in = scratch->q8;
     a.xsum_in = scratch->xsum;
     a.scale_in = scratch->scale;
+    sh.split = split;
   }
   const GemvPtrs p{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in};
   switch (a.epi) {

@@ -50,6 +50,9 @@ struct QuantArgs {
   int8_t* q8;
   int32_t* xsum;
   float* scale;
+  // Write each quad in the nibble-split form the 4-bit GEMV reads (split_quad_word)
+  // instead of q8 bytes; the chunk sums and the scale are the same.
+  bool split = false;
 };
 hipError_t launch_quantize(hipStream_t stream, const QuantArgs& a);
 

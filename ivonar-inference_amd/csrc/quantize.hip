@@ -32,9 +32,10 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(QuantArgs a) {
   int value = 0;
   if (u < chunks) value = quantize_word<MODE>(src, u, (word >> 2) & 3, word & 3, inv_rms, scale);
   const int total = chunk_lane_sum(word_sum(value));
+  const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // lane ^ 2
   if (u < chunks) {
     int32_t* q8 = reinterpret_cast<int32_t*>(a.q8 + (size_t)t * chunks * kChunk);
-    q8[u * 16 + (word & 15)] = value;
+    q8[u * 16 + (word & 15)] = a.split ? (int)split_quad_word((unsigned)value, partner, word & 3) : value;
     if ((word & 15) == 0) a.xsum[(size_t)t * chunks + u] = total;
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) a.scale[t] = scale;
@@ -88,9 +89,10 @@ __global__ __launch_bounds__(T) void quantize_plain_kernel(QuantArgs a) {
   }
   const int value = (int)word;
   const int total = chunk_lane_sum(word_sum(value));
+  const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // lane ^ 2
   if (u < chunks) {
     int32_t* q8 = reinterpret_cast<int32_t*>(a.q8 + (size_t)t * chunks * kChunk);
-    q8[u * 16 + (tid & 15)] = value;
+    q8[u * 16 + (tid & 15)] = a.split ? (int)split_quad_word(word, partner, tid & 3) : value;
     if ((tid & 15) == 0) a.xsum[(size_t)t * chunks + u] = total;
   }
   if (blockIdx.x == 0 && tid == 0) a.scale[t] = scale;

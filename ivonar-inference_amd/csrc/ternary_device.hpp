@@ -97,6 +97,72 @@ __device__ __forceinline__ int sdot4_zero(unsigned a, int b) {
   return d;
 }
 
+// Nibble-split activations for 4-bit dot products.  A packed word W holds 16
+// codes, input 4b + f of its 16 in field f of byte b; W & 0x33333333 keeps
+// fields 0 and 2 of every byte as the nibbles 2b and 2b + 1, and
+// (W >> 2) & 0x33333333 fields 1 and 3.  The matching activation words split
+// each q into q = 16 * hi + lo (hi = q >> 4 in -8..7, lo = q & 15): word 0 of a
+// split quad holds hi of inputs 4b and 4b + 2 as nibbles 2b and 2b + 1, word 1
+// hi of inputs 4b + 1 and 4b + 3, words 2 and 3 the lo nibbles likewise.  In q8
+// terms (word k of a quad holds input 4b + k at byte b), word 0 = hi nibbles of
+// q8 words 0 and 2, word 1 = of words 1 and 3, words 2 and 3 the lo nibbles:
+// word k of the split quad, from q8 word k and the word of lane k ^ 2.
+__device__ __forceinline__ unsigned split_quad_word(unsigned own, unsigned partner, int k) {
+  const unsigned a = k < 2 ? own : partner;  // q8 word 0 or 1 (inputs 4b + 0 or 1)
+  const unsigned b = k < 2 ? partner : own;  // q8 word 2 or 3 (inputs 4b + 2 or 3)
+  return k < 2 ? ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u) : (a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u);
+}
+
+// The split form of a whole q8 quad (words 0..3), as split_quad_word gives it
+// word by word.
+__device__ __forceinline__ int4 split_quad(int4 q) {
+  const unsigned w0 = (unsigned)q.x, w1 = (unsigned)q.y, w2 = (unsigned)q.z, w3 = (unsigned)q.w;
+  return make_int4((int)(((w0 >> 4) & 0x0F0F0F0Fu) | (w2 & 0xF0F0F0F0u)),
+                   (int)(((w1 >> 4) & 0x0F0F0F0Fu) | (w3 & 0xF0F0F0F0u)),
+                   (int)((w0 & 0x0F0F0F0Fu) | ((w2 << 4) & 0xF0F0F0F0u)),
+                   (int)((w1 & 0x0F0F0F0Fu) | ((w3 << 4) & 0xF0F0F0F0u)));
+}
+
+// v_dot8_i32_i4 seeded from zero and v_dot8_u32_u4 in its three-operand form.
+__device__ __forceinline__ int sdot8_zero(unsigned a, unsigned b) {
+  int d;
+  asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ __forceinline__ unsigned udot8_seed(unsigned a, unsigned b, unsigned c) {
+  unsigned d;
+  asm("v_dot8_u32_u4 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+// Sum over one 64-input chunk of code * q plus acc, times 16, from the
+// nibble-split activations (the value chunk_code_dot returns for the q8 form):
+// per packed word two masks and a shift with the four 4-bit dot products, 7
+// VALU against chunk_code_dot's 9.  The hi products (signed nibbles) and lo
+// products (unsigned, seeded with acc) run in two accumulators; two
+// shift-adds give 16 * (16 * sum(code * hi) + sum(code * lo) + acc), exact in
+// int32 (the lo accumulator in unsigned arithmetic, modulo 2^32).
+__device__ __forceinline__ int chunk_split_dot(const uint4 w, const int4 s0, const int4 s1, const int4 s2,
+                                               const int4 s3, int acc) {
+  const unsigned words[4] = {w.x, w.y, w.z, w.w};
+  const int4 quads[4] = {s0, s1, s2, s3};
+  int hi = 0;
+  unsigned lo = (unsigned)acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned n0 = words[i] & 0x33333333u, n1 = (words[i] >> 2) & 0x33333333u;
+    if (i == 0) {
+      hi = sdot8_zero(n0, (unsigned)quads[i].x);
+      lo = udot8_seed(n0, (unsigned)quads[i].z, lo);
+    } else {
+      hi = __builtin_amdgcn_sdot8((int)n0, quads[i].x, hi, false);
+      lo = __builtin_amdgcn_udot8(n0, (unsigned)quads[i].z, lo, false);
+    }
+    hi = __builtin_amdgcn_sdot8((int)n1, quads[i].y, hi, false);
+    lo = __builtin_amdgcn_udot8(n1, (unsigned)quads[i].w, lo, false);
+  }
+  return (int)(((unsigned)hi << 8) + (lo << 4));
+}
+
 __device__ __forceinline__ int chunk_code_dot(const uint4 w, const int4 q0, const int4 q1, const int4 q2,
                                               const int4 q3, int acc) {
   int a1 = sdot4_seed(w.x & 0x03030303u, q0.x, acc);

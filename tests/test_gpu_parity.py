@@ -171,7 +171,7 @@ def test_gemv_plain_store_model_shapes(cuda, oracle, rows, k):
     _check_gemv_store(cuda, oracle, rows, k, bias=False)
 
 
-@pytest.mark.parametrize("k", [24, 1024, 4096, 5000, 8192, 8200, 28672])
+@pytest.mark.parametrize("k", [24, 1024, 4096, 5000, 8192, 8200, 28672, 40000, 49152])
 def test_gemv_residual_and_silu_pair(cuda, oracle, k):
     import torch
     from ivonar_amd import ops, runtime
@@ -200,7 +200,7 @@ def test_gemv_residual_and_silu_pair(cuda, oracle, k):
     assert_within(to_np(half), ref, rtol=1e-5, atol=1e-6, what="silu pair vs reference order")
 
 
-@pytest.mark.parametrize("k", [96, 1024, 4100, 8192, 8193])
+@pytest.mark.parametrize("k", [96, 1024, 4100, 8192, 8193, 40000])
 def test_gemv_norm_store_and_prequant(cuda, oracle, k):
     import torch
     from ivonar_amd import ops, runtime
@@ -228,7 +228,7 @@ def test_gemv_norm_store_and_prequant(cuda, oracle, k):
     assert_bits_equal(head, expected, "prequant")
 
 
-@pytest.mark.parametrize("head_dim,heads,splits", [(4, 4, 4), (64, 16, 4)])
+@pytest.mark.parametrize("head_dim,heads,splits", [(4, 4, 4), (64, 16, 4), (64, 80, 2)])
 def test_gemv_attn_residual(cuda, oracle, head_dim, heads, splits):
     from ivonar_amd import ops, runtime
 
