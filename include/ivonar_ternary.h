@@ -47,7 +47,9 @@ extern "C" {
  * eager calls on different streams never share one; a call under capture
  * uses its stream's scratch if it has one, else the device's.  Call once per
  * device outside graph capture; replaces the reference's compile_module
- * set-up step (kernels/runtime.py:301-324).  Calls with the device current. */
+ * set-up step (kernels/runtime.py:301-324).  Calls with the device current.
+ * Calling it again clears the GEMV's launch counters of every scratch of the
+ * device (see the decode GEMV below), with no call of the device in flight. */
 hipError_t ivonar_init(int device);
 
 /* Process-wide values the reference passes as -D defines to NVRTC
@@ -78,11 +80,16 @@ int ivonar_gemm_plan(int m, int rows, int n);
  * [heads, splits, HEAD_DIM+2] first; prequant reads q8_in/xsum_in/scale_in.
  * Epilogue: store, residual (output[r] += y), silu pair (interleaved
  * gate/up rows; output[r/2] = silu(y[r]) * y[r+1], rows even).
- * A row longer than 4096 inputs (PLAIN, NORM, ATTN) is quantized by a
- * separate launch into the stream's scratch (see ivonar_init) and then read
- * by the GEMV: calls in one stream order are safe, and so are eager calls on
- * different streams; graphs whose captured calls share a scratch (captured
- * on one stream, or on streams that had none) race when replayed at once. */
+ * A row longer than 4096 inputs is quantized into the stream's scratch (see
+ * ivonar_init) and then read by the GEMV: a 16-byte aligned PLAIN row of up
+ * to 32768 inputs by the first blocks of the GEMV launch itself (the other
+ * blocks wait for it through counters in the scratch that every launch
+ * leaves at zero), other rows by a separate quantizer launch.  Calls in one
+ * stream order are safe, and so are eager calls on different streams; graphs
+ * whose captured calls share a scratch (captured on one stream, or on
+ * streams that had none) race when replayed at once: their outputs are
+ * undefined, a launch may wait up to about a second (its outputs then NaN),
+ * and the counters can be left set, which ivonar_init clears. */
 #define IVONAR_GEMV_ARGS                                                                                    \
   const float *input, const float *aux, const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, \
       const uint8_t *packed, const uint16_t *scales, const float *bias, float *output, int rows, int n,      \

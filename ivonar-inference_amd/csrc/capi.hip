@@ -42,19 +42,25 @@ hipError_t allocate_scratch(Scratch& s) {
   void* xsum = nullptr;
   void* scale = nullptr;
   void* partials = nullptr;
+  void* sync = nullptr;
   hipError_t status = hipMalloc(&q8, (size_t)kScratchChunks * kChunk);
   if (status == hipSuccess) status = hipMalloc(&xsum, (size_t)kScratchChunks * sizeof(int32_t));
   if (status == hipSuccess) status = hipMalloc(&scale, 256);
   if (status == hipSuccess) status = hipMalloc(&partials, (size_t)kTokenPartialFloats * sizeof(float));
+  if (status == hipSuccess) status = hipMalloc(&sync, kSyncBytes);
+  if (status == hipSuccess) status = hipMemset(sync, 0, kSyncBytes);  // the GEMV's counters start at zero
   if (status != hipSuccess) {
     if (q8) (void)hipFree(q8);
     if (xsum) (void)hipFree(xsum);
     if (scale) (void)hipFree(scale);
+    if (partials) (void)hipFree(partials);
+    if (sync) (void)hipFree(sync);
     return status;
   }
   s.q8 = static_cast<int8_t*>(q8);
   s.xsum = static_cast<int32_t*>(xsum);
   s.scale = static_cast<float*>(scale);
+  s.sync = static_cast<unsigned*>(sync);
   s.token_partials = static_cast<float*>(partials);
   s.capacity_chunks = kScratchChunks;
   return hipSuccess;
@@ -113,12 +119,15 @@ hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, cons
 // ------------------------------------------------ no-allocation GEMV scratch
 // Rows longer than the fused limit are quantized before the GEMV; the
 // no-allocation entry point quantizes them into this array (q8, chunk sums,
-// token scale) instead of the scratch the library allocates.  Each device
+// token scale) instead of the scratch the library allocates, always in a
+// launch of its own (no counters: nothing in the array must start at zero).
+// Each device
 // holds its own copy at its own address, looked up once per device with
 // hipGetSymbolAddress; host code uses only that address.
 constexpr int kStaticChunks = 512;  // rows up to 32768 inputs
 constexpr size_t kStaticQ8Bytes = (size_t)kStaticChunks * kChunk;
-constexpr size_t kStaticBytes = kStaticQ8Bytes + (size_t)kStaticChunks * sizeof(int32_t) + 256;
+constexpr size_t kStaticScaleOffset = kStaticQ8Bytes + (size_t)kStaticChunks * sizeof(int32_t);
+constexpr size_t kStaticBytes = kStaticScaleOffset + 256;
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 std::mutex g_static_lock;
 Scratch g_static[kMaxDevices];
@@ -136,7 +145,8 @@ hipError_t static_scratch(Scratch** out) {
     if (status != hipSuccess) return status;
     unsigned char* bytes = static_cast<unsigned char*>(base);
     s.xsum = reinterpret_cast<int32_t*>(bytes + kStaticQ8Bytes);
-    s.scale = reinterpret_cast<float*>(bytes + kStaticQ8Bytes + (size_t)kStaticChunks * sizeof(int32_t));
+    s.scale = reinterpret_cast<float*>(bytes + kStaticScaleOffset);
+    s.sync = nullptr;  // the quantizer runs in a launch of its own
     s.capacity_chunks = kStaticChunks;
     s.q8 = reinterpret_cast<int8_t*>(bytes);
   }
@@ -187,6 +197,11 @@ hipError_t init_device(int device) {
     if (status != hipSuccess) return status;
   }
   status = allocate_scratch(g_scratch[device]);
+  // The in-launch quantizer's counters are zero between launches; clearing them
+  // here recovers a scratch that overlapping launches left set.
+  if (status == hipSuccess) status = hipMemset(g_scratch[device].sync, 0, kSyncBytes);
+  for (int i = 0; status == hipSuccess && i < g_stream_scratch_count[device]; ++i)
+    status = hipMemset(g_stream_scratch[device][i].scratch.sync, 0, kSyncBytes);
   if (current != device) (void)hipSetDevice(current);
   return status;
 }

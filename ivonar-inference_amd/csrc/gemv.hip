@@ -27,11 +27,14 @@
 // fp32 input itself into LDS (the fused prologue of gemv_plain_*,
 // gemv_norm_*, gemv_attn_*), quad-planar (quad w of chunk u at int4 index
 // w*C + u), and each lane then keeps its chunks' quads in registers.  Longer
-// rows are quantized once by the quantizer into the stream's scratch, and
-// pre-quantized activations are read by each lane straight from global
-// memory: once for the whole kernel when a row needs at most two steps per
-// lane, else with every step's weights.  That path has no LDS and no
-// barrier: the q8 row is small and stays in the caches for every block.
+// rows are quantized once into the stream's scratch: PLAIN rows (16-byte
+// aligned) of 4097..32768 inputs by the first blocks of the long-row GEMV
+// launch itself while the other blocks load their first weights
+// (quantize_publish / wait_published), other rows by the quantizer in a launch
+// of its own.  Pre-quantized activations are read by each lane straight from
+// global memory when a row needs at most two steps per lane (no LDS: the q8
+// row is small and stays in the caches for every block), else copied to LDS
+// once per block.
 //
 // Integer core.  The fused kernels take 8-bit dot products on q8 quads
 // (chunk_code_dot, 9 VALU per packed word).  Pre-quantized activations take
@@ -60,6 +63,8 @@ struct GemvShape {
   int lanes, lane_shift, iters;
   int exact;  // every lane's chunks exist (C is a multiple of lanes): no per-chunk masks
   int split;  // the activations are nibble-split quads (the two-pass path's own scratch)
+  int qblocks;  // > 0: qblocks blocks quantize the PLAIN row into q8_out first (in-launch quantizer)
+  int qstride;  // those blocks: 0, qstride, 2*qstride, ... (slice blockIdx / qstride)
 };
 
 struct GemvPtrs {
@@ -68,6 +73,12 @@ struct GemvPtrs {
   const int8_t* q8_in;
   const int32_t* xsum_in;
   const float* scale_in;
+  // In-launch quantizer (qblocks > 0): where the row goes (q8_in, xsum_in and
+  // scale_in point at the same buffers) and the scratch's counters and flags.
+  int8_t* q8_out;
+  int32_t* xsum_out;
+  float* scale_out;
+  unsigned* sync;
 };
 
 // One pipeline item's loads: weights of NJ steps for kRows rows (w[j][0] of
@@ -356,6 +367,17 @@ __device__ __forceinline__ int load_u16(const void* p) {
   asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
   return r;
 }
+// Device-coherent (sc1) forms, for the row the launch publishes itself.
+__device__ __forceinline__ v4i32 load_b128_sc1(const void* p) {
+  v4i32 r;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+__device__ __forceinline__ int load_b32_sc1(const void* p) {
+  int r;
+  asm volatile("global_load_dword %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
 // The same loads at a constant byte offset (-4096..4095) from p.
 template <int OFF>
 __device__ __forceinline__ v4i32 load_b128_at(const void* p) {
@@ -372,6 +394,108 @@ __device__ __forceinline__ int load_u16_at(const void* p) {
   return r;
 }
 
+// In-launch quantization of a PLAIN row of 4097..32768 inputs (the long-row
+// kernel, gemv_rows_kernel<..., QUANT = true>).  Blocks
+// s*qstride (s < Q = qblocks, at most 16) each quantize slice s of the row into
+// the scratch (nibble-split) and count themselves into `arrive`; the block
+// whose count is the last raises the ready flag of each of 8 block groups.
+// Each block's first thread waits for its group's flag (blockIdx & 7) and the
+// block barrier hands the row to its other threads.
+//
+// Visibility without cache maintenance: every store and load of the
+// published row, of the counters and of the flags is device-coherent (an
+// agent-scope relaxed atomic, or a load or store with the sc1 bit): such an
+// access is performed at the device's coherence point, past the per-XCD L2s,
+// so no write-back (buffer_wbl2) or invalidation (buffer_inv) is needed -
+// both serialize per XCD and cost microseconds when a thousand blocks issue
+// them.  Order comes from completion: a quantizing block waits until all its
+// stores are acknowledged (vmcnt(0) in every thread, then the barrier) before
+// it counts itself, the last block raises the flags after its count has
+// returned, and a waiting block issues its row loads only after it has read
+// its flag.
+//
+// The quantizing blocks have the lowest block numbers of their stride class
+// (at most 8*15), so they are dispatched ahead of the blocks that wait behind
+// them, and they themselves wait only for one another.  The host picks a
+// stride of 8 for large grids: blocks are spread over the XCDs round-robin,
+// so all quantizing blocks then run on the XCD that starts the launch first
+// and share its L2 copy of the fp32 row (the XCDs start a launch up to about
+// 4 us apart).  Eight flags in eight cache lines spread the polling of up to
+// 512 waiting blocks (two per CU).
+//
+// At its end every block counts itself into its group's `done` counter; the
+// block that completes a group counts the group into `top`, and the block
+// that completes `top` sets every counter and flag back to zero, so every
+// launch starts from zero without a memset.  A block counts itself done only
+// after it has passed its wait, and every quantizing block has counted into
+// `arrive` before that, so nothing is counted or raised after the reset.  The
+// wait is bounded (kPublishSpins polls, about a second): a wait that gives up
+// makes the block's outputs NaN instead of hanging the launch.  Two launches
+// that share one scratch must not overlap (stream order or one scratch per
+// stream).
+constexpr int kPublishSpins = 1 << 20;
+constexpr int kSyncGroups = 8;
+constexpr int kSyncLineWords = 32;  // one counter or flag per 128-byte line
+constexpr int kArriveLine = 0, kReadyLine = 1, kDoneLine = 1 + kSyncGroups, kTopLine = 1 + 2 * kSyncGroups;
+static_assert((kTopLine + 1) * kSyncLineWords * 4 <= kSyncBytes, "the scratch's counter region holds every line");
+
+__device__ __forceinline__ unsigned* sync_line(unsigned* sync, int line) { return sync + line * kSyncLineWords; }
+
+__device__ __forceinline__ bool quantizes(const GemvShape& sh) {
+  return sh.qblocks > 0 && (int)blockIdx.x % sh.qstride == 0 && (int)blockIdx.x / sh.qstride < sh.qblocks;
+}
+
+// Rows of up to ROUNDS*T*4 inputs take one load round for the row amax.
+template <int T, int ROUNDS>
+__device__ __forceinline__ void quantize_publish(const GemvPtrs& in, const GemvShape& sh, float* slots) {
+  quantize_plain_slice<T, ROUNDS, true>(in.input, sh.n, (int)blockIdx.x / sh.qstride, true, in.q8_out, in.xsum_out,
+                                        in.scale_out, slots);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are performed device-wide
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned before =
+        __hip_atomic_fetch_add(sync_line(in.sync, kArriveLine), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == (unsigned)sh.qblocks - 1) {
+      for (int j = 0; j < kSyncGroups; ++j)
+        __hip_atomic_store(sync_line(in.sync, kReadyLine + j), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// All threads of the block call it; true when the row is published.
+__device__ __forceinline__ bool wait_published(const GemvPtrs& in, int* status) {
+  if (threadIdx.x == 0) {
+    const unsigned* ready = sync_line(in.sync, kReadyLine + (int)(blockIdx.x & (kSyncGroups - 1)));
+    int ok = 1;
+    for (int spins = 0; __hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++spins) {
+      if (spins == kPublishSpins) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    *status = ok;
+  }
+  __syncthreads();
+  return *status != 0;
+}
+
+// Called by every thread at the end of the block (after its wait).
+__device__ __forceinline__ void retire_block(const GemvPtrs& in) {
+  if (threadIdx.x != 0) return;
+  const unsigned group = blockIdx.x & (kSyncGroups - 1);
+  const unsigned members = (gridDim.x - group + kSyncGroups - 1) / kSyncGroups;
+  const unsigned groups = gridDim.x < (unsigned)kSyncGroups ? gridDim.x : (unsigned)kSyncGroups;
+  if (__hip_atomic_fetch_add(sync_line(in.sync, kDoneLine + (int)group), 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) != members - 1)
+    return;
+  if (__hip_atomic_fetch_add(sync_line(in.sync, kTopLine), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+      groups - 1)
+    return;
+  for (int line = 0; line <= kTopLine; ++line)
+    __hip_atomic_store(sync_line(in.sync, line), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): an
 // unrolled loop whose index can feed an immediate operand.
 template <int N, int I = 0, typename F>
@@ -385,6 +509,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Byte offset of gemv_rows_kernel's 16-byte dump slot: past the q8 row and
 // its chunk sums, 16-byte aligned.
 __host__ __device__ constexpr int rows_dump_offset(int chunks) { return (chunks * (kChunk + 4) + 15) & ~15; }
+constexpr int kRowsQuantLds = 64;  // QUANT, after the dump slot: 8 block max slots and the wait status
+constexpr int kRowsBlocksPerCu2 = 2;  // QUANT with two steps per row
 
 // One step of a row pair in flight: the 16 weight bytes of the lane's chunk in
 // its own row (w0) and in its partner's row (w1), and the group scale of the
@@ -417,11 +543,14 @@ struct RowStep {
 // step complete; stores only make the waits longer.  (Compiled loads would
 // get compiler-placed waits, which at this depth drain every load in flight
 // at loop joins.)  The activation copy's loads go out first and are waited for with
-// the first row pair's weights still in flight.  The build disassembles
+// the first row pair's weights still in flight; with QUANT (the launch
+// quantizes the row itself) they go out after the first weights, once the row
+// is published, device-coherent, and are waited for with vmcnt(0).  The build
+// disassembles
 // these kernels and checks every VGPR access against the loads in flight
 // (asmcheck.py).  Lane layout and fp32 order are those of gemv_kernel
 // (orc_gemv_pairs).
-template <int EPI, int STEPS, bool EXACT>
+template <int EPI, int STEPS, bool EXACT, bool QUANT>
 __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
                                                         const float* __restrict__ bias, float* __restrict__ output,
@@ -439,7 +568,9 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   const int waves = gridDim.x * (kBlock / 64);
   const int words = chunks * 4;
   constexpr bool kScales = EPI != kPartials;  // the partials export passes no scales
-  const float sx = kScales ? *in.scale_in : 1.0f;
+  static_assert(!(QUANT && EPI == kPartials), "the partials export reads a pre-quantized row");
+  float sx = 1.0f;
+  if constexpr (!QUANT) sx = kScales ? *in.scale_in : 1.0f;
 
   // Loads that a layout does not need still go out, from the first bytes of
   // the packed matrix (the one operand every entry point passes), so that the
@@ -491,19 +622,43 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   };
 
   v4i32 qv[kCopy];
-#pragma unroll
-  for (int k = 0; k < kCopy; ++k) qv[k] = load_b128(gq + min(k * kBlock + tid, words - 1));
-  int xv = load_b32(in.xsum_in + min(tid, chunks - 1));
-
+  int xv;
   RowStep st[STEPS];
-  int it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));  // wave-uniform
-  PairBase pb = pair_base(it);
-  static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
-
-  asm volatile("s_waitcnt vmcnt(%5)"
-               : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv)
-               : "n"(3 * STEPS)
-               : "memory");
+  int it;
+  PairBase pb;
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (int k = 0; k < kCopy; ++k) qv[k] = load_b128(gq + min(k * kBlock + tid, words - 1));
+    xv = load_b32(in.xsum_in + min(tid, chunks - 1));
+    it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));  // wave-uniform
+    pb = pair_base(it);
+    static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
+    asm volatile("s_waitcnt vmcnt(%5)"
+                 : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv)
+                 : "n"(3 * STEPS)
+                 : "memory");
+  } else {
+    // The quantizing blocks publish their slices first; every block issues its
+    // first row pair's weights, waits for the row and then copies it
+    // (device-coherent loads: q8, chunk sums and the token scale).
+    float* slots = reinterpret_cast<float*>(lds_raw + rows_dump_offset(chunks) + 16);
+    int* published = reinterpret_cast<int*>(slots + kBlock / 64);
+    // Rows of STEPS*4096 inputs: 2*STEPS float4 of the row amax per thread, one round.
+    if (quantizes(sh)) quantize_publish<kBlock, 2 * STEPS>(in, sh, slots);
+    it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));
+    pb = pair_base(it);
+    static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
+    const bool ok = wait_published(in, published);
+#pragma unroll
+    for (int k = 0; k < kCopy; ++k) qv[k] = load_b128_sc1(gq + min(k * kBlock + tid, words - 1));
+    xv = load_b32_sc1(in.xsum_in + min(tid, chunks - 1));
+    int sv = load_b32_sc1(in.scale_in);
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv), "+v"(sv)
+                 :
+                 : "memory");
+    sx = ok ? __int_as_float(sv) : __builtin_nanf("");
+  }
   int4* dump = reinterpret_cast<int4*>(lds_raw + rows_dump_offset(chunks));
 #pragma unroll
   for (int k = 0; k < kCopy; ++k) {
@@ -582,6 +737,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     epilogue(acc, row0, b_side, base_side);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // a wave with no row pair still has its first loads out
+  if constexpr (QUANT) retire_block(in);
 }
 
 template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
@@ -610,19 +766,36 @@ bool launch_layout(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, con
   return false;
 }
 
+template <int EPI, int STEPS, bool QUANT>
+void launch_rows_as(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
+                    size_t lds) {
+  if (sh.exact)
+    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, true, QUANT>), dim3(blocks), dim3(512), lds, stream, p, a.packed,
+                       a.scales, a.bias, a.output, a.partials, sh);
+  else
+    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, false, QUANT>), dim3(blocks), dim3(512), lds, stream, p,
+                       a.packed, a.scales, a.bias, a.output, a.partials, sh);
+}
+
 template <int EPI, int STEPS>
 void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int /*blocks*/,
                  size_t /*lds*/) {
-  size_t lds;
   const int cus = device_cus();
-  const int blocks = ceil_div(sh.iters, 8) < cus ? ceil_div(sh.iters, 8) : cus;
-  lds = (size_t)rows_dump_offset((sh.n + kChunk - 1) / kChunk) + 16;
-  if (sh.exact)
-    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, true>), dim3(blocks), dim3(512), lds, stream, p, a.packed,
-                       a.scales, a.bias, a.output, a.partials, sh);
-  else
-    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, false>), dim3(blocks), dim3(512), lds, stream, p, a.packed,
-                       a.scales, a.bias, a.output, a.partials, sh);
+  int blocks = ceil_div(sh.iters, 8) < cus ? ceil_div(sh.iters, 8) : cus;
+  const size_t lds = (size_t)rows_dump_offset((sh.n + kChunk - 1) / kChunk) + 16;
+  if constexpr (EPI != kPartials) {
+    if (sh.qblocks > 0) {
+      // Two steps per row leave room for two blocks per CU (more bytes in flight).
+      const int cap = (STEPS == 2 ? kRowsBlocksPerCu2 : 1) * cus;
+      blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
+      if (blocks < sh.qblocks) blocks = sh.qblocks;  // the in-launch quantizer's slices
+      GemvShape shape = sh;
+      shape.qstride = blocks >= 8 * sh.qblocks ? 8 : 1;
+      launch_rows_as<EPI, STEPS, true>(stream, p, a, shape, blocks, lds + kRowsQuantLds);
+      return;
+    }
+  }
+  launch_rows_as<EPI, STEPS, false>(stream, p, a, sh, blocks, lds);
 }
 
 // Steps per pipeline item: a whole row of up to two steps (q8 in registers),
@@ -639,6 +812,12 @@ hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, c
                      size_t lds, int steps) {
   const int nj = steps_per_item(steps);
   bool launched = false;
+  if constexpr (!FUSED && EPI != kPartials) {
+    if (sh.qblocks > 0 && steps == 2) {  // in-launch quantizer: the long-row kernel, two steps per row
+      launch_rows<EPI, 2>(stream, p, a, sh, blocks, lds);
+      return hipGetLastError();
+    }
+  }
   if (steps <= 2) {
     if (nj == 1) launched = launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
     else launched = launch_layout<MODE, EPI, FUSED, 2, false>(stream, p, a, sh, blocks, lds);
@@ -723,6 +902,8 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   // Dead lanes exist when the last step is partial (items never hold dead steps).
   sh.exact = chunks % lanes == 0;
   sh.split = 0;
+  sh.qblocks = 0;
+  sh.qstride = 1;
   const int cus = device_cus();
   const bool roll = !fused && steps > 2;  // the layouts launch_nj picks
   int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);
@@ -739,6 +920,7 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
       default: return hipErrorInvalidValue;
     }
   }
+  GemvPtrs p_quant{};
   if (a.q8_in == nullptr) {
     Scratch* scratch = a.work;
     if (scratch == nullptr) {
@@ -746,19 +928,28 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
       if (status != hipSuccess) return status;
     }
     if (chunks > scratch->capacity_chunks) return hipErrorInvalidValue;
-    hipError_t status;
-    // The scratch row is the GEMV's alone: the quantizer writes it nibble-split for the 4-bit dots.
+    // The scratch row is the GEMV's alone: it is written nibble-split for the 4-bit dots.
     const bool split = true;
-    QuantArgs q{a.mode, a.input, a.n, a.aux, a.n, a.eps, a.splits, a.head_dim, 1, scratch->q8, scratch->xsum,
-                scratch->scale, split};
-    status = launch_quantize(stream, q);
-    if (status != hipSuccess) return status;
+    sh.split = split;
+    const bool aligned = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.input) & 15) == 0;
+    if (a.mode == kPlain && aligned && lanes == 64 && steps >= 2 && steps <= 8 && scratch->sync != nullptr) {
+      // In-launch quantizer (the long-row kernel): one q8 word per thread, 32 chunks per slice.
+      sh.qblocks = ceil_div(chunks, 512 / 16);
+      p_quant = GemvPtrs{a.input, nullptr, scratch->q8, scratch->xsum, scratch->scale,
+                         scratch->q8, scratch->xsum, scratch->scale, scratch->sync};
+    } else {
+      QuantArgs q{a.mode, a.input, a.n, a.aux, a.n, a.eps, a.splits, a.head_dim, 1, scratch->q8, scratch->xsum,
+                  scratch->scale, split};
+      const hipError_t status = launch_quantize(stream, q);
+      if (status != hipSuccess) return status;
+    }
     a.q8_in = scratch->q8;
     a.xsum_in = scratch->xsum;
     a.scale_in = scratch->scale;
-    sh.split = split;
   }
-  const GemvPtrs p{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in};
+  const GemvPtrs p = sh.qblocks > 0 ? p_quant
+                                    : GemvPtrs{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in,
+                                               nullptr, nullptr, nullptr, nullptr};
   switch (a.epi) {
     case kStore: return launch_nj<kPlain, kStore, false>(stream, p, a, sh, blocks, lds, steps);
     case kResidual: return launch_nj<kPlain, kResidual, false>(stream, p, a, sh, blocks, lds, steps);

@@ -31,7 +31,11 @@ struct Scratch {
   float* scale = nullptr;
   int capacity_chunks = 0;
   float* token_partials = nullptr;  // fp32 wave partials of the K-sliced token GEMV
+  // Counters and flags of the GEMV's in-launch quantizer (kSyncBytes, zero
+  // between launches); null: quantize in a launch of its own.
+  unsigned* sync = nullptr;
 };
+constexpr int kSyncBytes = 4096;
 // Capacity of Scratch::token_partials (floats; 16 MB per device).
 constexpr long long kTokenPartialFloats = 4LL << 20;
 hipError_t scratch_for_stream(hipStream_t stream, Scratch** out);

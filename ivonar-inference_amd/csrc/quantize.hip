@@ -3,10 +3,11 @@
 //
 // PLAIN rows that are 16-byte aligned take quantize_plain_kernel: a block of
 // T threads (256, or 1024 for rows longer than 16 chunks) quantizes T/16
-// chunks of one token row, one q8 word per thread.  Every thread issues all
-// of its loads in one round - its four inputs and its share of the row's
-// amax as float4 - so the kernel costs one memory round trip, a block max
-// and the divisions.  Other rows (NORM, ATTN, unaligned) take
+// chunks of one token row, one q8 word per thread (quantize_plain_slice, which
+// the long-row GEMV launches also run in their first blocks).  Every thread
+// issues all of its loads in one round - its four inputs and its share of the
+// row's amax as float4 - so the kernel costs one memory round trip, a block
+// max and the divisions.  Other rows (NORM, ATTN, unaligned) take
 // quantize_rows_kernel: one block of 256 threads per slice of 16 chunks that
 // first reduces the whole row (sum of squares in the reference tree for NORM,
 // then amax) and then quantizes its slice.  Thread d of a slice writes q8
@@ -41,61 +42,13 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(QuantArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) a.scale[t] = scale;
 }
 
-// Row amax share of one thread: float4 j*T + tid of the row for j < kMaxRounds
-// per round; a row longer than kMaxRounds*T float4 takes more rounds.
-constexpr int kMaxRounds = 8;
-
 template <int T>
 __global__ __launch_bounds__(T) void quantize_plain_kernel(QuantArgs a) {
   __shared__ float slots[T / 64];
-  constexpr int kSlice = T / 16;  // chunks per block
   const int t = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int n = a.n;
-  const int n4 = n >> 2;
-  const int chunks = (n + kChunk - 1) / kChunk;
-  const float* row = a.input + (size_t)t * a.in_stride;
-  const float4* row4 = reinterpret_cast<const float4*>(row);
-
-  // This thread's q8 word: chunk u, quad w, field k holds inputs
-  // u*64 + w*16 + k + 4b for b = 0..3.
-  const int u = blockIdx.x * kSlice + (tid >> 4);
-  const int first = u * kChunk + ((tid >> 2) & 3) * 16 + (tid & 3);
-  float mine[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) mine[b] = row[min(first + 4 * b, n - 1)];
-  float amax = 0.0f;
-  for (int base = 0; base < n4; base += kMaxRounds * T) {
-    float4 v[kMaxRounds];
-#pragma unroll
-    for (int j = 0; j < kMaxRounds; ++j) v[j] = row4[min(base + j * T + tid, n4 - 1)];
-#pragma unroll
-    for (int j = 0; j < kMaxRounds; ++j)
-      amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
-  }
-  amax = wave_max(amax);
-  if ((tid & 63) == 0) slots[tid >> 6] = amax;
-  __syncthreads();
-  amax = slots[0];
-#pragma unroll
-  for (int w = 1; w < T / 64; ++w) amax = fmaxf(amax, slots[w]);
-  const float scale = fmaxf(amax / 127.0f, 1e-5f);
-
-  unsigned word = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int q = first + 4 * b < n ? (int)__builtin_rintf(mine[b] / scale) : 0;
-    word |= ((unsigned)q & 0xffu) << (8 * b);
-  }
-  const int value = (int)word;
-  const int total = chunk_lane_sum(word_sum(value));
-  const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // lane ^ 2
-  if (u < chunks) {
-    int32_t* q8 = reinterpret_cast<int32_t*>(a.q8 + (size_t)t * chunks * kChunk);
-    q8[u * 16 + (tid & 15)] = a.split ? (int)split_quad_word(word, partner, tid & 3) : value;
-    if ((tid & 15) == 0) a.xsum[(size_t)t * chunks + u] = total;
-  }
-  if (blockIdx.x == 0 && tid == 0) a.scale[t] = scale;
+  const int chunks = (a.n + kChunk - 1) / kChunk;
+  quantize_plain_slice<T>(a.input + (size_t)t * a.in_stride, a.n, blockIdx.x, a.split,
+                          a.q8 + (size_t)t * chunks * kChunk, a.xsum + (size_t)t * chunks, a.scale + t, slots);
 }
 
 }  // namespace

@@ -449,4 +449,69 @@ __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int c
   return scale;
 }
 
+// One block's share of the PLAIN quantizer for a 16-byte aligned row of n
+// inputs (n a multiple of 4): T/16 chunks (slice `slice`), one q8 word per
+// thread.  Every thread issues all of its loads in one round - its four
+// inputs and its share of the row's amax as float4 (a row longer than
+// ROUNDS*T float4 takes more rounds) - so the slice costs one memory
+// round trip, a block max and the divisions.  Writes the slice's q8 words
+// (split_quad_word form if `split`), its chunk sums and, from slice 0, the
+// token scale.  slots holds T/64 floats; all threads of the block call it.
+// COHERENT: the stores are device-coherent (agent-scope relaxed atomics, sc1),
+// complete device-wide once the storing wave's vmcnt reaches zero.
+template <int T, int ROUNDS = 8, bool COHERENT = false>
+__device__ __forceinline__ void quantize_plain_slice(const float* __restrict__ row, int n, int slice, bool split,
+                                                     int8_t* __restrict__ q8, int32_t* __restrict__ xsum,
+                                                     float* __restrict__ scale_out, float* slots) {
+  constexpr int kSlice = T / 16;  // chunks per block
+  const int tid = threadIdx.x;
+  const int n4 = n >> 2;
+  const int chunks = (n + kChunk - 1) / kChunk;
+  const float4* row4 = reinterpret_cast<const float4*>(row);
+
+  // This thread's q8 word: chunk u, quad w, field k holds inputs
+  // u*64 + w*16 + k + 4b for b = 0..3.
+  const int u = slice * kSlice + (tid >> 4);
+  const int first = u * kChunk + ((tid >> 2) & 3) * 16 + (tid & 3);
+  float mine[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) mine[b] = row[min(first + 4 * b, n - 1)];
+  float amax = 0.0f;
+  for (int base = 0; base < n4; base += ROUNDS * T) {
+    float4 v[ROUNDS];
+#pragma unroll
+    for (int j = 0; j < ROUNDS; ++j) v[j] = row4[min(base + j * T + tid, n4 - 1)];
+#pragma unroll
+    for (int j = 0; j < ROUNDS; ++j)
+      amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+  }
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) slots[tid >> 6] = amax;
+  __syncthreads();
+  amax = slots[0];
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) amax = fmaxf(amax, slots[w]);
+  const float scale = fmaxf(amax / 127.0f, 1e-5f);
+
+  unsigned word = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int q = first + 4 * b < n ? (int)__builtin_rintf(mine[b] / scale) : 0;
+    word |= ((unsigned)q & 0xffu) << (8 * b);
+  }
+  const int value = (int)word;
+  const int total = chunk_lane_sum(word_sum(value));
+  const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+  auto put = [](auto* p, auto v) {
+    if constexpr (COHERENT) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+  };
+  if (u < chunks) {
+    int32_t* q8w = reinterpret_cast<int32_t*>(q8);
+    put(q8w + u * 16 + (tid & 15), split ? (int)split_quad_word(word, partner, tid & 3) : value);
+    if ((tid & 15) == 0) put(xsum + u, total);
+  }
+  if (slice == 0 && tid == 0) put(scale_out, scale);
+}
+
 }  // namespace ivo

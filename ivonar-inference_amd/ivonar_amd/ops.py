@@ -90,6 +90,9 @@ def gemv(
     name = _GEMV_NAMES.get((mode, epilogue))
     if name is None:
         raise KernelError(f"no GEMV entry point for mode={mode!r} epilogue={epilogue!r}")
+    for tensor in (x, aux):
+        if tensor is not None and (tensor.dtype != torch.float32 or tensor.stride(-1) != 1):
+            raise KernelError(f"{name} needs fp32 activations with unit stride")
     rows_out = matrix.rows // 2 if epilogue == "silu_pair" else matrix.rows
     if out is None:
         if epilogue == "residual":

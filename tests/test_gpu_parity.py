@@ -171,6 +171,44 @@ def test_gemv_plain_store_model_shapes(cuda, oracle, rows, k):
     _check_gemv_store(cuda, oracle, rows, k, bias=False)
 
 
+@pytest.mark.parametrize("k", [5000, 8192, 28672, 40000])
+@pytest.mark.parametrize("rows", [2, 600])
+def test_gemv_long_rows_back_to_back(cuda, oracle, rows, k):
+    """Rows longer than 4096 inputs are quantized inside the GEMV launch by its first blocks, which the
+    other blocks wait for through two scratch counters that the launch sets back to zero.  Eight calls
+    with different inputs go out back to back on one stream (two rows: the quantizing blocks outnumber
+    the blocks with rows); each output must be the oracle's for its own input.  The same rows read
+    from an input that is not 16-byte aligned take the separate quantizer launch and give the same
+    bits."""
+    import torch
+    from ivonar_amd import ops, runtime
+
+    print(f"back-to-back gemv_plain_store K={k} N={rows}", flush=True)
+    rng = np.random.default_rng(rows + 3 * k)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    calls = 8
+    xs = (rng.standard_normal((calls, k)) * np.geomspace(1e-3, 1e3, calls)[:, None]).astype(np.float32)
+    inputs = _t(xs, cuda)
+    shifted = torch.zeros(calls * k + 1, dtype=torch.float32, device=cuda)
+    shifted[1:] = inputs.reshape(-1)
+    outs = torch.empty((2, calls, rows), dtype=torch.float32, device=cuda)
+    torch.cuda.synchronize()
+    for i in range(calls):
+        ops.gemv(matrix, inputs[i], out=outs[0, i])
+    for i in range(calls):
+        ops.gemv(matrix, shifted[1 + i * k:1 + (i + 1) * k], out=outs[1, i])
+    torch.cuda.synchronize()
+    got = to_np(outs)
+    for i in range(calls):
+        q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, xs[i], k)
+        mine = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, b,
+                                 np.zeros(rows, np.float32), k, lanes)
+        assert_bits_equal(got[0, i], mine, f"aligned input, call {i}")
+        assert_bits_equal(got[1, i], mine, f"unaligned input, call {i}")
+
+
 @pytest.mark.parametrize("k", [24, 1024, 4096, 5000, 8192, 8200, 28672, 40000, 49152])
 def test_gemv_residual_and_silu_pair(cuda, oracle, k):
     import torch
