@@ -414,14 +414,16 @@ __device__ __forceinline__ int load_u16_at(const void* p) {
 // returned, and a waiting block issues its row loads only after it has read
 // its flag.
 //
-// The quantizing blocks have the lowest block numbers of their stride class
-// (at most 8*15), so they are dispatched ahead of the blocks that wait behind
-// them, and they themselves wait only for one another.  The host picks a
-// stride of 8 for large grids: blocks are spread over the XCDs round-robin,
-// so all quantizing blocks then run on the XCD that starts the launch first
-// and share its L2 copy of the fp32 row (the XCDs start a launch up to about
-// 4 us apart).  Eight flags in eight cache lines spread the polling of up to
-// 512 waiting blocks (two per CU).
+// Progress: workgroups are dispatched in the order of their numbers, the
+// quantizing blocks wait only for one another, and every block numbered up
+// to the last of them fits on the device at once (stride 8 is used only when
+// 8*(Q-1) is below the resident block count, else stride 1), so a waiting
+// block never holds the slot a quantizing block needs.  Stride 8 is chosen
+// for speed: blocks are spread over the XCDs round-robin, so all quantizing
+// blocks then run on the XCD that starts the launch first and share its L2
+// copy of the fp32 row (the XCDs start a launch up to about 4 us apart).
+// Eight flags in eight cache lines spread the polling of up to 512 waiting
+// blocks (two per CU).
 //
 // At its end every block counts itself into its group's `done` counter; the
 // block that completes a group counts the group into `top`, and the block
@@ -789,8 +791,11 @@ void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const
       const int cap = (STEPS == 2 ? kRowsBlocksPerCu2 : 1) * cus;
       blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
       if (blocks < sh.qblocks) blocks = sh.qblocks;  // the in-launch quantizer's slices
+      // Stride 8 only when every block up to the last quantizing one can be
+      // resident at once (cap blocks are): no waiting block can then hold the
+      // slot a quantizing block needs.
       GemvShape shape = sh;
-      shape.qstride = blocks >= 8 * sh.qblocks ? 8 : 1;
+      shape.qstride = blocks >= 8 * sh.qblocks && 8 * (sh.qblocks - 1) < cap ? 8 : 1;
       launch_rows_as<EPI, STEPS, true>(stream, p, a, shape, blocks, lds + kRowsQuantLds);
       return;
     }
