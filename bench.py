@@ -704,7 +704,7 @@ def main() -> None:
             "traffic": None if not traffic or "error" in traffic else round(traffic["bytes_per_launch"]),
             "traffic_detail": traffic,
             "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
-            "kernel": "gemv_kernel at K=8192, gemv_rows_kernel at K=28672 (pre-quantized activations)",
+            "kernel": "gemv_rows_kernel, two steps per row at K=8192 and seven at K=28672 (pre-quantized activations)",
             "read_ceiling": ceiling,
             "graph_frac_of_read_ceiling": round(achieved_graph / ceiling["GBps"], 4),
             "frac_of_read_ceiling_trace": (round(achieved / trace["stream_read"]["copy_launch_GBps"], 4)

@@ -19,9 +19,10 @@
 // Memory.  Loads are unconditional: indices past the row or the matrix are
 // clamped to valid addresses and the integer result is masked, which keeps
 // the loop free of exec-mask branches.  The first weight loads are issued
-// before the activation prologue, and when a row needs at most two steps
-// per lane the next row step's weights are prefetched while the current one
-// is computed (double buffering), so each wave keeps 2-4 KB in flight.
+// before the activation prologue, and when a row needs one step per lane the
+// next row's weights are prefetched while the current one is computed
+// (double buffering), so each wave keeps 2-4 KB in flight; rows of 2..8
+// steps keep all steps of a row pair in flight (gemv_rows_kernel).
 //
 // Activations.  For rows up to kFusedLimit inputs the block quantizes the
 // fp32 input itself into LDS (the fused prologue of gemv_plain_*,
@@ -32,9 +33,9 @@
 // launch itself while the other blocks load their first weights
 // (quantize_publish / wait_published), other rows by the quantizer in a launch
 // of its own.  Pre-quantized activations are read by each lane straight from
-// global memory when a row needs at most two steps per lane (no LDS: the q8
-// row is small and stays in the caches for every block), else copied to LDS
-// once per block.
+// global memory when a row needs one step per lane (no LDS: the q8 row is
+// small and stays in the caches for every block), else copied to LDS once
+// per block (gemv_rows_kernel for 2..8 steps, the rolling layout above).
 //
 // Integer core.  The fused kernels take 8-bit dot products on q8 quads
 // (chunk_code_dot, 9 VALU per packed word).  Pre-quantized activations take
@@ -512,7 +513,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // its chunk sums, 16-byte aligned.
 __host__ __device__ constexpr int rows_dump_offset(int chunks) { return (chunks * (kChunk + 4) + 15) & ~15; }
 constexpr int kRowsQuantLds = 64;  // QUANT, after the dump slot: 8 block max slots and the wait status
-constexpr int kRowsBlocksPerCu2 = 2;  // QUANT with two steps per row
+constexpr int kRowsBlocksPerCu2 = 2;  // blocks per CU with two steps per row (one above)
 
 // One step of a row pair in flight: the 16 weight bytes of the lane's chunk in
 // its own row (w0) and in its partner's row (w1), and the group scale of the
@@ -522,8 +523,8 @@ struct RowStep {
   int s;
 };
 
-// Pre-quantized rows of 3..8 steps (8193 <= K <= 32768 inputs), 64 lanes per
-// row, activation row in LDS (nibble-split).  Every lane keeps all STEPS steps of its row pair in
+// Rows of 2..8 steps (4097 <= K <= 32768 inputs, two blocks per CU at two
+// steps, one above), 64 lanes per row, activation row in LDS (nibble-split).  Every lane keeps all STEPS steps of its row pair in
 // flight (3*STEPS loads: 14 KB per wave at K=28672, 8 waves and 112 KB per
 // CU) instead of the rolling pipeline's one or two, and refills a step with
 // the same step of the wave's next row pair as soon as it is computed.
@@ -783,13 +784,12 @@ template <int EPI, int STEPS>
 void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int /*blocks*/,
                  size_t /*lds*/) {
   const int cus = device_cus();
-  int blocks = ceil_div(sh.iters, 8) < cus ? ceil_div(sh.iters, 8) : cus;
+  // Two steps per row leave room for two blocks per CU (more bytes in flight).
+  const int cap = (STEPS == 2 ? kRowsBlocksPerCu2 : 1) * cus;
+  int blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
   const size_t lds = (size_t)rows_dump_offset((sh.n + kChunk - 1) / kChunk) + 16;
   if constexpr (EPI != kPartials) {
     if (sh.qblocks > 0) {
-      // Two steps per row leave room for two blocks per CU (more bytes in flight).
-      const int cap = (STEPS == 2 ? kRowsBlocksPerCu2 : 1) * cus;
-      blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
       if (blocks < sh.qblocks) blocks = sh.qblocks;  // the in-launch quantizer's slices
       // Stride 8 only when every block up to the last quantizing one can be
       // resident at once (cap blocks are): no waiting block can then hold the
@@ -803,10 +803,9 @@ void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const
   launch_rows_as<EPI, STEPS, false>(stream, p, a, sh, blocks, lds);
 }
 
-// Steps per pipeline item: a whole row of up to two steps (q8 in registers),
-// else the largest of 4, 2, 1 that divides the row's steps (no dead steps).
+// Steps per pipeline item of the rolling layout (rows of more than 8 steps):
+// the largest of 4, 2, 1 that divides the row's steps (no dead steps).
 int steps_per_item(int steps) {
-  if (steps <= 2) return steps;
   if (steps % 4 == 0) return 4;
   if (steps % 2 == 0) return 2;
   return 1;
@@ -815,20 +814,14 @@ int steps_per_item(int steps) {
 template <int MODE, int EPI, bool FUSED>
 hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
                      size_t lds, int steps) {
-  const int nj = steps_per_item(steps);
   bool launched = false;
-  if constexpr (!FUSED && EPI != kPartials) {
-    if (sh.qblocks > 0 && steps == 2) {  // in-launch quantizer: the long-row kernel, two steps per row
-      launch_rows<EPI, 2>(stream, p, a, sh, blocks, lds);
-      return hipGetLastError();
-    }
-  }
-  if (steps <= 2) {
-    if (nj == 1) launched = launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
-    else launched = launch_layout<MODE, EPI, FUSED, 2, false>(stream, p, a, sh, blocks, lds);
+  if (steps <= 1) {  // one step per row: q8 in registers
+    launched = launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
   } else if constexpr (!FUSED) {
+    // Rows of more than one step have 64 lanes (lanes < 64 span a row in one step).
     if (sh.lanes == 64 && steps <= 8) {
       switch (steps) {
+        case 2: launch_rows<EPI, 2>(stream, p, a, sh, blocks, lds); break;
         case 3: launch_rows<EPI, 3>(stream, p, a, sh, blocks, lds); break;
         case 4: launch_rows<EPI, 4>(stream, p, a, sh, blocks, lds); break;
         case 5: launch_rows<EPI, 5>(stream, p, a, sh, blocks, lds); break;
@@ -838,6 +831,7 @@ hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, c
       }
       return hipGetLastError();
     }
+    const int nj = steps_per_item(steps);
     if (nj == 4) launched = launch_layout<MODE, EPI, FUSED, 4, true>(stream, p, a, sh, blocks, lds);
     else if (nj == 2) launched = launch_layout<MODE, EPI, FUSED, 2, true>(stream, p, a, sh, blocks, lds);
     else launched = launch_layout<MODE, EPI, FUSED, 1, true>(stream, p, a, sh, blocks, lds);
@@ -910,7 +904,7 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   sh.qblocks = 0;
   sh.qstride = 1;
   const int cus = device_cus();
-  const bool roll = !fused && steps > 2;  // the layouts launch_nj picks
+  const bool roll = !fused && steps > 8;  // the rolling layout (2..8 steps: the long-row kernel sizes its own grid)
   int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);
   const int cap = (fused ? 2 : roll ? 1 : kBlocksPerCu) * cus;
   if (blocks > cap) blocks = cap;
