@@ -56,8 +56,11 @@ hipError_t ivonar_init(int device);
  * (kernel_decoder.py:215, ternary.cu:1-46): "HEAD_DIM" (ATTN prologue head
  * width, default 64), "TILE" (token rows of quantize_tile_*, default 32),
  * "MAX_CHUNKS" (caller q8 capacity, default 70), "MAX_TOPK" (largest top-k
- * of sample_token, 1..1024, default 256).  Unknown names and out-of-range
- * values return hipErrorInvalidValue. */
+ * of sample_token, 1..1024, default 256).  With no reference counterpart,
+ * "GEMV_WAIT_SPINS" (0 or more, default 2^20) bounds how often a block of a
+ * GEMV that quantizes its row in-launch polls for the row before it gives up
+ * (its outputs are then NaN); tests lower it to exercise that path.  Unknown
+ * names and out-of-range values return hipErrorInvalidValue. */
 hipError_t ivonar_define(const char* name, int value);
 
 const char* ivonar_error_string(hipError_t status);

@@ -252,7 +252,12 @@ extern "C" {
 hipError_t ivonar_init(int device) { return init_device(device); }
 
 hipError_t ivonar_define(const char* name, int value) {
-  if (name == nullptr || value <= 0) return hipErrorInvalidValue;
+  if (name == nullptr) return hipErrorInvalidValue;
+  if (strcmp(name, "GEMV_WAIT_SPINS") == 0 && value >= 0) {
+    defines().wait_spins = value;
+    return hipSuccess;
+  }
+  if (value <= 0) return hipErrorInvalidValue;
   if (strcmp(name, "HEAD_DIM") == 0) defines().head_dim = value;
   else if (strcmp(name, "TILE") == 0) defines().tile = value;
   else if (strcmp(name, "MAX_CHUNKS") == 0) defines().max_chunks = value;

@@ -66,6 +66,7 @@ struct GemvShape {
   int split;  // the activations are nibble-split quads (the two-pass path's own scratch)
   int qblocks;  // > 0: qblocks blocks quantize the PLAIN row into q8_out first (in-launch quantizer)
   int qstride;  // those blocks: 0, qstride, 2*qstride, ... (slice blockIdx / qstride)
+  int spins;    // polls before a waiting block gives up (GEMV_WAIT_SPINS)
 };
 
 struct GemvPtrs {
@@ -432,11 +433,10 @@ __device__ __forceinline__ int load_u16_at(const void* p) {
 // launch starts from zero without a memset.  A block counts itself done only
 // after it has passed its wait, and every quantizing block has counted into
 // `arrive` before that, so nothing is counted or raised after the reset.  The
-// wait is bounded (kPublishSpins polls, about a second): a wait that gives up
-// makes the block's outputs NaN instead of hanging the launch.  Two launches
+// wait is bounded (sh.spins polls, 2^20 by default: about a second): a wait
+// that gives up makes the block's outputs NaN instead of hanging the launch.  Two launches
 // that share one scratch must not overlap (stream order or one scratch per
 // stream).
-constexpr int kPublishSpins = 1 << 20;
 constexpr int kSyncGroups = 8;
 constexpr int kSyncLineWords = 32;  // one counter or flag per 128-byte line
 constexpr int kArriveLine = 0, kReadyLine = 1, kDoneLine = 1 + kSyncGroups, kTopLine = 1 + 2 * kSyncGroups;
@@ -466,12 +466,12 @@ __device__ __forceinline__ void quantize_publish(const GemvPtrs& in, const GemvS
 }
 
 // All threads of the block call it; true when the row is published.
-__device__ __forceinline__ bool wait_published(const GemvPtrs& in, int* status) {
+__device__ __forceinline__ bool wait_published(const GemvPtrs& in, int spins_limit, int* status) {
   if (threadIdx.x == 0) {
     const unsigned* ready = sync_line(in.sync, kReadyLine + (int)(blockIdx.x & (kSyncGroups - 1)));
     int ok = 1;
     for (int spins = 0; __hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++spins) {
-      if (spins == kPublishSpins) {
+      if (spins >= spins_limit) {
         ok = 0;
         break;
       }
@@ -651,7 +651,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));
     pb = pair_base(it);
     static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
-    const bool ok = wait_published(in, published);
+    const bool ok = wait_published(in, sh.spins, published);
 #pragma unroll
     for (int k = 0; k < kCopy; ++k) qv[k] = load_b128_sc1(gq + min(k * kBlock + tid, words - 1));
     xv = load_b32_sc1(in.xsum_in + min(tid, chunks - 1));
@@ -903,6 +903,7 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   sh.split = 0;
   sh.qblocks = 0;
   sh.qstride = 1;
+  sh.spins = defines().wait_spins;
   const int cus = device_cus();
   const bool roll = !fused && steps > 8;  // the rolling layout (2..8 steps: the long-row kernel sizes its own grid)
   int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);

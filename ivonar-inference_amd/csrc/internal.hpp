@@ -12,7 +12,8 @@ namespace ivo {
 // (kernel_decoder.py:215): HEAD_DIM for the ATTN prologue, TILE for the
 // token count of the quantize_tile_* entry points, MAX_CHUNKS (capacity of
 // the caller's q8 buffers, used only for argument checks), MAX_TOPK (largest
-// top-k of the sampler, ternary.cu:8).  Atomic, so that ivonar_define on one
+// top-k of the sampler, ternary.cu:8), and GEMV_WAIT_SPINS (no reference
+// counterpart).  Atomic, so that ivonar_define on one
 // thread and a launch on another never race (a launch reads each value once).
 constexpr int kMaxTopK = 1024;
 constexpr int kMaxSampleVocab = 1 << 18;
@@ -21,6 +22,9 @@ struct Defines {
   std::atomic<int> tile{32};
   std::atomic<int> max_chunks{70};
   std::atomic<int> max_topk{256};
+  // Polls a block of the GEMV's in-launch quantizer makes before it gives up
+  // (its outputs are then NaN); lowered only by tests of that path.
+  std::atomic<int> wait_spins{1 << 20};
 };
 Defines& defines();
 

@@ -209,6 +209,44 @@ def test_gemv_long_rows_back_to_back(cuda, oracle, rows, k):
         assert_bits_equal(got[1, i], mine, f"unaligned input, call {i}")
 
 
+@pytest.mark.parametrize("k", [8192, 28672])
+def test_gemv_in_launch_wait_gives_up_loudly(cuda, oracle, k):
+    """A block of the in-launch quantizer that stops waiting for the published row writes NaN for its
+    rows, never other values.  The host lowers the poll limit to zero (GEMV_WAIT_SPINS), so blocks that
+    find the row unpublished give up at once and every kernel still exits normally; each output must
+    be NaN or the oracle's bits.  With the limit restored, the next calls on the same scratch give
+    the oracle's bits in every row (the counters a launch leaves stay consistent)."""
+    import torch
+    from ivonar_amd import ops, runtime
+    from ivonar_amd.runtime import check
+
+    rows = 4096
+    print(f"in-launch wait limit 0: gemv_plain_store K={k} N={rows}", flush=True)
+    rng = np.random.default_rng(k + 77)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    expected = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, b,
+                                 np.zeros(rows, np.float32), k, lanes)
+    xv = _t(x, cuda)
+    lib = runtime.library()
+    gave_up = 0
+    try:
+        check(lib.ivonar_define(b"GEMV_WAIT_SPINS", 0), "define GEMV_WAIT_SPINS")
+        for rep in range(4):
+            got = to_np(ops.gemv(matrix, xv))
+            nan = np.isnan(got)
+            gave_up += int(nan.sum())
+            assert_bits_equal(got[~nan], expected[~nan], f"limit 0, call {rep}: rows that did not give up")
+    finally:
+        check(lib.ivonar_define(b"GEMV_WAIT_SPINS", 1 << 20), "define GEMV_WAIT_SPINS")
+    print(f"rows written as NaN with limit 0: {gave_up} of {4 * rows}", flush=True)
+    for rep in range(3):
+        assert_bits_equal(to_np(ops.gemv(matrix, xv)), expected, f"limit restored, call {rep}")
+
+
 @pytest.mark.parametrize("k", [24, 1024, 4096, 5000, 8192, 8200, 28672, 40000, 49152])
 def test_gemv_residual_and_silu_pair(cuda, oracle, k):
     import torch
