@@ -30,88 +30,115 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const float* __restric
   output[i] = tile[t * n + i];
 }
 
-constexpr int kArgmaxThreads = 1024;
+// Greedy argmax: first index of the maximum over n values.  One block of
+// 1024 threads reading 128 KB of logits is bound by how many misses one CU
+// keeps in flight, so the values are split into tiles of kArgmaxTile
+// elements over up to kArgmaxBlocks blocks (grid-stride over tiles).  Every
+// block reduces its tiles to one (value, index) pair; with more than one
+// block, each stores its pair device-coherently into the stream's scratch,
+// waits for the store, and counts itself; the block that makes the count
+// complete reduces the pairs and resets the count to zero (so every launch
+// starts from zero).  (value, index) pairs are ordered by value, then by the
+// smaller index, over NaN-free values, so the result does not depend on how
+// the elements are split or in which order pairs are merged.
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxTile = kArgmaxThreads * 8;  // elements per tile: 8 per thread (two float4)
+constexpr int kArgmaxBlocks = 64;
 
-// First index of the maximum over n values (one block).
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ values, int n,
-                                                                 int64_t* __restrict__ out) {
-  __shared__ float best_value[kArgmaxThreads / 64];
-  __shared__ int best_index[kArgmaxThreads / 64];
-  // (value, index) pairs are compared by value, then by smaller index, so
-  // the result does not depend on the order the elements are visited in.
-  // Loads go out in batches (a 16-byte vector per element group when the
-  // row allows it), clamped to the row and masked after.
-  float value = -__builtin_inff();
-  int index = n;
-  auto consider = [&](float v, int i) {
+struct Best {
+  float value;
+  int index;
+  __device__ void take(float v, int i) {
     if (v > value || (v == value && i < index)) {
       value = v;
       index = i;
     }
-  };
-  constexpr int kBatch = 8;
-  int scalar_from = 0;
-  if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(values) & 15) == 0) {
-    const float4* v4 = reinterpret_cast<const float4*>(values);
-    const int n4 = n >> 2;
-    for (int base = 0; base < n4; base += kArgmaxThreads * kBatch) {
-      float4 b[kBatch];
+  }
+};
+
+// Wave reduction, complete in lane 0 only (DPP row shifts and permlane swaps;
+// each stage reads a lane that has already folded its share, and the order
+// above does not depend on the pairing).
+__device__ __forceinline__ void wave_best(Best& b) {
+  b.take(row_shl<1>(b.value), row_shl_int<1>(b.index));
+  b.take(row_shl<2>(b.value), row_shl_int<2>(b.index));
+  b.take(row_shl<4>(b.value), row_shl_int<4>(b.index));
+  b.take(row_shl<8>(b.value), row_shl_int<8>(b.index));
+  b.take(row_swap16(b.value), __float_as_int(row_swap16(__int_as_float(b.index))));
+  b.take(row_swap32(b.value), __float_as_int(row_swap32(__int_as_float(b.index))));
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ values, int n,
+                                                                 int64_t* __restrict__ out, float* part_value,
+                                                                 int* part_index, unsigned* count) {
+  __shared__ float best_value[kArgmaxThreads / 64];
+  __shared__ int best_index[kArgmaxThreads / 64];
+  __shared__ int last_block;
+  Best b{-__builtin_inff(), n};
+  const int tiles = (n + kArgmaxTile - 1) / kArgmaxTile;
+  const int tid = threadIdx.x;
+  // Loads go out two float4 (or eight scalars) per thread and tile, clamped
+  // to the row and masked after.
+  const bool vec = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(values) & 15) == 0;
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    if (vec) {
+      const float4* v4 = reinterpret_cast<const float4*>(values);
+      const int n4 = n >> 2;
+      const int j0 = tile * (kArgmaxTile / 4) + tid, j1 = j0 + kArgmaxThreads;
+      const float4 a = v4[min(j0, n4 - 1)], c = v4[min(j1, n4 - 1)];
+      if (j0 < n4) {
+        b.take(a.x, 4 * j0);
+        b.take(a.y, 4 * j0 + 1);
+        b.take(a.z, 4 * j0 + 2);
+        b.take(a.w, 4 * j0 + 3);
+      }
+      if (j1 < n4) {
+        b.take(c.x, 4 * j1);
+        b.take(c.y, 4 * j1 + 1);
+        b.take(c.z, 4 * j1 + 2);
+        b.take(c.w, 4 * j1 + 3);
+      }
+    } else {
+      float v[8];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) b[k] = v4[min(base + k * kArgmaxThreads + (int)threadIdx.x, n4 - 1)];
+      for (int k = 0; k < 8; ++k) v[k] = values[min(tile * kArgmaxTile + k * kArgmaxThreads + tid, n - 1)];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        const int j = base + k * kArgmaxThreads + threadIdx.x;
-        if (j < n4) {
-          consider(b[k].x, 4 * j);
-          consider(b[k].y, 4 * j + 1);
-          consider(b[k].z, 4 * j + 2);
-          consider(b[k].w, 4 * j + 3);
-        }
+      for (int k = 0; k < 8; ++k) {
+        const int i = tile * kArgmaxTile + k * kArgmaxThreads + tid;
+        if (i < n) b.take(v[k], i);
       }
     }
-    scalar_from = n;
   }
-  for (int base = scalar_from; base < n; base += kArgmaxThreads * kBatch) {
-    float b[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) b[k] = values[min(base + k * kArgmaxThreads + (int)threadIdx.x, n - 1)];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int i = base + k * kArgmaxThreads + threadIdx.x;
-      if (i < n) consider(b[k], i);
-    }
-  }
-  // Wave reduction, complete in lane 0 only (DPP row shifts and permlane
-  // swaps; each stage reads a lane that has already folded its share, and
-  // the (value, smaller index) order over NaN-free values does not depend on
-  // the pairing).
-  auto take = [&](float other, int other_index) {
-    if (other > value || (other == value && other_index < index)) {
-      value = other;
-      index = other_index;
-    }
-  };
-  take(row_shl<1>(value), row_shl_int<1>(index));
-  take(row_shl<2>(value), row_shl_int<2>(index));
-  take(row_shl<4>(value), row_shl_int<4>(index));
-  take(row_shl<8>(value), row_shl_int<8>(index));
-  take(row_swap16(value), __float_as_int(row_swap16(__int_as_float(index))));
-  take(row_swap32(value), __float_as_int(row_swap32(__int_as_float(index))));
-  if ((threadIdx.x & 63) == 0) {
-    best_value[threadIdx.x >> 6] = value;
-    best_index[threadIdx.x >> 6] = index;
+  wave_best(b);
+  if ((tid & 63) == 0) {
+    best_value[tid >> 6] = b.value;
+    best_index[tid >> 6] = b.index;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float v = best_value[0];
-    int k = best_index[0];
-    for (int w = 1; w < kArgmaxThreads / 64; ++w) {
-      if (best_value[w] > v || (best_value[w] == v && best_index[w] < k)) {
-        v = best_value[w];
-        k = best_index[w];
-      }
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) b.take(best_value[w], best_index[w]);
+    int last = 1;
+    if (gridDim.x > 1) {
+      __hip_atomic_store(part_value + blockIdx.x, b.value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(part_index + blockIdx.x, b.index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the pair is performed device-wide before the count
+      last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     }
-    *out = k < n ? k : 0;
+    last_block = last;
+    if (gridDim.x == 1) *out = b.index < n ? b.index : 0;
+  }
+  __syncthreads();
+  if (gridDim.x == 1 || !last_block || tid >= 64) return;
+  // The last block's first wave: lane l reads the pairs of blocks l and l + 64 (issued after the
+  // count returned, device-coherent).
+  Best f{-__builtin_inff(), n};
+  for (int blk = tid; blk < (int)gridDim.x; blk += 64)
+    f.take(__hip_atomic_load(part_value + blk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+           __hip_atomic_load(part_index + blk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  wave_best(f);
+  if (tid == 0) {
+    *out = f.index < n ? f.index : 0;
+    __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -133,7 +160,25 @@ hipError_t launch_gather(hipStream_t stream, const float* tile, float* output, i
 
 hipError_t launch_argmax(hipStream_t stream, const float* values, int n, int64_t* out) {
   if (n <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, stream, values, n, out);
+  const int tiles = ceil_div(n, kArgmaxTile);
+  int blocks = tiles < kArgmaxBlocks ? tiles : kArgmaxBlocks;
+  float* part_value = nullptr;
+  int* part_index = nullptr;
+  unsigned* count = nullptr;
+  if (blocks > 1) {
+    Scratch* scratch = nullptr;
+    const hipError_t status = scratch_for_stream(stream, &scratch);
+    if (status != hipSuccess) return status;
+    if (scratch->token_partials == nullptr || scratch->sync == nullptr) {
+      blocks = 1;  // no scratch for the pairs: one block scans every tile
+    } else {
+      part_value = scratch->token_partials;
+      part_index = reinterpret_cast<int*>(scratch->token_partials + kArgmaxBlocks);
+      count = scratch->sync + kArgmaxCountWord;
+    }
+  }
+  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kArgmaxThreads), 0, stream, values, n, out, part_value,
+                     part_index, count);
   return hipGetLastError();
 }
 

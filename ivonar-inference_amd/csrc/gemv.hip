@@ -440,7 +440,7 @@ __device__ __forceinline__ int load_u16_at(const void* p) {
 constexpr int kSyncGroups = 8;
 constexpr int kSyncLineWords = 32;  // one counter or flag per 128-byte line
 constexpr int kArriveLine = 0, kReadyLine = 1, kDoneLine = 1 + kSyncGroups, kTopLine = 1 + 2 * kSyncGroups;
-static_assert((kTopLine + 1) * kSyncLineWords * 4 <= kSyncBytes, "the scratch's counter region holds every line");
+static_assert((kTopLine + 1) * kSyncLineWords <= kArgmaxCountWord, "the counter lines stop before the argmax count");
 
 __device__ __forceinline__ unsigned* sync_line(unsigned* sync, int line) { return sync + line * kSyncLineWords; }
 

@@ -40,6 +40,9 @@ struct Scratch {
   unsigned* sync = nullptr;
 };
 constexpr int kSyncBytes = 4096;
+// The argmax's block count, in the last 128-byte line of the sync region (the
+// GEMV's in-launch quantizer uses the lines before it).
+constexpr int kArgmaxCountWord = kSyncBytes / 4 - 32;
 // Capacity of Scratch::token_partials (floats; 16 MB per device).
 constexpr long long kTokenPartialFloats = 4LL << 20;
 hipError_t scratch_for_stream(hipStream_t stream, Scratch** out);

@@ -415,7 +415,7 @@ def test_embed_gather_and_argmax(cuda, oracle):
     assert int(to_np(ops.argmax(_t(values, cuda)))[0]) == oracle.argmax(values) == 123
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 1023, 32000, 32001, 100003])
+@pytest.mark.parametrize("n", [1, 3, 4, 1023, 2048, 2049, 32000, 32001, 100003, 262144])
 @pytest.mark.parametrize("offset", [0, 1])
 def test_argmax_first_maximum(cuda, oracle, n, offset):
     """Vector and scalar load paths (offset 1 breaks 16-byte alignment), ties, all-negative rows."""
@@ -430,6 +430,28 @@ def test_argmax_first_maximum(cuda, oracle, n, offset):
     device_values = _t(values, cuda)[offset:]
     got = int(to_np(ops.argmax(device_values))[0])
     assert got == oracle.argmax(values[offset:]) == int(ties[0])
+
+
+def test_argmax_back_to_back(cuda, oracle):
+    """Eight argmax calls over different 32000-value rows go out back to back on one stream (the blocks'
+    pairs and their count live in the stream's scratch and are reused by every call); each token must be
+    the first maximum of its own row, including ties that span blocks."""
+    import torch
+    from ivonar_amd import ops
+
+    rng = np.random.default_rng(9)
+    rows = rng.standard_normal((8, 32000)).astype(np.float32)
+    for r in range(8):
+        peak = rows[r].max() + 1.0
+        rows[r, [int(rng.integers(0, 32000)), int(rng.integers(0, 32000))]] = peak
+    device_rows = _t(rows, cuda)
+    outs = torch.empty(8, dtype=torch.int64, device=cuda)
+    torch.cuda.synchronize()
+    for r in range(8):
+        ops.argmax(device_rows[r], out=outs[r:r + 1])
+    got = to_np(outs)
+    for r in range(8):
+        assert int(got[r]) == oracle.argmax(rows[r]), f"row {r}"
 
 
 # ----------------------------------------------------------- graph capture
