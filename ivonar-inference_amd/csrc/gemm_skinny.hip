@@ -35,12 +35,6 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr unsigned kSignedLut = 0x000100FFu;  // v_perm table: code 0 -> -1, 1 -> 0, 2 -> +1
-
-__device__ __forceinline__ unsigned signed_codes(unsigned w, int k) {
-  return __builtin_amdgcn_perm(0u, kSignedLut, (w >> (2 * k)) & kLow2);
-}
-
 template <int MT, int R>
 struct SkinnyStage {
   static constexpr int kGroups = (MT == 1 && R <= 2) ? 4 : 2;  // groups per stage (register budget)

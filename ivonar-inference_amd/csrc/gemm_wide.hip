@@ -31,9 +31,15 @@
 //   B: 64*WN weight rows x 2 pieces of 16 bytes (the group's packed bytes),
 //      piece p of row r at slot p * 64*WN + r, so the 8-byte operand reads of
 //      a wave cover two contiguous 256-byte runs;
-//   minus each token's group sum (seeds the MFMA accumulator so that
-//   sum(code * q) - sum(q) = P comes out exact) and the rows' fp32 scales,
-//   both written from registers one group ahead.
+//   the rows' fp32 scales, loaded into registers three groups ahead and
+//   written to LDS one step before their group is computed.
+// The weight fragments are expanded to signed int8 codes (-1, 0, +1; one
+// v_perm_b32 table lookup per four codes), so the MFMA chain of a group starts
+// from zero and returns P itself: no per-token group sums are staged or read
+// (with the unsigned codes 0..2, the seed -sum(q) of every token row was a
+// third of the LDS operand reads; K=4096 -> N=14336 at M=2048: 164 -> 151 us).
+// Loading the scales three groups ahead instead of two took 158 -> 155 us
+// on its own.
 #include "buffer_ops.hpp"
 #include "internal.hpp"
 #include "ternary_device.hpp"
@@ -51,12 +57,11 @@ struct WideTile {
   static constexpr int kAOffset = 0;
   static constexpr int kBOffset = kTokens * 128;
   static constexpr int kStageBytes = kBOffset + kRows * 32;  // DMA part of one stage
-  static constexpr int kLdsBytes = 3 * (kStageBytes + kTokens * 4 + kRows * 4);
+  static constexpr int kLdsBytes = 3 * (kStageBytes + kRows * 4);
   static constexpr int kLoadsA = kTokens * 8 / kThreads;  // 16-byte pieces per thread and group
   static constexpr int kLoadsB = kRows * 2 / kThreads;
   static constexpr int kLoads = kLoadsA + kLoadsB;         // DMA instructions per thread and group
   static_assert(kTokens * 8 % kThreads == 0 && kRows * 2 == 2 * kThreads, "whole DMA rounds");
-  static_assert(kTokens <= kThreads, "one thread per token seed");
 };
 
 template <int EPI, int MT, int WN>
@@ -68,7 +73,6 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
                                                             float* __restrict__ output, GemmArgs a) {
   using T = WideTile<MT, WN>;
   __shared__ __align__(16) unsigned char stages[3][T::kStageBytes];
-  __shared__ __align__(16) int seeds[3][T::kTokens];
   __shared__ __align__(16) float row_scales[3][T::kRows];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -84,7 +88,6 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
   const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
   const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
   const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
-  const v4u x_buf = wide_buffer(a.xsum_in, (long long)a.m * chunks * 4);
 
   // Per-thread DMA offsets, fixed for the kernel (the group moves the scalar
   // offset).  A: slot s = j * threads + tid holds token s >> 3, piece
@@ -100,8 +103,6 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
   }
   // B: slot s = j * threads + tid holds row tid, piece j.
   const int b_off = (row0 + tid) * a.row_bytes;
-  const int seed_token = tid % T::kTokens;
-  const int x_off = (token0 + seed_token) * chunks * 4;
   const int s_off = (row0 + tid) * a.groups * 2;
 
   auto dma = [&](int g, int stage) {
@@ -114,25 +115,14 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
     for (int j = 0; j < T::kLoadsB; ++j)
       dma16(w_buf, base + T::kBOffset + j * T::kThreads * 16, b_off + j * 16, g * 32);
   };
-  // The token sums and the row scale of a group, loaded into registers and
-  // written to LDS (as minus the group sum and as fp32) once they arrive.
-  struct Side {
-    int x0, x1, s;
-  };
-  auto side_load = [&](int g) {
-    const bool second_live = 2 * g + 1 < chunks;
-    Side r;
-    r.x0 = load_b32(x_buf, x_off, g * 8);
-    r.x1 = load_b32(x_buf, second_live ? x_off + 4 : kPast, g * 8);
-    r.s = load_u16(s_buf, s_off, g * 2);
-    return r;
-  };
-  // Waits until at most `kLoads` loads are in flight - the DMA issued after
-  // the side loads - then stores the side values.
-  auto side_store = [&](Side& r, int stage) {
-    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(r.x0), "+v"(r.x1), "+v"(r.s) : "n"(T::kLoads) : "memory");
-    seeds[stage][seed_token] = -(r.x0 + r.x1);
-    row_scales[stage][tid] = h2f((uint16_t)r.s);
+  // The row scale of a group (thread tid: row tid), loaded into a register
+  // three groups ahead and written to LDS as fp32 two steps later.  The
+  // wait before the store leaves in flight only what the wave issued after
+  // that load: the DMA of the next group (kLoads) and the next scale load (1).
+  auto scale_load = [&](int g) { return load_u16(s_buf, s_off, g * 2); };
+  auto scale_store = [&](int& r, int stage) {
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(r) : "n"(T::kLoads + 1) : "memory");
+    row_scales[stage][tid] = h2f((uint16_t)r);
   };
 
   float acc[MT][4][4];
@@ -164,16 +154,17 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
   const int sc_read = wave * 64 + col;
 
   // One group step.  Group g+2 streams into the stage group g-1 used while
-  // group g is computed: first the side loads of g+2, then its DMA, then the
-  // MFMAs of g, then the side values of g+2 go to LDS.  The wait for those
-  // side loads also retires the DMA of g+1 (loads complete in order) and
-  // leaves the DMA of g+2 in flight, so the barrier at the top of the next
-  // step publishes every wave's pieces of g+1.
-  auto step = [&](int g, int cur, int fill) {
+  // group g is computed: first its DMA, then the scale load of g+3, then the
+  // MFMAs of g, then the scale of g+2 (loaded in the previous step) goes to
+  // LDS.  The wait before that store also retires the DMA of g+1 (loads
+  // complete in order) and leaves the DMA of g+2 and the scale load of g+3
+  // in flight, so the barrier at the top of the next step publishes every
+  // wave's pieces of g+1.  `pending` holds the scale of g+2 and `fresh`
+  // receives that of g+3; the caller alternates the two registers.
+  auto step = [&](int g, int cur, int fill, int& pending, int& fresh) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const int g_fill = min(g + 2, groups - 1);  // past the end: the last group again (never read)
-    Side side = side_load(g_fill);
-    dma(g_fill, fill);
+    dma(min(g + 2, groups - 1), fill);  // past the end: the last group again (never read)
+    fresh = scale_load(min(g + 3, groups - 1));
 
     // The step is written as a fixed issue order (scheduling fences between
     // units): per token row, eight units of one MFMA and two outputs (four
@@ -181,6 +172,7 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
     // reads go out at the start of a row; in the first row each unit also
     // expands the weight fragment its MFMA takes.
     const unsigned char* base = stages[cur];
+    const v4i zero = {0, 0, 0, 0};
     uint2 w[4];
     float sc[4];
 #pragma unroll
@@ -188,20 +180,19 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
       w[nt] = *reinterpret_cast<const uint2*>(base + T::kBOffset + b_read + nt * 16 * 16);
       sc[nt] = row_scales[cur][sc_read + nt * 16];
     }
-    auto operands = [&](int mt, v4i& a0, v4i& a1, v4i& seed) {
+    auto operands = [&](int mt, v4i& a0, v4i& a1) {
       const int t = mt * 16 + col;
       const unsigned char* arow = base + T::kAOffset + t * 128;
       a0 = *reinterpret_cast<const v4i*>(arow + (((2 * kb) ^ a_swizzle(t)) * 16));
       a1 = *reinterpret_cast<const v4i*>(arow + (((2 * kb + 1) ^ a_swizzle(t)) * 16));
-      seed = *reinterpret_cast<const v4i*>(&seeds[cur][mt * 16 + 4 * kb]);
     };
-    v4i a0, a1, seed;
-    operands(0, a0, a1, seed);
+    v4i a0, a1;
+    operands(0, a0, a1);
     v4i bf[2][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      v4i na0, na1, nseed;
-      if (mt + 1 < MT) operands(mt + 1, na0, na1, nseed);
+      v4i na0, na1;
+      if (mt + 1 < MT) operands(mt + 1, na0, na1);
       const int fold_row = mt == 0 ? MT - 1 : mt - 1;
       v4i p[4];
 #pragma unroll
@@ -209,9 +200,10 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
         const int h = u >> 2, nt = u & 3;
         if (mt == 0) {
           const unsigned x = h ? w[nt].y : w[nt].x;
-          bf[h][nt] = v4i{(int)(x & kLow2), (int)((x >> 2) & kLow2), (int)((x >> 4) & kLow2), (int)((x >> 6) & kLow2)};
+          bf[h][nt] = v4i{(int)signed_codes(x, 0), (int)signed_codes(x, 1), (int)signed_codes(x, 2),
+                          (int)signed_codes(x, 3)};
         }
-        p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : seed, 0, 0, 0);
+        p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : zero, 0, 0, 0);
         const int ft = u >> 1, fi = (u & 1) * 2;
         acc[fold_row][ft][fi] = __builtin_fmaf((float)prev[ft][fi], prev_sc[ft], acc[fold_row][ft][fi]);
         acc[fold_row][ft][fi + 1] = __builtin_fmaf((float)prev[ft][fi + 1], prev_sc[ft], acc[fold_row][ft][fi + 1]);
@@ -226,29 +218,40 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
       if (mt + 1 < MT) {
         a0 = na0;
         a1 = na1;
-        seed = nseed;
       }
     }
-    side_store(side, fill);
+    scale_store(pending, fill);
   };
 
+  // Prologue: groups 0 and 1 staged, the scales of 0 and 1 in LDS (the wait
+  // of each store leaves the DMA of group 1 and the scale load of group 2 in
+  // flight), the scale of group 2 pending.
+  int scale_a, scale_b;
   {
-    Side s0 = side_load(0);
+    int s0 = scale_load(0);
     dma(0, 0);
-    Side s1 = side_load(min(1, groups - 1));
+    int s1 = scale_load(min(1, groups - 1));
     dma(min(1, groups - 1), 1);
-    side_store(s0, 0);  // waits for all but the DMA of group 1: group 0 is complete
-    side_store(s1, 1);
+    scale_a = scale_load(min(2, groups - 1));
+    scale_store(s0, 0);
+    scale_store(s1, 1);
   }
+  // Unrolled by two so that the pending and the fresh scale swap registers
+  // without a copy: a copy would read a register whose load may not have
+  // landed yet.
   int cur = 0;
-  for (int g = 0; g < groups; ++g) {
-    const int fill = cur == 0 ? 2 : cur - 1;  // (g + 2) % 3
-    step(g, cur, fill);
+  int g = 0;
+  for (; g + 1 < groups; g += 2) {
+    step(g, cur, cur == 0 ? 2 : cur - 1, scale_a, scale_b);  // fill = (g + 2) % 3
+    cur = cur == 2 ? 0 : cur + 1;
+    step(g + 1, cur, cur == 0 ? 2 : cur - 1, scale_b, scale_a);
     cur = cur == 2 ? 0 : cur + 1;
   }
+  if (g < groups) step(g, cur, cur == 0 ? 2 : cur - 1, scale_a, scale_b);
   // No direct-to-LDS load may still be in flight when the block's LDS is
-  // handed to the next block.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // handed to the next block, and the last scale loads (never stored) keep
+  // their registers until they have landed.
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(scale_a), "+v"(scale_b)::"memory");
   fold(MT - 1);
 
   // Epilogue.  y = acc * s_x[t] (+ bias[r]) in the MFMA layout (lane holds
@@ -368,7 +371,6 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
                                                                      float* __restrict__ output, GemmArgs a) {
   constexpr int MT = kSplitTokens / 16;
   __shared__ __align__(16) unsigned char stages[kSplitWaves][2][kSplitStage];
-  __shared__ __align__(16) int seeds[kSplitWaves][2][kSplitTokens];
   __shared__ __align__(16) float row_scales[kSplitWaves][2][kSplitRows];
   static_assert(kSplitWaves * kSplitTokens * kSplitPitch * 4 <= (int)sizeof(stages), "partial tiles fit");
   const int tid = threadIdx.x;
@@ -387,7 +389,6 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   const v4u q8_buf = wide_buffer(q8, (long long)a.m * q8_stride);
   const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
   const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
-  const v4u x_buf = wide_buffer(a.xsum_in, (long long)a.m * chunks * 4);
 
   // A piece j of a lane: slot j*64 + lane = token 8j + (lane >> 3), piece
   // (lane & 7) ^ swz(token), where swz(8j + (lane >> 3)) = (lane >> 3) ^ (j & 1).
@@ -400,7 +401,6 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   }
   const int a_step = 8 * q8_stride;  // next DMA round: 8 tokens on
   const int b_off = (row0 + lane) * a.row_bytes;
-  const int x_off0 = (token0 + lane) * chunks * 4, x_off1 = (token0 + 64 + lane) * chunks * 4;
   const int s_off = (row0 + lane) * a.groups * 2;
 
   auto dma = [&](int g, int stage) {
@@ -414,26 +414,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
 #pragma unroll
     for (int j = 0; j < 2; ++j) dma16(w_buf, base + kSplitTokens * 128 + j * 64 * 16, b_off + j * 16, g * 32);
   };
-  struct Side {
-    int x00, x01, x10, x11, s;
-  };
-  auto side_load = [&](int g) {
-    const bool second_live = 2 * g + 1 < chunks;
-    Side r;
-    r.x00 = load_b32(x_buf, x_off0, g * 8);
-    r.x01 = load_b32(x_buf, second_live ? x_off0 + 4 : kPast, g * 8);
-    r.x10 = load_b32(x_buf, x_off1, g * 8);
-    r.x11 = load_b32(x_buf, second_live ? x_off1 + 4 : kPast, g * 8);
-    r.s = load_u16(s_buf, s_off, g * 2);
-    return r;
-  };
-  // Every load of the wave retired: the side values arrived and the stage
-  // just filled is complete.
-  auto side_store = [&](Side& r, int stage) {
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(r.x00), "+v"(r.x01), "+v"(r.x10), "+v"(r.x11), "+v"(r.s)::"memory");
-    seeds[wave][stage][lane] = -(r.x00 + r.x01);
-    seeds[wave][stage][64 + lane] = -(r.x10 + r.x11);
-    row_scales[wave][stage][lane] = h2f((uint16_t)r.s);
+  // The row scale of a group (lane: row lane of the tile), written to LDS as
+  // fp32 once every load of the wave has retired: the scale arrived and the
+  // stage just filled is complete.
+  auto scale_load = [&](int g) { return load_u16(s_buf, s_off, g * 2); };
+  auto scale_store = [&](int& r, int stage) {
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(r)::"memory");
+    row_scales[wave][stage][lane] = h2f((uint16_t)r);
   };
 
   float acc[MT][4][4];
@@ -453,9 +440,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   const int b_read = ((kb >> 1) * kSplitRows + col) * 16 + (kb & 1) * 8;
 
   auto step = [&](int cur, int fill, int g_fill) {
-    Side side = side_load(g_fill);
+    int scale = scale_load(g_fill);
     dma(g_fill, fill);
     const unsigned char* base = stages[wave][cur];
+    const v4i zero = {0, 0, 0, 0};
     uint2 w[4];
     float sc[4];
 #pragma unroll
@@ -463,20 +451,19 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
       w[nt] = *reinterpret_cast<const uint2*>(base + kSplitTokens * 128 + b_read + nt * 16 * 16);
       sc[nt] = row_scales[wave][cur][col + nt * 16];
     }
-    auto operands = [&](int mt, v4i& a0, v4i& a1, v4i& seed) {
+    auto operands = [&](int mt, v4i& a0, v4i& a1) {
       const int t = mt * 16 + col;
       const unsigned char* arow = base + t * 128;
       a0 = *reinterpret_cast<const v4i*>(arow + (((2 * kb) ^ a_swizzle(t)) * 16));
       a1 = *reinterpret_cast<const v4i*>(arow + (((2 * kb + 1) ^ a_swizzle(t)) * 16));
-      seed = *reinterpret_cast<const v4i*>(&seeds[wave][cur][mt * 16 + 4 * kb]);
     };
-    v4i a0, a1, seed;
-    operands(0, a0, a1, seed);
+    v4i a0, a1;
+    operands(0, a0, a1);
     v4i bf[2][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      v4i na0, na1, nseed;
-      if (mt + 1 < MT) operands(mt + 1, na0, na1, nseed);
+      v4i na0, na1;
+      if (mt + 1 < MT) operands(mt + 1, na0, na1);
       const int fold_row = mt == 0 ? MT - 1 : mt - 1;
       v4i p[4];
 #pragma unroll
@@ -484,9 +471,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
         const int h = u >> 2, nt = u & 3;
         if (mt == 0) {
           const unsigned x = h ? w[nt].y : w[nt].x;
-          bf[h][nt] = v4i{(int)(x & kLow2), (int)((x >> 2) & kLow2), (int)((x >> 4) & kLow2), (int)((x >> 6) & kLow2)};
+          bf[h][nt] = v4i{(int)signed_codes(x, 0), (int)signed_codes(x, 1), (int)signed_codes(x, 2),
+                          (int)signed_codes(x, 3)};
         }
-        p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : seed, 0, 0, 0);
+        p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : zero, 0, 0, 0);
         const int ft = u >> 1, fi = (u & 1) * 2;
         acc[fold_row][ft][fi] = __builtin_fmaf((float)prev[ft][fi], prev_sc[ft], acc[fold_row][ft][fi]);
         acc[fold_row][ft][fi + 1] = __builtin_fmaf((float)prev[ft][fi + 1], prev_sc[ft], acc[fold_row][ft][fi + 1]);
@@ -501,17 +489,16 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
       if (mt + 1 < MT) {
         a0 = na0;
         a1 = na1;
-        seed = nseed;
       }
     }
-    side_store(side, fill);
+    scale_store(scale, fill);
   };
 
   if (g_begin < g_end) {
     {
-      Side s0 = side_load(g_begin);
+      int s0 = scale_load(g_begin);
       dma(g_begin, 0);
-      side_store(s0, 0);
+      scale_store(s0, 0);
     }
     int cur = 0;
     for (int g = g_begin; g < g_end; ++g) {

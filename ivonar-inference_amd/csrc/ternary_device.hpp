@@ -26,6 +26,14 @@ constexpr unsigned kLow2 = 0x03030303u;
 enum Mode : int { kPlain = 0, kNorm = 1, kAttn = 2 };
 enum Epi : int { kStore = 0, kResidual = 1, kSiluPair = 2, kPartials = 3 };
 
+constexpr unsigned kSignedLut = 0x000100FFu;  // v_perm table: code 0 -> -1, 1 -> 0, 2 -> +1
+
+// Code field k (inputs 4b + k of bytes b = 0..3) of a packed word as four
+// signed int8 weights (-1, 0, +1): one v_perm_b32 table lookup per four codes.
+__device__ __forceinline__ unsigned signed_codes(unsigned w, int k) {
+  return __builtin_amdgcn_perm(0u, kSignedLut, (w >> (2 * k)) & kLow2);
+}
+
 __device__ __forceinline__ float h2f(uint16_t bits) {
   _Float16 h;
   __builtin_memcpy(&h, &bits, 2);
