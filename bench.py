@@ -269,10 +269,14 @@ def validate_throughput(matrices, stream) -> dict:
     return {"GBps": round(total / seconds / 1e9, 1), "bytes": total, "us_per_operand": round(seconds / len(operands) * 1e6, 2)}
 
 
-def time_calls(call, stream, calls_per_graph: int, replays: int, warmup: int = 2) -> float:
+def time_calls(call, stream, calls_per_graph: int, replays: int, warmup: int = 2, warm_ms: float = 0.0) -> float:
     """Seconds per call: `calls_per_graph` back-to-back calls recorded in one HIP graph, so that the time of
-    a short kernel is not the host's graph-launch time."""
+    a short kernel is not the host's graph-launch time.  With `warm_ms`, the graph is first replayed for about
+    that long (sustained MFMA work runs slower for its first ~20 ms on a fresh box)."""
     graph = graph_of(lambda: [call() for _ in range(calls_per_graph)], stream)
+    if warm_ms > 0:
+        estimate = time_graph(graph, 2, 1)
+        warmup = max(warmup, int(warm_ms * 1e-3 / max(estimate, 1e-6)) + 1)
     return time_graph(graph, replays, warmup) / calls_per_graph
 
 
@@ -478,7 +482,10 @@ def m_sweep(device, stream) -> dict:
         x = torch.from_numpy(synthetic.student_t(rng, (m, k))).to(device)
         q8, xsum, sx = ops.quantize_rows(x)
         out = torch.empty((m, n), dtype=torch.float32, device=device)
-        t_gemm = time_calls(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream, 20 if m <= 128 else 4, 10)
+        # Long prompts: about 25 ms of the same calls before the timed replays (the first 20 ms of
+        # sustained MFMA load on a fresh box run up to 20% slower than the steady state).
+        t_gemm = time_calls(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream, 20 if m <= 128 else 4, 10,
+                            warm_ms=25.0 if m >= 512 else 0.0)
         entry = {"gemm_us": round(t_gemm * 1e6, 3), "gemm_TOPS": round(2 * m * n * k / t_gemm / 1e12, 2)}
         if m <= 16:
             rows = [(q8[i], xsum[i], sx[i:i + 1], out[i]) for i in range(m)]
@@ -493,8 +500,8 @@ def m_sweep(device, stream) -> dict:
                 crossover = m
         table[str(m)] = entry
     return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover,
-            "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph; gemm_us for M <= 16 "
-                    "is the token GEMV (K a multiple of 256)"}
+            "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph, M >= 512 after 25 ms "
+                    "of the same calls; gemm_us for M <= 16 is the token GEMV (K a multiple of 256)"}
 
 
 def stress_tokens(matrices, stress, stream, replays: int) -> dict:
@@ -654,7 +661,8 @@ def main() -> None:
                     ops.gemm(mat, q, x, s_, out=o)
 
             t_tiles = time_calls(tiled, stream, max(1, 64 // len(tiles)), 10)
-            t_one = time_calls(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream, 20 if length <= 128 else 4, 10)
+            t_one = time_calls(lambda: ops.gemm(mat, q8, xsum, sx, out=out), stream, 20 if length <= 128 else 4, 10,
+                               warm_ms=25.0 if length >= 512 else 0.0)
             ops_count = 2 * length * layer.rows * k
             shape[str(length)] = {"tiles_us": round(t_tiles * 1e6, 3), "tiles_TOPS": round(ops_count / t_tiles / 1e12, 2),
                                   "one_launch_us": round(t_one * 1e6, 3),

@@ -604,7 +604,12 @@ int gemm_wide_tokens(int m, int rows, int n) {
   const long long row_blocks = ceil_div(rows, 256);
   if (ceil_div(n, kGroup) >= 16) {
     const bool fits = WideTile<8, 4>::kLdsBytes <= max_lds_per_block();
-    return fits && row_blocks * ceil_div(m, 128) >= 192 ? 128 : 0;
+    if (fits && row_blocks * ceil_div(m, 128) >= 192) return 128;
+    // Too few 128-token tiles: 64-token tiles beat the split-K kernel once
+    // they give 192 blocks (K=4096 -> N=14336 at M=256: 32.4 against 35.2 us;
+    // K=4096 -> N=4096 at M=1024: 35.1 against 37.4 us).
+    const bool fits64 = WideTile<4, 4>::kLdsBytes <= max_lds_per_block();
+    return fits64 && row_blocks * ceil_div(m, 64) >= 192 ? 64 : 0;
   }
   const bool fits = WideTile<4, 4>::kLdsBytes <= max_lds_per_block();
   return fits && row_blocks * ceil_div(m, 64) >= 96 ? 64 : 0;
