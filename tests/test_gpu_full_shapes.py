@@ -151,9 +151,12 @@ def _sweep():
     return _SWEEP
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 64, 128, 512, 2048])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 2048])
 def test_m_sweep_every_row(cuda, oracle, m):
-    """K=4096->N=14336 with the sweep's statistics; every output row of every token bit-exact."""
+    """K=4096->N=14336 with the sweep's statistics; every output row of every token bit-exact.
+
+    M=256 runs the 64-token long-prompt tiles (the 128-token grid has 112 blocks), M=512 and 2048
+    the 128-token tiles, M=128 the split-K kernel."""
     from ivonar_amd import ops, runtime
 
     print(f"m sweep m={m}", flush=True)
@@ -168,6 +171,10 @@ def test_m_sweep_every_row(cuda, oracle, m):
     assert_bits_equal(to_np(dsx), sx, "token scales")
     y = to_np(ops.gemm(matrix, dq8, dxsum, dsx))
     splits = runtime.gemm_plan(m, rows, k)
+    if m in (256, 512, 2048):
+        assert splits == 1, "long-prompt tiles (one fmaf chain per output)"
+    if m == 128:
+        assert splits == 4, "split-K kernel"
     q = T.q8_linear(q8, k)
     expected = finish_all_rows(oracle, 1, splits, T.EPI_STORE, codes, q, scale_bits, sx, None,
                                np.zeros((m, rows), np.float32), k, rows)
