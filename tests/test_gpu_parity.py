@@ -717,6 +717,32 @@ def test_gemm_wide_128_token_tiles_epilogues(cuda, oracle, epilogue):
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
+# 64-token tiles at 2048 inputs and more: 850 tokens x 6144 rows give 168 blocks of 128 tokens (too
+# few) and 336 of 64 tokens, so the long-prompt kernel runs 64-token tiles over 16 groups rather than
+# the split-K kernel.  A ragged last token tile, bias, all three epilogues, every token.
+@pytest.mark.parametrize("epilogue", ["store", "residual", "silu_pair"])
+def test_gemm_wide_64_token_tiles_long_k(cuda, oracle, epilogue):
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng({"store": 81, "residual": 82, "silu_pair": 83}[epilogue])
+    m, k, rows = 850, 2048, 6144
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    assert runtime.gemm_plan(m, rows, k) == 1
+    width = rows // 2 if epilogue == "silu_pair" else rows
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    epi = {"store": T.EPI_STORE, "residual": T.EPI_RESIDUAL, "silu_pair": T.EPI_SILU_PAIR}[epilogue]
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, 1, epi, base.copy(), stride)
+    assert_bits_equal(to_np(out), expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
+
+
 # Long prompts with few output rows run the split-K kernel (four waves per 128 x 64 tile, each a
 # contiguous quarter of the groups, added in order): its plan reports 4 splits.  Ragged tokens and
 # rows, an odd chunk count with a group count not divisible by four, bias, and both epilogues.
