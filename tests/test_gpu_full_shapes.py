@@ -11,6 +11,9 @@
   activations, M in {1, 2, 4, 8, 16, 32, 64, 128, 512, 2048}: every output row of the token GEMM
   bit-exact against the oracle's split order (from exact partials), and the pre-quantized GEMV for
   single tokens.
+* The prefill shapes K=1024->N=4096 and K=4096->N=1024 with the bench's activations (N(0,1), 1% of the
+  channels scaled x20), prompts of 32, 128 and 2048 tokens as one launch and as 32-token tiles: every
+  output row bit-exact in each launch's own order.
 * The secondary boundary ``TernaryLinear.forward`` (reference quantization.py:177-178) at M=1 and M=37.
 """
 
@@ -219,3 +222,37 @@ def test_ternary_linear_forward(cuda, oracle, m):
         truth = T.truth_fp64(oracle.group_partials(q8[t], xsum[t], packed, rows, k), T.half_bits_to_float(scale_bits),
                              sx[t], b)
         assert_within(y[t], truth, what=f"token {t} vs fp64 truth")
+
+
+@pytest.mark.parametrize("shape", [(1024, 4096), (4096, 1024)])
+@pytest.mark.parametrize("length", [32, 128, 2048])
+def test_prefill_outlier_channels_every_row(cuda, oracle, shape, length):
+    """Prompts with the bench's outlier channels, as one launch and as the reference's 32-token tiles."""
+    import torch
+    from ivonar_amd import ops, runtime, synthetic
+
+    k, rows = shape
+    print(f"prefill {k}->{rows} length={length}", flush=True)
+    rng = np.random.default_rng(40 + length + k)
+    codes, packed, scale_bits, _ = big_layer(rng, rows, k)
+    x = synthetic.prefill_activations(rng, length, k)
+    matrix = device_matrix(packed, scale_bits, k, device=cuda)
+    dq8, dxsum, dsx = ops.quantize_rows(_t(x, cuda))
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    assert_bits_equal(to_np(dq8), q8, "q8")
+    assert_bits_equal(to_np(dsx), sx, "token scales")
+    q = T.q8_linear(q8, k)
+
+    def expected(lo, hi):
+        splits = runtime.gemm_plan(hi - lo, rows, k)
+        return finish_all_rows(oracle, 1, splits, T.EPI_STORE, codes, q[lo:hi], scale_bits, sx[lo:hi], None,
+                               np.zeros((hi - lo, rows), np.float32), k, rows)
+
+    y = to_np(ops.gemm(matrix, dq8, dxsum, dsx))
+    assert_bits_equal(y, expected(0, length), f"one launch of {length} tokens")
+    tiles = torch.empty((length, rows), dtype=torch.float32, device=cuda)
+    for lo in range(0, length, 32):
+        ops.gemm(matrix, dq8[lo:lo + 32], dxsum[lo:lo + 32], dsx[lo:lo + 32], out=tiles[lo:lo + 32])
+    tiled = to_np(tiles)
+    for lo in range(0, length, 32):
+        assert_bits_equal(tiled[lo:lo + 32], expected(lo, lo + 32), f"32-token tile at {lo}")
