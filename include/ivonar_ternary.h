@@ -39,28 +39,29 @@ extern "C" {
 
 /* ---------------------------------------------------------------- set-up */
 
-/* Allocates the device's scratch: the activation row a GEMV quantizes when
- * its rows are longer than the fused limit, and the 16 MB of fp32 wave
- * chains of a K-sliced token GEMM (1..16 tokens whose q8 rows exceed LDS).
- * Besides it, every stream (up to 32 per device) that makes such a call
- * outside graph capture gets a scratch of its own on its first call, so
- * eager calls on different streams never share one; a call under capture
- * uses its stream's scratch if it has one, else the device's.  Call once per
- * device outside graph capture; replaces the reference's compile_module
- * set-up step (kernels/runtime.py:301-324).  Calls with the device current.
- * Calling it again clears the GEMV's launch counters of every scratch of the
- * device (see the decode GEMV below), with no call of the device in flight. */
+/* Allocates the device's scratch: the activation row a GEMV quantizes in a
+ * launch of its own (rows longer than 4096 inputs that the GEMV does not
+ * quantize itself: NORM and ATTN rows, unaligned PLAIN rows, rows above
+ * 32768 inputs), the 16 MB of fp32 wave chains of a K-sliced token GEMM
+ * (1..16 tokens whose q8 rows exceed LDS) and the argmax's block count.
+ * Besides it, every stream that makes such a call outside graph capture
+ * gets a scratch of its own (about 17 MB, kept until the process ends) on
+ * its first call, so eager calls on different streams never share one; a
+ * call under capture uses its stream's scratch if it has one, else the
+ * device's.  The null stream and hipStreamPerThread each use one scratch,
+ * whatever thread calls.  Call once per device outside graph capture;
+ * replaces the reference's compile_module set-up step
+ * (kernels/runtime.py:301-324).  Calls with the device current.  Calling it
+ * again clears the argmax counts of every scratch of the device, with no
+ * call of the device in flight. */
 hipError_t ivonar_init(int device);
 
 /* Process-wide values the reference passes as -D defines to NVRTC
  * (kernel_decoder.py:215, ternary.cu:1-46): "HEAD_DIM" (ATTN prologue head
  * width, default 64), "TILE" (token rows of quantize_tile_*, default 32),
  * "MAX_CHUNKS" (caller q8 capacity, default 70), "MAX_TOPK" (largest top-k
- * of sample_token, 1..1024, default 256).  With no reference counterpart,
- * "GEMV_WAIT_SPINS" (0 or more, default 2^20) bounds how often a block of a
- * GEMV that quantizes its row in-launch polls for the row before it gives up
- * (its outputs are then NaN); tests lower it to exercise that path.  Unknown
- * names and out-of-range values return hipErrorInvalidValue. */
+ * of sample_token, 1..1024, default 256).  Unknown names and out-of-range
+ * values return hipErrorInvalidValue. */
 hipError_t ivonar_define(const char* name, int value);
 
 const char* ivonar_error_string(hipError_t status);
@@ -83,16 +84,14 @@ int ivonar_gemm_plan(int m, int rows, int n);
  * [heads, splits, HEAD_DIM+2] first; prequant reads q8_in/xsum_in/scale_in.
  * Epilogue: store, residual (output[r] += y), silu pair (interleaved
  * gate/up rows; output[r/2] = silu(y[r]) * y[r+1], rows even).
- * A row longer than 4096 inputs is quantized into the stream's scratch (see
- * ivonar_init) and then read by the GEMV: a 16-byte aligned PLAIN row of up
- * to 32768 inputs by the first blocks of the GEMV launch itself (the other
- * blocks wait for it through counters in the scratch that every launch
- * leaves at zero), other rows by a separate quantizer launch.  Calls in one
- * stream order are safe, and so are eager calls on different streams; graphs
- * whose captured calls share a scratch (captured on one stream, or on
- * streams that had none) race when replayed at once: their outputs are
- * undefined, a launch may wait up to about a second (its outputs then NaN),
- * and the counters can be left set, which ivonar_init clears. */
+ * A 16-byte aligned PLAIN row of 4097..32768 inputs is quantized by every
+ * block of the GEMV launch itself, into its own shared memory (no scratch,
+ * no waiting between blocks); other rows longer than 4096 inputs are
+ * quantized into the stream's scratch (see ivonar_init) by a separate
+ * quantizer launch and then read by the GEMV.  Calls in one stream order are
+ * safe, and so are eager calls on different streams; graphs whose captured
+ * calls share a scratch (captured on one stream, or on streams that had
+ * none) give undefined outputs for those calls when replayed at once. */
 #define IVONAR_GEMV_ARGS                                                                                    \
   const float *input, const float *aux, const int8_t *q8_in, const int32_t *xsum_in, const float *scale_in, \
       const uint8_t *packed, const uint16_t *scales, const float *bias, float *output, int rows, int n,      \

@@ -3,7 +3,9 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "ivonar_ternary.h"
 #include "internal.hpp"
@@ -21,18 +23,14 @@ namespace {
 constexpr int kMaxDevices = 64;
 constexpr int kScratchChunks = 16384;  // rows up to 1,048,576 inputs
 // Scratch per (device, stream): the device's own (set up by ivonar_init, used
-// by the null stream, by calls under graph capture on a stream that has none
-// yet, and past kMaxStreamScratch streams), and one per stream that calls
-// outside capture, so that eager calls on different streams never share one.
-constexpr int kMaxStreamScratch = 32;
-struct StreamScratch {
-  hipStream_t stream = nullptr;
-  Scratch scratch;
-};
+// by the null stream and by calls under graph capture on a stream that has
+// none yet), and one per stream that calls outside capture, so that eager
+// calls on different streams never share one.  Entries are kept until the
+// process ends (a stream handle that HIP hands out again after its stream
+// was destroyed finds the same scratch, which its predecessor no longer uses).
 std::mutex g_scratch_lock;
 Scratch g_scratch[kMaxDevices];
-StreamScratch g_stream_scratch[kMaxDevices][kMaxStreamScratch];
-int g_stream_scratch_count[kMaxDevices] = {0};
+std::map<std::pair<int, uintptr_t>, Scratch> g_stream_scratch;  // node-based: entries never move
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -48,7 +46,7 @@ hipError_t allocate_scratch(Scratch& s) {
   if (status == hipSuccess) status = hipMalloc(&scale, 256);
   if (status == hipSuccess) status = hipMalloc(&partials, (size_t)kTokenPartialFloats * sizeof(float));
   if (status == hipSuccess) status = hipMalloc(&sync, kSyncBytes);
-  if (status == hipSuccess) status = hipMemset(sync, 0, kSyncBytes);  // the GEMV's counters start at zero
+  if (status == hipSuccess) status = hipMemset(sync, 0, kSyncBytes);  // the argmax's block count starts at zero
   if (status != hipSuccess) {
     if (q8) (void)hipFree(q8);
     if (xsum) (void)hipFree(xsum);
@@ -117,13 +115,13 @@ hipError_t gemv_entry(hipStream_t stream, int mode, int epi, bool prequant, cons
 }
 
 // ------------------------------------------------ no-allocation GEMV scratch
-// Rows longer than the fused limit are quantized before the GEMV; the
-// no-allocation entry point quantizes them into this array (q8, chunk sums,
-// token scale) instead of the scratch the library allocates, always in a
-// launch of its own (no counters: nothing in the array must start at zero).
-// Each device
-// holds its own copy at its own address, looked up once per device with
-// hipGetSymbolAddress; host code uses only that address.
+// Rows longer than the fused limit that the long-row GEMV does not quantize
+// itself (unaligned inputs) are quantized before the GEMV; the no-allocation
+// entry point quantizes them into this array (q8, chunk sums, token scale)
+// instead of the scratch the library allocates, in a launch of its own
+// (nothing in the array must start at zero).  Each device holds its own copy
+// at its own address, looked up once per device with hipGetSymbolAddress;
+// host code uses only that address.
 constexpr int kStaticChunks = 512;  // rows up to 32768 inputs
 constexpr size_t kStaticQ8Bytes = (size_t)kStaticChunks * kChunk;
 constexpr size_t kStaticScaleOffset = kStaticQ8Bytes + (size_t)kStaticChunks * sizeof(int32_t);
@@ -146,7 +144,7 @@ hipError_t static_scratch(Scratch** out) {
     unsigned char* bytes = static_cast<unsigned char*>(base);
     s.xsum = reinterpret_cast<int32_t*>(bytes + kStaticQ8Bytes);
     s.scale = reinterpret_cast<float*>(bytes + kStaticScaleOffset);
-    s.sync = nullptr;  // the quantizer runs in a launch of its own
+    s.sync = nullptr;  // no counters: the GEMV uses none, and the argmax takes its own scratch
     s.capacity_chunks = kStaticChunks;
     s.q8 = reinterpret_cast<int8_t*>(bytes);
   }
@@ -197,11 +195,13 @@ hipError_t init_device(int device) {
     if (status != hipSuccess) return status;
   }
   status = allocate_scratch(g_scratch[device]);
-  // The in-launch quantizer's counters are zero between launches; clearing them
-  // here recovers a scratch that overlapping launches left set.
+  // The argmax's block count is zero between launches; clearing it here
+  // recovers a scratch that overlapping graph replays left set.
   if (status == hipSuccess) status = hipMemset(g_scratch[device].sync, 0, kSyncBytes);
-  for (int i = 0; status == hipSuccess && i < g_stream_scratch_count[device]; ++i)
-    status = hipMemset(g_stream_scratch[device][i].scratch.sync, 0, kSyncBytes);
+  for (auto it = g_stream_scratch.lower_bound({device, 0}); status == hipSuccess && it != g_stream_scratch.end() &&
+                                                             it->first.first == device;
+       ++it)
+    status = hipMemset(it->second.sync, 0, kSyncBytes);
   if (current != device) (void)hipSetDevice(current);
   return status;
 }
@@ -217,20 +217,17 @@ hipError_t scratch_for_stream(hipStream_t stream, Scratch** out) {
   const bool capturing = capture != hipStreamCaptureStatusNone;
   std::lock_guard<std::mutex> guard(g_scratch_lock);
   if (stream != nullptr) {
-    StreamScratch* table = g_stream_scratch[device];
-    const int count = g_stream_scratch_count[device];
-    for (int i = 0; i < count; ++i) {
-      if (table[i].stream == stream) {
-        *out = &table[i].scratch;
-        return hipSuccess;
-      }
+    const std::pair<int, uintptr_t> key{device, reinterpret_cast<uintptr_t>(stream)};
+    auto found = g_stream_scratch.find(key);
+    if (found != g_stream_scratch.end()) {
+      *out = &found->second;
+      return hipSuccess;
     }
-    if (!capturing && count < kMaxStreamScratch) {
-      status = allocate_scratch(table[count].scratch);
+    if (!capturing) {
+      Scratch fresh;
+      status = allocate_scratch(fresh);
       if (status != hipSuccess) return status;
-      table[count].stream = stream;
-      g_stream_scratch_count[device] = count + 1;
-      *out = &table[count].scratch;
+      *out = &g_stream_scratch.emplace(key, fresh).first->second;
       return hipSuccess;
     }
   }
@@ -252,12 +249,7 @@ extern "C" {
 hipError_t ivonar_init(int device) { return init_device(device); }
 
 hipError_t ivonar_define(const char* name, int value) {
-  if (name == nullptr) return hipErrorInvalidValue;
-  if (strcmp(name, "GEMV_WAIT_SPINS") == 0 && value >= 0) {
-    defines().wait_spins = value;
-    return hipSuccess;
-  }
-  if (value <= 0) return hipErrorInvalidValue;
+  if (name == nullptr || value <= 0) return hipErrorInvalidValue;
   if (strcmp(name, "HEAD_DIM") == 0) defines().head_dim = value;
   else if (strcmp(name, "TILE") == 0) defines().tile = value;
   else if (strcmp(name, "MAX_CHUNKS") == 0) defines().max_chunks = value;

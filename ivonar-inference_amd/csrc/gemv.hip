@@ -27,12 +27,11 @@
 // Activations.  For rows up to kFusedLimit inputs the block quantizes the
 // fp32 input itself into LDS (the fused prologue of gemv_plain_*,
 // gemv_norm_*, gemv_attn_*), quad-planar (quad w of chunk u at int4 index
-// w*C + u), and each lane then keeps its chunks' quads in registers.  Longer
-// rows are quantized once into the stream's scratch: PLAIN rows (16-byte
-// aligned) of 4097..32768 inputs by the first blocks of the long-row GEMV
-// launch itself while the other blocks load their first weights
-// (quantize_publish / wait_published), other rows by the quantizer in a launch
-// of its own.  Pre-quantized activations are read by each lane straight from
+// w*C + u), and each lane then keeps its chunks' quads in registers.  PLAIN
+// rows (16-byte aligned) of 4097..32768 inputs are quantized by every block
+// of the long-row GEMV itself into its LDS (quantize_row_split), while its
+// first weights stream; other long rows are quantized once into the stream's
+// scratch by the quantizer, in a launch of its own.  Pre-quantized activations are read by each lane straight from
 // global memory when a row needs one step per lane (no LDS: the q8 row is
 // small and stays in the caches for every block), else copied to LDS once
 // per block (gemv_rows_kernel for 2..8 steps, the rolling layout above).
@@ -64,9 +63,6 @@ struct GemvShape {
   int lanes, lane_shift, iters;
   int exact;  // every lane's chunks exist (C is a multiple of lanes): no per-chunk masks
   int split;  // the activations are nibble-split quads (the two-pass path's own scratch)
-  int qblocks;  // > 0: qblocks blocks quantize the PLAIN row into q8_out first (in-launch quantizer)
-  int qstride;  // those blocks: 0, qstride, 2*qstride, ... (slice blockIdx / qstride)
-  int spins;    // polls before a waiting block gives up (GEMV_WAIT_SPINS)
 };
 
 struct GemvPtrs {
@@ -75,12 +71,6 @@ struct GemvPtrs {
   const int8_t* q8_in;
   const int32_t* xsum_in;
   const float* scale_in;
-  // In-launch quantizer (qblocks > 0): where the row goes (q8_in, xsum_in and
-  // scale_in point at the same buffers) and the scratch's counters and flags.
-  int8_t* q8_out;
-  int32_t* xsum_out;
-  float* scale_out;
-  unsigned* sync;
 };
 
 // One pipeline item's loads: weights of NJ steps for kRows rows (w[j][0] of
@@ -369,17 +359,6 @@ __device__ __forceinline__ int load_u16(const void* p) {
   asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
   return r;
 }
-// Device-coherent (sc1) forms, for the row the launch publishes itself.
-__device__ __forceinline__ v4i32 load_b128_sc1(const void* p) {
-  v4i32 r;
-  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
-  return r;
-}
-__device__ __forceinline__ int load_b32_sc1(const void* p) {
-  int r;
-  asm volatile("global_load_dword %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
-  return r;
-}
 // The same loads at a constant byte offset (-4096..4095) from p.
 template <int OFF>
 __device__ __forceinline__ v4i32 load_b128_at(const void* p) {
@@ -396,108 +375,15 @@ __device__ __forceinline__ int load_u16_at(const void* p) {
   return r;
 }
 
-// In-launch quantization of a PLAIN row of 4097..32768 inputs (the long-row
-// kernel, gemv_rows_kernel<..., QUANT = true>).  Blocks
-// s*qstride (s < Q = qblocks, at most 16) each quantize slice s of the row into
-// the scratch (nibble-split) and count themselves into `arrive`; the block
-// whose count is the last raises the ready flag of each of 8 block groups.
-// Each block's first thread waits for its group's flag (blockIdx & 7) and the
-// block barrier hands the row to its other threads.
-//
-// Visibility without cache maintenance: every store and load of the
-// published row, of the counters and of the flags is device-coherent (an
-// agent-scope relaxed atomic, or a load or store with the sc1 bit): such an
-// access is performed at the device's coherence point, past the per-XCD L2s,
-// so no write-back (buffer_wbl2) or invalidation (buffer_inv) is needed -
-// both serialize per XCD and cost microseconds when a thousand blocks issue
-// them.  Order comes from completion: a quantizing block waits until all its
-// stores are acknowledged (vmcnt(0) in every thread, then the barrier) before
-// it counts itself, the last block raises the flags after its count has
-// returned, and a waiting block issues its row loads only after it has read
-// its flag.
-//
-// Progress: workgroups are dispatched in the order of their numbers, the
-// quantizing blocks wait only for one another, and every block numbered up
-// to the last of them fits on the device at once (stride 8 is used only when
-// 8*(Q-1) is below the resident block count, else stride 1), so a waiting
-// block never holds the slot a quantizing block needs.  Stride 8 is chosen
-// for speed: blocks are spread over the XCDs round-robin, so all quantizing
-// blocks then run on the XCD that starts the launch first and share its L2
-// copy of the fp32 row (the XCDs start a launch up to about 4 us apart).
-// Eight flags in eight cache lines spread the polling of up to 512 waiting
-// blocks (two per CU).
-//
-// At its end every block counts itself into its group's `done` counter; the
-// block that completes a group counts the group into `top`, and the block
-// that completes `top` sets every counter and flag back to zero, so every
-// launch starts from zero without a memset.  A block counts itself done only
-// after it has passed its wait, and every quantizing block has counted into
-// `arrive` before that, so nothing is counted or raised after the reset.  The
-// wait is bounded (sh.spins polls, 2^20 by default: about a second): a wait
-// that gives up makes the block's outputs NaN instead of hanging the launch.  Two launches
-// that share one scratch must not overlap (stream order or one scratch per
-// stream).
-constexpr int kSyncGroups = 8;
-constexpr int kSyncLineWords = 32;  // one counter or flag per 128-byte line
-constexpr int kArriveLine = 0, kReadyLine = 1, kDoneLine = 1 + kSyncGroups, kTopLine = 1 + 2 * kSyncGroups;
-static_assert((kTopLine + 1) * kSyncLineWords <= kArgmaxCountWord, "the counter lines stop before the argmax count");
-
-__device__ __forceinline__ unsigned* sync_line(unsigned* sync, int line) { return sync + line * kSyncLineWords; }
-
-__device__ __forceinline__ bool quantizes(const GemvShape& sh) {
-  return sh.qblocks > 0 && (int)blockIdx.x % sh.qstride == 0 && (int)blockIdx.x / sh.qstride < sh.qblocks;
+typedef float v4f32 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4f32 load_f128(const void* p) {
+  v4f32 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
 }
-
-// Rows of up to ROUNDS*T*4 inputs take one load round for the row amax.
-template <int T, int ROUNDS>
-__device__ __forceinline__ void quantize_publish(const GemvPtrs& in, const GemvShape& sh, float* slots) {
-  quantize_plain_slice<T, ROUNDS, true>(in.input, sh.n, (int)blockIdx.x / sh.qstride, true, in.q8_out, in.xsum_out,
-                                        in.scale_out, slots);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are performed device-wide
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned before =
-        __hip_atomic_fetch_add(sync_line(in.sync, kArriveLine), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before == (unsigned)sh.qblocks - 1) {
-      for (int j = 0; j < kSyncGroups; ++j)
-        __hip_atomic_store(sync_line(in.sync, kReadyLine + j), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
-// All threads of the block call it; true when the row is published.
-__device__ __forceinline__ bool wait_published(const GemvPtrs& in, int spins_limit, int* status) {
-  if (threadIdx.x == 0) {
-    const unsigned* ready = sync_line(in.sync, kReadyLine + (int)(blockIdx.x & (kSyncGroups - 1)));
-    int ok = 1;
-    for (int spins = 0; __hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++spins) {
-      if (spins >= spins_limit) {
-        ok = 0;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    *status = ok;
-  }
-  __syncthreads();
-  return *status != 0;
-}
-
-// Called by every thread at the end of the block (after its wait).
-__device__ __forceinline__ void retire_block(const GemvPtrs& in) {
-  if (threadIdx.x != 0) return;
-  const unsigned group = blockIdx.x & (kSyncGroups - 1);
-  const unsigned members = (gridDim.x - group + kSyncGroups - 1) / kSyncGroups;
-  const unsigned groups = gridDim.x < (unsigned)kSyncGroups ? gridDim.x : (unsigned)kSyncGroups;
-  if (__hip_atomic_fetch_add(sync_line(in.sync, kDoneLine + (int)group), 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT) != members - 1)
-    return;
-  if (__hip_atomic_fetch_add(sync_line(in.sync, kTopLine), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
-      groups - 1)
-    return;
-  for (int line = 0; line <= kTopLine; ++line)
-    __hip_atomic_store(sync_line(in.sync, line), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// A value u = fma(x, 1/s, 128) at least this far below the next half-integer
+// and above the previous one rounds like x/s + 128 (see quantize_row_split).
+constexpr float kTieGuard = 0.49997f;
 
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): an
 // unrolled loop whose index can feed an immediate operand.
@@ -509,10 +395,104 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// In-launch quantization of a PLAIN row (the long-row kernel with QUANT): every
+// block quantizes the whole row into its own LDS copy, so no block waits for
+// another.  T threads; thread t holds float4 k*T + t of the row (inputs
+// 4f .. 4f + 3 of float4 f, k < X) in xv: coalesced loads.  n is a multiple of
+// 4; the row is zero past n up to its C = `chunks` chunks of 64.  Writes the
+// nibble-split quads (word k of quad w of chunk u at lds_words[(w*C + u)*4 + k],
+// the form split_quad gives) and minus the chunk sums (lds_x[u]) and returns
+// the token scale.  step(k) runs after the k-th float4 is quantized (the
+// caller issues weight loads there).  slots holds T/64 floats.  The LDS
+// writes are not yet waited for.
+//
+// Bit-exact with the quantizer kernels (quantize_plain_slice):
+// scale = max(amax/127, 1e-5) and q = (int)rint(x / scale).  The division is
+// replaced by u = RN(x * inv + 128) with inv = RN(1/scale), q + 128 = rint(u):
+// |x/scale| <= 127 * (1 + 2^-23), so |x*inv - x/scale| <= 127 * 2^-24 and the
+// fma's rounding adds at most 2^-17 (half an ulp below 256), |u - (x/scale + 128)|
+// < 1.6e-5; the correctly rounded quotient is within 2^-18 of x/scale.  When u
+// lies more than 2e-5 from every half-integer, rint(u) - 128 is therefore
+// rint(RN(x/scale)).  Closer values (about 6 in 10^5 inputs, exact ties among
+// them), NaN and infinities take the division itself.
+//
+// Layout: the lanes 4g .. 4g + 3 hold the four float4 of one 16-input quad g;
+// q8 word k of the quad holds inputs 4b + k at byte b, so lane j (= t & 3)
+// forms word j from byte j of each of the four lanes' packed bytes (three DPP
+// quad permutations), then the split word j with the word of lane j ^ 2.  The
+// bytes are biased (b = q + 128 = q ^ 0x80), which keeps the low nibble of q
+// and flips bit 3 of the high one: one XOR with 0x88888888 fixes the split
+// words of high nibbles.
+template <int T, int X, typename Step>
+__device__ __forceinline__ float quantize_row_split(v4f32 (&xv)[X], int n, int chunks, int* lds_words, int* lds_x,
+                                                    float* slots, Step&& step) {
+  const int tid = threadIdx.x;
+  const int n4 = n >> 2;
+  const int j = tid & 3;
+#pragma unroll
+  for (int k = 0; k < X; ++k)
+    if (k * T + tid >= n4) xv[k] = v4f32{0.0f, 0.0f, 0.0f, 0.0f};
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < X; ++k)
+    amax = fmaxf(fmaxf(amax, fmaxf(fabsf(xv[k][0]), fabsf(xv[k][1]))), fmaxf(fabsf(xv[k][2]), fabsf(xv[k][3])));
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) slots[tid >> 6] = amax;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the weight loads stay in flight
+  amax = slots[0];
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) amax = fmaxf(amax, slots[w]);
+  const float scale = fmaxf(amax / 127.0f, 1e-5f);
+  const float inv = 1.0f / scale;
+  const unsigned own_shift = 8 * j;
+  const unsigned shift1 = 8 * (1 ^ j), shift2 = 8 * (2 ^ j), shift3 = 8 * (3 ^ j);
+  const unsigned high_fix = j < 2 ? 0x88888888u : 0u;
+  static_for<X>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int f = k * T + tid;
+    float v[4];
+    bool near = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float u = __builtin_fmaf(xv[k][e], inv, 128.0f);
+      const float r = __builtin_rintf(u);
+      near = near || !(fabsf(u - r) < kTieGuard);
+      v[e] = r;
+    }
+    if (near) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (float)((int)__builtin_rintf(xv[k][e] / scale) + 128);
+    }
+    unsigned packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[0], 0, 0u);
+    packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[1], 1, packed4);
+    packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[2], 2, packed4);
+    packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[3], 3, packed4);
+    // Word j of the quad: byte j of lane 4g + i's bytes at byte i.
+    const unsigned p1 = (unsigned)__builtin_amdgcn_mov_dpp((int)packed4, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+    const unsigned p2 = (unsigned)__builtin_amdgcn_mov_dpp((int)packed4, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+    const unsigned p3 = (unsigned)__builtin_amdgcn_mov_dpp((int)packed4, 0x1B, 0xF, 0xF, false);  // lane ^ 3
+    unsigned word = __builtin_amdgcn_ubfe(packed4, own_shift, 8) << own_shift;
+    word |= __builtin_amdgcn_ubfe(p1, own_shift, 8) << shift1;
+    word |= __builtin_amdgcn_ubfe(p2, own_shift, 8) << shift2;
+    word |= __builtin_amdgcn_ubfe(p3, own_shift, 8) << shift3;
+    const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp((int)word, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+    const unsigned split = split_quad_word(word, partner, j) ^ high_fix;
+    // Chunk sums: the 16 float4 of chunk f / 16 sit in one 16-lane row.
+    const int sum = chunk_lane_sum((int)__builtin_amdgcn_udot4(packed4, 0x01010101u, 0u, false) - 4 * 128);
+    if (f < chunks * 16) {
+      const int g = f >> 2;  // quad g: chunk g / 4, quad g % 4
+      lds_words[(((g & 3) * chunks + (g >> 2)) << 2) + j] = (int)split;
+      if ((tid & 15) == 0) lds_x[f >> 4] = -sum;
+    }
+    step(kc);
+  });
+  return scale;
+}
+
 // Byte offset of gemv_rows_kernel's 16-byte dump slot: past the q8 row and
 // its chunk sums, 16-byte aligned.
 __host__ __device__ constexpr int rows_dump_offset(int chunks) { return (chunks * (kChunk + 4) + 15) & ~15; }
-constexpr int kRowsQuantLds = 64;  // QUANT, after the dump slot: 8 block max slots and the wait status
+constexpr int kRowsQuantLds = 64;  // QUANT, after the dump slot: the 8 waves' row maxima
 constexpr int kRowsBlocksPerCu2 = 2;  // blocks per CU with two steps per row (one above)
 
 // One step of a row pair in flight: the 16 weight bytes of the lane's chunk in
@@ -545,14 +525,13 @@ struct RowStep {
 // order, so a count that leaves only younger loads outstanding proves the
 // step complete; stores only make the waits longer.  (Compiled loads would
 // get compiler-placed waits, which at this depth drain every load in flight
-// at loop joins.)  The activation copy's loads go out first and are waited for with
-// the first row pair's weights still in flight; with QUANT (the launch
-// quantizes the row itself) they go out after the first weights, once the row
-// is published, device-coherent, and are waited for with vmcnt(0).  The build
-// disassembles
-// these kernels and checks every VGPR access against the loads in flight
-// (asmcheck.py).  Lane layout and fp32 order are those of gemv_kernel
-// (orc_gemv_pairs).
+// at loop joins.)  The activation row's loads (the q8 copy, or with QUANT the
+// fp32 row the block quantizes itself) go out first, with the first step of
+// weights behind them; the other steps of the first row pair go out between
+// the pieces of the copy or of the quantization (see the prologue).  The
+// build disassembles these kernels and checks every VGPR access against the
+// loads in flight (asmcheck.py).  Lane layout and fp32 order are those of
+// gemv_kernel (orc_gemv_pairs).
 template <int EPI, int STEPS, bool EXACT, bool QUANT>
 __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
@@ -624,54 +603,72 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     base = load_b32(EPI == kResidual ? static_cast<const void*>(output + own) : static_cast<const void*>(packed));
   };
 
-  v4i32 qv[kCopy];
-  int xv;
   RowStep st[STEPS];
   int it;
   PairBase pb;
+  // The activation row goes out first, with one step of weights behind it;
+  // the other steps are issued one by one between the pieces of the copy or
+  // of the quantization.  (Memory serves the row's loads among the weight
+  // bytes in flight, not ahead of them: with a row pair's 14 KB per wave
+  // already requested, 28 KB of q8 take about 3 us to arrive instead of
+  // 0.5 us.  And a wave that issues many loads at once stalls until the
+  // CU's memory pipeline accepts them, so work placed after a burst of loads
+  // waits for it.)
+  it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));  // wave-uniform
+  pb = pair_base(it);
   if constexpr (!QUANT) {
+    v4i32 qv[kCopy];
+    int xv;
 #pragma unroll
     for (int k = 0; k < kCopy; ++k) qv[k] = load_b128(gq + min(k * kBlock + tid, words - 1));
     xv = load_b32(in.xsum_in + min(tid, chunks - 1));
-    it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));  // wave-uniform
-    pb = pair_base(it);
-    static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
-    asm volatile("s_waitcnt vmcnt(%5)"
-                 : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv)
-                 : "n"(3 * STEPS)
-                 : "memory");
+    issue_step(st[0], pb, it, std::integral_constant<int, 0>{});
+    // The copy's loads are older than step 0's three.
+    asm volatile("s_waitcnt vmcnt(3)" : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv) : : "memory");
+    int4* dump = reinterpret_cast<int4*>(lds_raw + rows_dump_offset(chunks));
+    static_for<kCopy>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      const int e = k * kBlock + tid;
+      // Caller q8 quads are split here, once per block (the scratch's arrive split).
+      const int4 quad = __builtin_bit_cast(int4, qv[k]);
+      const int4 stored = sh.split ? quad : split_quad(quad);
+      *(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = stored;
+      if constexpr (k + 1 < STEPS) issue_step(st[k + 1], pb, it, std::integral_constant<int, k + 1>{});
+    });
+    *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = -xv;  // minus the chunk sums
+    static_for<STEPS>([&](auto sc) {
+      if constexpr (decltype(sc)::value > kCopy) issue_step(st[sc], pb, it, sc);
+    });
   } else {
-    // The quantizing blocks publish their slices first; every block issues its
-    // first row pair's weights, waits for the row and then copies it
-    // (device-coherent loads: q8, chunk sums and the token scale).
+    // The block quantizes the PLAIN row itself (quantize_row_split), issuing
+    // one step of weights after every second float4 of the row.
+    constexpr int kX = 2 * STEPS;  // float4 per thread: rows of STEPS * 4096 inputs
+    constexpr int kMid = STEPS <= 2 ? STEPS - 1 : 0;
+    v4f32 xv[kX];
+    const v4f32* x4 = reinterpret_cast<const v4f32*>(in.input);
+    const int n4 = sh.n >> 2;
+#pragma unroll
+    for (int k = 0; k < kX; ++k) xv[k] = load_f128(x4 + min(k * kBlock + tid, n4 - 1));
+    issue_step(st[0], pb, it, std::integral_constant<int, 0>{});
+    // The row's loads are older than step 0's three.
+#pragma unroll
+    for (int k = 0; k < kX; ++k) asm volatile("s_waitcnt vmcnt(3)" : "+v"(xv[k]) : : "memory");
+    // Rows of two steps: step 1 goes out as soon as the row is in.  Longer
+    // rows: steps 1.. go out one after every second float4 of the
+    // quantization (all at once, they stall the wave until the memory
+    // pipeline takes them and hold up the quantization: 16.5 us against
+    // 16.8-18.1 us per K=28672 -> N=8192 call with 1, 2, 3 or 5 of them up
+    // front).
+    static_for<kMid + 1>([&](auto sc) {
+      if constexpr (decltype(sc)::value > 0) issue_step(st[sc], pb, it, sc);
+    });
     float* slots = reinterpret_cast<float*>(lds_raw + rows_dump_offset(chunks) + 16);
-    int* published = reinterpret_cast<int*>(slots + kBlock / 64);
-    // Rows of STEPS*4096 inputs: 2*STEPS float4 of the row amax per thread, one round.
-    if (quantizes(sh)) quantize_publish<kBlock, 2 * STEPS>(in, sh, slots);
-    it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));
-    pb = pair_base(it);
-    static_for<STEPS>([&](auto s) { issue_step(st[s], pb, it, s); });
-    const bool ok = wait_published(in, sh.spins, published);
-#pragma unroll
-    for (int k = 0; k < kCopy; ++k) qv[k] = load_b128_sc1(gq + min(k * kBlock + tid, words - 1));
-    xv = load_b32_sc1(in.xsum_in + min(tid, chunks - 1));
-    int sv = load_b32_sc1(in.scale_in);
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv), "+v"(sv)
-                 :
-                 : "memory");
-    sx = ok ? __int_as_float(sv) : __builtin_nanf("");
+    sx = quantize_row_split<kBlock, kX>(xv, sh.n, chunks, reinterpret_cast<int*>(lds_q), lds_x, slots, [&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k % 2 == 0 && k / 2 + kMid + 1 < STEPS)
+        issue_step(st[k / 2 + kMid + 1], pb, it, std::integral_constant<int, k / 2 + kMid + 1>{});
+    });
   }
-  int4* dump = reinterpret_cast<int4*>(lds_raw + rows_dump_offset(chunks));
-#pragma unroll
-  for (int k = 0; k < kCopy; ++k) {
-    const int e = k * kBlock + tid;
-    // Caller q8 quads are split here, once per block (the scratch's arrive split).
-    const int4 quad = __builtin_bit_cast(int4, qv[k]);
-    const int4 stored = sh.split ? quad : split_quad(quad);
-    *(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = stored;
-  }
-  *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = -xv;  // minus the chunk sums
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   const int4 qr_unused[1][4] = {};
@@ -740,7 +737,6 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     epilogue(acc, row0, b_side, base_side);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // a wave with no row pair still has its first loads out
-  if constexpr (QUANT) retire_block(in);
 }
 
 template <int MODE, int EPI, bool FUSED, int NJ, int LANES, bool EXACT, bool ROLL>
@@ -782,21 +778,15 @@ void launch_rows_as(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, co
 
 template <int EPI, int STEPS>
 void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int /*blocks*/,
-                 size_t /*lds*/) {
+                 size_t /*lds*/, bool quant) {
   const int cus = device_cus();
   // Two steps per row leave room for two blocks per CU (more bytes in flight).
   const int cap = (STEPS == 2 ? kRowsBlocksPerCu2 : 1) * cus;
-  int blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
+  const int blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
   const size_t lds = (size_t)rows_dump_offset((sh.n + kChunk - 1) / kChunk) + 16;
   if constexpr (EPI != kPartials) {
-    if (sh.qblocks > 0) {
-      if (blocks < sh.qblocks) blocks = sh.qblocks;  // the in-launch quantizer's slices
-      // Stride 8 only when every block up to the last quantizing one can be
-      // resident at once (cap blocks are): no waiting block can then hold the
-      // slot a quantizing block needs.
-      GemvShape shape = sh;
-      shape.qstride = blocks >= 8 * sh.qblocks && 8 * (sh.qblocks - 1) < cap ? 8 : 1;
-      launch_rows_as<EPI, STEPS, true>(stream, p, a, shape, blocks, lds + kRowsQuantLds);
+    if (quant) {
+      launch_rows_as<EPI, STEPS, true>(stream, p, a, sh, blocks, lds + kRowsQuantLds);
       return;
     }
   }
@@ -813,7 +803,7 @@ int steps_per_item(int steps) {
 
 template <int MODE, int EPI, bool FUSED>
 hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int blocks,
-                     size_t lds, int steps) {
+                     size_t lds, int steps, bool quant = false) {
   bool launched = false;
   if (steps <= 1) {  // one step per row: q8 in registers
     launched = launch_layout<MODE, EPI, FUSED, 1, false>(stream, p, a, sh, blocks, lds);
@@ -821,13 +811,13 @@ hipError_t launch_nj(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, c
     // Rows of more than one step have 64 lanes (lanes < 64 span a row in one step).
     if (sh.lanes == 64 && steps <= 8) {
       switch (steps) {
-        case 2: launch_rows<EPI, 2>(stream, p, a, sh, blocks, lds); break;
-        case 3: launch_rows<EPI, 3>(stream, p, a, sh, blocks, lds); break;
-        case 4: launch_rows<EPI, 4>(stream, p, a, sh, blocks, lds); break;
-        case 5: launch_rows<EPI, 5>(stream, p, a, sh, blocks, lds); break;
-        case 6: launch_rows<EPI, 6>(stream, p, a, sh, blocks, lds); break;
-        case 7: launch_rows<EPI, 7>(stream, p, a, sh, blocks, lds); break;
-        default: launch_rows<EPI, 8>(stream, p, a, sh, blocks, lds); break;
+        case 2: launch_rows<EPI, 2>(stream, p, a, sh, blocks, lds, quant); break;
+        case 3: launch_rows<EPI, 3>(stream, p, a, sh, blocks, lds, quant); break;
+        case 4: launch_rows<EPI, 4>(stream, p, a, sh, blocks, lds, quant); break;
+        case 5: launch_rows<EPI, 5>(stream, p, a, sh, blocks, lds, quant); break;
+        case 6: launch_rows<EPI, 6>(stream, p, a, sh, blocks, lds, quant); break;
+        case 7: launch_rows<EPI, 7>(stream, p, a, sh, blocks, lds, quant); break;
+        default: launch_rows<EPI, 8>(stream, p, a, sh, blocks, lds, quant); break;
       }
       return hipGetLastError();
     }
@@ -901,9 +891,6 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   // Dead lanes exist when the last step is partial (items never hold dead steps).
   sh.exact = chunks % lanes == 0;
   sh.split = 0;
-  sh.qblocks = 0;
-  sh.qstride = 1;
-  sh.spins = defines().wait_spins;
   const int cus = device_cus();
   const bool roll = !fused && steps > 8;  // the rolling layout (2..8 steps: the long-row kernel sizes its own grid)
   int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);
@@ -920,8 +907,12 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
       default: return hipErrorInvalidValue;
     }
   }
-  GemvPtrs p_quant{};
-  if (a.q8_in == nullptr) {
+  // A 16-byte aligned PLAIN row of 2..8 steps is quantized by every block of
+  // the long-row kernel itself; other rows by the quantizer, into the
+  // stream's scratch, in a launch of its own.
+  const bool aligned = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.input) & 15) == 0;
+  const bool quant = a.q8_in == nullptr && a.mode == kPlain && aligned && lanes == 64 && steps >= 2 && steps <= 8;
+  if (a.q8_in == nullptr && !quant) {
     Scratch* scratch = a.work;
     if (scratch == nullptr) {
       hipError_t status = scratch_for_stream(stream, &scratch);
@@ -929,32 +920,22 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
     }
     if (chunks > scratch->capacity_chunks) return hipErrorInvalidValue;
     // The scratch row is the GEMV's alone: it is written nibble-split for the 4-bit dots.
-    const bool split = true;
-    sh.split = split;
-    const bool aligned = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.input) & 15) == 0;
-    if (a.mode == kPlain && aligned && lanes == 64 && steps >= 2 && steps <= 8 && scratch->sync != nullptr) {
-      // In-launch quantizer (the long-row kernel): one q8 word per thread, 32 chunks per slice.
-      sh.qblocks = ceil_div(chunks, 512 / 16);
-      p_quant = GemvPtrs{a.input, nullptr, scratch->q8, scratch->xsum, scratch->scale,
-                         scratch->q8, scratch->xsum, scratch->scale, scratch->sync};
-    } else {
-      QuantArgs q{a.mode, a.input, a.n, a.aux, a.n, a.eps, a.splits, a.head_dim, 1, scratch->q8, scratch->xsum,
-                  scratch->scale, split};
-      const hipError_t status = launch_quantize(stream, q);
-      if (status != hipSuccess) return status;
-    }
+    sh.split = 1;
+    QuantArgs q{a.mode, a.input, a.n, a.aux, a.n, a.eps, a.splits, a.head_dim, 1, scratch->q8, scratch->xsum,
+                scratch->scale, true};
+    const hipError_t status = launch_quantize(stream, q);
+    if (status != hipSuccess) return status;
     a.q8_in = scratch->q8;
     a.xsum_in = scratch->xsum;
     a.scale_in = scratch->scale;
   }
-  const GemvPtrs p = sh.qblocks > 0 ? p_quant
-                                    : GemvPtrs{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in,
-                                               nullptr, nullptr, nullptr, nullptr};
+  const GemvPtrs p = quant ? GemvPtrs{a.input, nullptr, nullptr, nullptr, nullptr}
+                           : GemvPtrs{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in};
   switch (a.epi) {
-    case kStore: return launch_nj<kPlain, kStore, false>(stream, p, a, sh, blocks, lds, steps);
-    case kResidual: return launch_nj<kPlain, kResidual, false>(stream, p, a, sh, blocks, lds, steps);
-    case kSiluPair: return launch_nj<kPlain, kSiluPair, false>(stream, p, a, sh, blocks, lds, steps);
-    case kPartials: return launch_nj<kPlain, kPartials, false>(stream, p, a, sh, blocks, lds, steps);
+    case kStore: return launch_nj<kPlain, kStore, false>(stream, p, a, sh, blocks, lds, steps, quant);
+    case kResidual: return launch_nj<kPlain, kResidual, false>(stream, p, a, sh, blocks, lds, steps, quant);
+    case kSiluPair: return launch_nj<kPlain, kSiluPair, false>(stream, p, a, sh, blocks, lds, steps, quant);
+    case kPartials: return launch_nj<kPlain, kPartials, false>(stream, p, a, sh, blocks, lds, steps, quant);
     default: return hipErrorInvalidValue;
   }
 }

@@ -106,13 +106,16 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   // fields of one packed word W of a group); its fields (0, 1) and (2, 3) are
   // the halves W & 1 of the operands o = 0, 1 of lane group kb = 0, 0, 2, 2,
   // 1, 1, 3, 3 (W = 0..7).
+  // A token's q8 row is chunks * 64 bytes (K is a multiple of 256 here); the
+  // scale rows may be longer (sh.groups >= K / 128) and only set their stride.
   const int quads = abytes / 16;  // m * 8 * sg
+  const int row_quads = chunks * 4;
   v4u fill[FILL];
 #pragma unroll
   for (int j = 0; j < FILL; ++j) {
     const int p = min(j * nthr + tid, quads - 1);
     const int t = p / (8 * sg), quad = p - t * (8 * sg);
-    fill[j] = *reinterpret_cast<const v4u*>(q8 + ((size_t)t * 8 * sh.groups + 8 * g_first + quad) * 16);
+    fill[j] = *reinterpret_cast<const v4u*>(q8 + ((size_t)t * row_quads + 8 * g_first + quad) * 16);
   }
   int seed_value[kSeedsPerThread];
 #pragma unroll
@@ -126,15 +129,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   const uint8_t* wrow = packed + (size_t)row * sh.row_bytes + (size_t)(g_first / 2 + span0) * kSpanBytes + kb * 16;
   const uint16_t* srow = scales + (size_t)row * sh.groups + g_first + span0 * 2;
   unsigned sc[PART];  // the two fp16 group scales of each span
+  if ((sh.groups & 1) == 0) {
+    // Even scale rows: every span's scale pair sits at a multiple of 4 bytes.
 #pragma unroll
-  for (int i = 0; i < PART; i += 2) {
-    if (i + 1 < PART) {
-      const uint2 v = *reinterpret_cast<const uint2*>(srow + 2 * i);
-      sc[i] = v.x;
-      sc[i + 1] = v.y;
-    } else {
-      sc[i] = *reinterpret_cast<const unsigned*>(srow + 2 * i);
+    for (int i = 0; i < PART; i += 2) {
+      if (i + 1 < PART) {
+        const uint2 v = *reinterpret_cast<const uint2*>(srow + 2 * i);
+        sc[i] = v.x;
+        sc[i + 1] = v.y;
+      } else {
+        sc[i] = *reinterpret_cast<const unsigned*>(srow + 2 * i);
+      }
     }
+  } else {
+    // Odd scale rows (padded past K / 128 groups): 2-byte aligned, one fp16 per load.
+#pragma unroll
+    for (int i = 0; i < PART; ++i) sc[i] = (unsigned)srow[2 * i] | ((unsigned)srow[2 * i + 1] << 16);
   }
   v4u w[UW];
 #pragma unroll

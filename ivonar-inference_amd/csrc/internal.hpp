@@ -11,10 +11,10 @@ namespace ivo {
 // Process-wide values the reference passes as compile-time defines
 // (kernel_decoder.py:215): HEAD_DIM for the ATTN prologue, TILE for the
 // token count of the quantize_tile_* entry points, MAX_CHUNKS (capacity of
-// the caller's q8 buffers, used only for argument checks), MAX_TOPK (largest
-// top-k of the sampler, ternary.cu:8), and GEMV_WAIT_SPINS (no reference
-// counterpart).  Atomic, so that ivonar_define on one
-// thread and a launch on another never race (a launch reads each value once).
+// the caller's q8 buffers, used only for argument checks) and MAX_TOPK
+// (largest top-k of the sampler, ternary.cu:8).  Atomic, so that
+// ivonar_define on one thread and a launch on another never race (a launch
+// reads each value once).
 constexpr int kMaxTopK = 1024;
 constexpr int kMaxSampleVocab = 1 << 18;
 struct Defines {
@@ -22,9 +22,6 @@ struct Defines {
   std::atomic<int> tile{32};
   std::atomic<int> max_chunks{70};
   std::atomic<int> max_topk{256};
-  // Polls a block of the GEMV's in-launch quantizer makes before it gives up
-  // (its outputs are then NaN); lowered only by tests of that path.
-  std::atomic<int> wait_spins{1 << 20};
 };
 Defines& defines();
 
@@ -35,13 +32,12 @@ struct Scratch {
   float* scale = nullptr;
   int capacity_chunks = 0;
   float* token_partials = nullptr;  // fp32 wave partials of the K-sliced token GEMV
-  // Counters and flags of the GEMV's in-launch quantizer (kSyncBytes, zero
-  // between launches); null: quantize in a launch of its own.
+  // Counters that start and end every launch at zero (kSyncBytes): the
+  // argmax's block count.
   unsigned* sync = nullptr;
 };
 constexpr int kSyncBytes = 4096;
-// The argmax's block count, in the last 128-byte line of the sync region (the
-// GEMV's in-launch quantizer uses the lines before it).
+// The argmax's block count, in the last 128-byte line of the sync region.
 constexpr int kArgmaxCountWord = kSyncBytes / 4 - 32;
 // Capacity of Scratch::token_partials (floats; 16 MB per device).
 constexpr long long kTokenPartialFloats = 4LL << 20;

@@ -182,9 +182,13 @@ class Launch:
 
     def __call__(self, stream: int) -> None:
         module = self.kernel.module
-        if module is not None and _applied_defines is not module.define_values:
-            module.apply_defines()
-        status = self.kernel.function(c_void_p(stream), *self._args)
+        # The define values live once per process in the library: making a
+        # module's values current and launching its kernel happen under one
+        # lock, so a launch of another module cannot switch them in between.
+        with _launch_lock:
+            if module is not None and _applied_defines is not module.define_values:
+                module.apply_defines()
+            status = self.kernel.function(c_void_p(stream), *self._args)
         if status != 0:
             check(status, self.kernel.name)
 
@@ -193,6 +197,7 @@ _DEFINES = ("HEAD_DIM", "TILE", "MAX_CHUNKS", "MAX_TOPK")
 _LIBRARY_DEFAULTS = {"HEAD_DIM": 64, "TILE": 32, "MAX_CHUNKS": 70, "MAX_TOPK": 256}
 # The define values the library currently holds (the tuple of the module that set them last).
 _applied_defines: tuple | None = None
+_launch_lock = threading.Lock()
 
 
 class Module:
@@ -254,7 +259,8 @@ def compile_module(
         if module is None:
             module = Module(key, defines)
             _modules[key] = module
-    module.apply_defines()  # rejects out-of-range values here, as NVRTC would at compile time
+    with _launch_lock:
+        module.apply_defines()  # rejects out-of-range values here, as NVRTC would at compile time
     return module
 
 

@@ -174,12 +174,11 @@ def test_gemv_plain_store_model_shapes(cuda, oracle, rows, k):
 @pytest.mark.parametrize("k", [5000, 8192, 28672, 40000])
 @pytest.mark.parametrize("rows", [2, 600])
 def test_gemv_long_rows_back_to_back(cuda, oracle, rows, k):
-    """Rows longer than 4096 inputs are quantized inside the GEMV launch by its first blocks, which the
-    other blocks wait for through two scratch counters that the launch sets back to zero.  Eight calls
-    with different inputs go out back to back on one stream (two rows: the quantizing blocks outnumber
-    the blocks with rows); each output must be the oracle's for its own input.  The same rows read
-    from an input that is not 16-byte aligned take the separate quantizer launch and give the same
-    bits."""
+    """Rows of 4097..32768 inputs are quantized inside the GEMV launch, by every block into its own LDS
+    (40000 inputs: by the separate quantizer).  Eight calls with inputs of magnitudes 1e-3 .. 1e3 go
+    out back to back on one stream (two rows: most blocks have no row and still quantize); each output
+    must be the oracle's for its own input.  The same rows read from an input that is not 16-byte
+    aligned take the separate quantizer launch and give the same bits."""
     import torch
     from ivonar_amd import ops, runtime
 
@@ -209,42 +208,46 @@ def test_gemv_long_rows_back_to_back(cuda, oracle, rows, k):
         assert_bits_equal(got[1, i], mine, f"unaligned input, call {i}")
 
 
-@pytest.mark.parametrize("k", [8192, 28672])
-def test_gemv_in_launch_wait_gives_up_loudly(cuda, oracle, k):
-    """A block of the in-launch quantizer that stops waiting for the published row writes NaN for its
-    rows, never other values.  The host lowers the poll limit to zero (GEMV_WAIT_SPINS), so blocks that
-    find the row unpublished give up at once and every kernel still exits normally; each output must
-    be NaN or the oracle's bits.  With the limit restored, the next calls on the same scratch give
-    the oracle's bits in every row (the counters a launch leaves stay consistent)."""
-    import torch
+# Rows the GEMV quantizes inside its own launch (16-byte aligned PLAIN rows of 4097..32768 inputs), with
+# the values the in-block quantizer treats specially: its u = fma(x, 1/s, 128) rounding decides every
+# value except those within 2e-5 of a half-integer, which take the exact division.
+@pytest.mark.parametrize("k", [4100, 8192, 12288, 28672, 32768])
+def test_gemv_in_launch_quantizer_edge_rows(cuda, oracle, k):
+    """Zero row (scale floor 1e-5, every q 0), a row below the floor, exact ties x/s = j + 1/2 (s a power
+    of two, so x/s is exact and rint goes to even), values one float step either side of those ties, -0.0
+    entries, and a single outlier over tiny values: every output the oracle's bits, and q8 from the
+    separate quantizer fed to gemv_prequant_store gives the same bits."""
     from ivonar_amd import ops, runtime
-    from ivonar_amd.runtime import check
 
-    rows = 4096
-    print(f"in-launch wait limit 0: gemv_plain_store K={k} N={rows}", flush=True)
-    rng = np.random.default_rng(k + 77)
+    rows = 600
+    print(f"in-launch quantizer edge rows K={k} N={rows}", flush=True)
+    rng = np.random.default_rng(k + 5)
     codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
     lanes, _ = runtime.gemv_plan(rows, k)
-    x = rng.standard_normal(k).astype(np.float32)
-    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
-    expected = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, b,
-                                 np.zeros(rows, np.float32), k, lanes)
-    xv = _t(x, cuda)
-    lib = runtime.library()
-    gave_up = 0
-    try:
-        check(lib.ivonar_define(b"GEMV_WAIT_SPINS", 0), "define GEMV_WAIT_SPINS")
-        for rep in range(4):
-            got = to_np(ops.gemv(matrix, xv))
-            nan = np.isnan(got)
-            gave_up += int(nan.sum())
-            assert_bits_equal(got[~nan], expected[~nan], f"limit 0, call {rep}: rows that did not give up")
-    finally:
-        check(lib.ivonar_define(b"GEMV_WAIT_SPINS", 1 << 20), "define GEMV_WAIT_SPINS")
-    print(f"rows written as NaN with limit 0: {gave_up} of {4 * rows}", flush=True)
-    for rep in range(3):
-        assert_bits_equal(to_np(ops.gemv(matrix, xv)), expected, f"limit restored, call {rep}")
+    s = np.float32(0.125)  # amax = 127 * s makes the scale exactly s
+    ties = (rng.integers(-126, 126, k) + np.float32(0.5)) * s
+    ties[rng.integers(0, k)] = 127 * s
+    near = ties.copy()
+    near[0::2] = np.nextafter(near[0::2], np.float32(np.inf))
+    near[1::2] = np.nextafter(near[1::2], np.float32(-np.inf))
+    near[np.argmax(np.abs(ties))] = 127 * s
+    signed_zero = rng.standard_normal(k).astype(np.float32)
+    signed_zero[::3] = -0.0
+    outlier = (rng.standard_normal(k) * 1e-6).astype(np.float32)
+    outlier[k // 3] = 500.0
+    cases = {"zeros": np.zeros(k, np.float32), "below floor": (rng.standard_normal(k) * 1e-4).astype(np.float32),
+             "exact ties": ties.astype(np.float32), "next to ties": near.astype(np.float32),
+             "signed zeros": signed_zero, "outlier": outlier}
+    for name, x in cases.items():
+        q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+        expected = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, b,
+                                     np.zeros(rows, np.float32), k, lanes)
+        xd = _t(x, cuda)
+        assert_bits_equal(to_np(ops.gemv(matrix, xd)), expected, f"{name}: gemv_plain_store")
+        dq8, dxsum, dsx = ops.quantize_rows(xd[None])
+        assert_bits_equal(to_np(dq8), q8, f"{name}: q8")
+        assert_bits_equal(to_np(ops.gemv_prequant(matrix, dq8, dxsum, dsx)), expected, f"{name}: prequant")
 
 
 @pytest.mark.parametrize("k", [24, 1024, 4096, 5000, 8192, 8200, 28672, 40000, 49152])

@@ -1,11 +1,12 @@
-"""GPU calls that go through the library's scratch, issued on two streams at once.
+"""GPU calls that go through the library's scratch, issued on several streams at once.
 
-A decode GEMV on a row longer than 4096 inputs quantizes the row into a scratch buffer in one launch
-and reads it in the next; a token GEMM of up to 16 tokens whose q8 rows exceed LDS writes its wave
-chains to a scratch buffer and adds them in a second launch.  Each stream has its own scratch, so
-calls on two streams, interleaved without synchronisation, must each give the oracle's bits, in
-every repetition (a shared buffer would let one stream's quantizer or chains overwrite the other's
-between its two launches)."""
+A decode GEMV on a row longer than 4096 inputs that it does not quantize itself (here: read from an
+address that is not 16-byte aligned) quantizes the row into a scratch buffer in one launch and reads
+it in the next; a token GEMM of up to 16 tokens whose q8 rows exceed LDS writes its wave chains to a
+scratch buffer and adds them in a second launch.  Each stream has its own scratch, so calls on two
+streams, interleaved without synchronisation, must each give the oracle's bits, in every repetition
+(a shared buffer would let one stream's quantizer or chains overwrite the other's between its two
+launches); so must calls on 40 streams, more than any fixed table of per-stream scratch would hold."""
 
 from __future__ import annotations
 
@@ -26,6 +27,16 @@ def _t(array, device):
     return torch.from_numpy(np.ascontiguousarray(array)).to(device)
 
 
+def _unaligned(x):
+    """The same values one float past a 16-byte boundary (the GEMV's separate-quantizer path)."""
+    import torch
+
+    padded = torch.zeros(x.numel() + 1, dtype=torch.float32, device=x.device)
+    padded[1:] = x
+    assert padded[1:].data_ptr() % 16 != 0
+    return padded[1:]
+
+
 def test_long_row_gemv_on_two_streams(cuda, oracle):
     import torch
     from ivonar_amd import ops, runtime
@@ -43,7 +54,7 @@ def test_long_row_gemv_on_two_streams(cuda, oracle):
         expected.append(oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, None,
                                           np.zeros(rows, np.float32), k, lanes))
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
-    inputs = [_t(x, cuda) for x in xs]
+    inputs = [_unaligned(_t(x, cuda)) for x in xs]
     outs = [torch.empty((REPEATS, rows), dtype=torch.float32, device=cuda) for _ in xs]
     torch.cuda.synchronize()
     for rep in range(REPEATS):
@@ -89,3 +100,37 @@ def test_sliced_token_gemm_on_two_streams(cuda, oracle):
         got = to_np(outs[side])
         for rep in range(REPEATS):
             assert_bits_equal(got[rep], expected[side], f"stream {side}, repetition {rep}")
+
+
+def test_scratch_calls_on_forty_streams(cuda, oracle):
+    """40 streams, each with its own input, make scratch-using GEMV calls (unaligned K=8192 rows) three
+    times each, interleaved without synchronisation: every stream gets a scratch of its own (no table
+    limit, no shared fallback), so every output is the oracle's for its stream's input."""
+    import torch
+    from ivonar_amd import ops, runtime
+
+    k, rows, count = 8192, 1024, 40
+    print(f"{count}-stream gemv_plain_store K={k} N={rows}", flush=True)
+    rng = np.random.default_rng(43)
+    codes, packed, scale_bits, _ = make_layer(rng, rows, k)
+    matrix = device_matrix(packed, scale_bits, k, device=cuda)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    xs = [(rng.standard_normal(k) * (1.0 + i)).astype(np.float32) for i in range(count)]
+    expected = []
+    for x in xs:
+        q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+        expected.append(oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, None,
+                                          np.zeros(rows, np.float32), k, lanes))
+    streams = [torch.cuda.Stream() for _ in range(count)]
+    inputs = [_unaligned(_t(x, cuda)) for x in xs]
+    outs = torch.empty((count, 3, rows), dtype=torch.float32, device=cuda)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i in range(count):
+            with torch.cuda.stream(streams[i]):
+                ops.gemv(matrix, inputs[i], out=outs[i, rep])
+    torch.cuda.synchronize()
+    got = to_np(outs)
+    for i in range(count):
+        for rep in range(3):
+            assert_bits_equal(got[i, rep], expected[i], f"stream {i}, repetition {rep}")

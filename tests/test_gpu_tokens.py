@@ -167,3 +167,60 @@ def test_token_gemv_graph_replays(cuda, oracle):
         for i, case in enumerate(cases):
             assert torch.equal(case[3], eager[i]), f"replay {replay}, case {i}"
             assert torch.equal(case[4], other_expected[i]), f"eager call after replay {replay}, case {i}"
+
+
+class _PaddedScales:
+    """A device matrix whose fp16 scale rows carry `extra` unused groups past ceil(K/128) (the C ABI accepts
+    groups >= ceil(K/128)); the q8 rows of the tokens stay K wide."""
+
+    def __init__(self, matrix, extra: int):
+        import torch
+
+        self.packed, self.bias = matrix.packed, matrix.bias
+        self.rows, self.in_features, self.row_bytes, self.lanes = (matrix.rows, matrix.in_features,
+                                                                    matrix.row_bytes, matrix.lanes)
+        self.groups = matrix.groups + extra
+        padded = torch.full((matrix.rows, self.groups), float("nan"), dtype=torch.float16,
+                            device=matrix.scales.device)
+        padded[:, :matrix.groups] = matrix.scales.view(matrix.rows, matrix.groups)
+        self.scales = padded
+
+
+# (m, k, rows): the token GEMV in one slice and in K slices, the skinny kernel, the 32-token slices and the
+# long-prompt and split-K tilings, all with one or three unused scale groups per row.
+@pytest.mark.parametrize("m,k,rows", [(5, 4096, 1000), (12, 28672, 4100), (3, 1024, 300), (32, 4096, 1024),
+                                      (100, 2048, 700), (512, 4096, 1024), (300, 4096, 14336)])
+@pytest.mark.parametrize("extra", [1, 2])
+def test_token_gemm_padded_scale_rows(cuda, oracle, m, k, rows, extra):
+    from ivonar_amd import ops, runtime
+
+    print(f"token gemm padded scales m={m} k={k} rows={rows} extra={extra}", flush=True)
+    rng = np.random.default_rng(m * 13 + k + rows + extra)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = _PaddedScales(device_matrix(packed, scale_bits, k, bias=b, device=cuda), extra)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    eq8, _, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    out = ops.gemm(matrix, q8, xsum, sx)
+    splits = runtime.gemm_plan(m, rows, k)
+    expected = finish_all_rows(oracle, 1, splits, T.EPI_STORE, codes, T.q8_linear(eq8, k), scale_bits, esx, b,
+                               np.zeros((m, rows), np.float32), k, rows)
+    assert_bits_equal(to_np(out), expected, f"padded scales m={m} k={k} rows={rows} ({splits} splits)")
+
+
+@pytest.mark.parametrize("k", [1024, 8192, 28672])
+def test_gemv_padded_scale_rows(cuda, oracle, k):
+    from ivonar_amd import ops, runtime
+
+    rows = 1000
+    print(f"gemv padded scales k={k} rows={rows}", flush=True)
+    rng = np.random.default_rng(k + 3)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal(k).astype(np.float32)
+    matrix = _PaddedScales(device_matrix(packed, scale_bits, k, bias=b, device=cuda), 2)
+    got = to_np(ops.gemv(matrix, _t(x, cuda)))
+    eq8, _, esx = oracle.quantize_rows(T.MODE_PLAIN, x[None], k)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    expected = finish_all_rows(oracle, 0, lanes, T.EPI_STORE, codes, T.q8_linear(eq8, k), scale_bits, esx, b,
+                               np.zeros((1, rows), np.float32), k, rows)
+    assert_bits_equal(got, expected[0], f"gemv padded scales k={k}")

@@ -66,9 +66,7 @@ def test_host_only_calls():
     assert lib.ivonar_define(b"TILE", 32) == 0
     assert lib.ivonar_define(b"MAX_TOPK", 1025) != 0
     assert lib.ivonar_define(b"MAX_TOPK", 256) == 0
-    assert lib.ivonar_define(b"GEMV_WAIT_SPINS", -1) != 0
-    assert lib.ivonar_define(b"GEMV_WAIT_SPINS", 0) == 0
-    assert lib.ivonar_define(b"GEMV_WAIT_SPINS", 1 << 20) == 0
+    assert lib.ivonar_define(b"GEMV_WAIT_SPINS", 1) != 0  # no in-launch wait to bound any more
     assert lib.ivonar_error_string(1)
     assert runtime.gemm_plan(2048, 4096, 1024) == 1
     assert runtime.gemm_plan(1, 4096, 1024) >= 1

@@ -90,3 +90,51 @@ def test_modules_keep_their_own_defines():
     assert dict(small.define_values)["HEAD_DIM"] == 16
     assert dict(default.define_values)["HEAD_DIM"] == 64
     assert dict(default.define_values)["TILE"] == 32
+
+
+def test_launches_of_modules_with_different_defines_do_not_interleave(monkeypatch):
+    """Two threads launch kernels of modules with different HEAD_DIM / TILE over and over; the
+    library's process-wide define values must be the launching module's at every launch (the values
+    are made current and the kernel launched under one lock).  A recording stand-in replaces the
+    library, so no device is needed."""
+    import threading
+    import time
+
+    current: dict[str, int] = {}
+    seen: list[tuple[str, tuple]] = []
+
+    class FakeLibrary:
+        def ivonar_define(self, name: bytes, value: int) -> int:
+            current[name.decode()] = int(value)
+            time.sleep(1e-4)  # let the other thread run between defines
+            return 0
+
+    def fake_kernel(tag):
+        def function(stream, *args):
+            seen.append((tag, tuple(sorted(current.items()))))
+            time.sleep(1e-4)
+            return 0
+        return function
+
+    monkeypatch.setattr(runtime, "library", lambda: FakeLibrary())
+    monkeypatch.setattr(runtime, "_applied_defines", None)
+    modules = {
+        "a": runtime.Module(("a",), {"HEAD_DIM": 64, "TILE": 32}),
+        "b": runtime.Module(("b",), {"HEAD_DIM": 128, "TILE": 16}),
+    }
+    launches = {tag: runtime.Launch(runtime.Kernel(fake_kernel(tag), "gather_token", module), (1, 1, 1), (1, 1, 1),
+                                    [None] * len(runtime.SIGNATURES["gather_token"]))
+                for tag, module in modules.items()}
+
+    def worker(tag):
+        for _ in range(100):
+            launches[tag](0)
+
+    threads = [threading.Thread(target=worker, args=(tag,)) for tag in launches]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join()
+    assert len(seen) == 200
+    for tag, values in seen:
+        assert values == modules[tag].define_values, f"launch of module {tag} ran with {values}"
