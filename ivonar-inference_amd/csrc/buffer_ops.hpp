@@ -67,5 +67,17 @@ __device__ __forceinline__ int load_u16(v4u buffer, int voffset, int soffset) {
 // cover all 64 banks once.
 __device__ __forceinline__ int a_swizzle(int t) { return (t & 7) ^ ((t >> 3) & 1); }
 
+// Bytes a direct-to-LDS load (dma16) wrote are read only after the issuing
+// wave's vmcnt wait has retired that load, lgkmcnt(0), and a workgroup
+// barrier that every wave of the block reaches: the sequence AMD's
+// composable_kernel places after its direct loads before reading them
+// (ck/utility/synchronization.hpp, block_sync_lds_direct_load, as installed
+// with ROCm), used here whether the reader is the loading wave or another.
+// Kernels that keep later loads in flight across it issue the same three
+// instructions with vmcnt(N) (loads retire in issue order).
+__device__ __forceinline__ void direct_load_sync() {
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 }  // namespace
 }  // namespace ivo

@@ -320,8 +320,8 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
       for (int i = 0; i < 4; ++i) acc[mt][r][i] = 0.0f;
   static_for<NG>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    // The reads of a direct-to-LDS load's bytes wait for the counter and then a barrier (a load
-    // was seen still writing LDS after the counter alone; every wave passes all NG barriers).
+    // The reads of a direct-to-LDS load's bytes follow direct_load_sync's sequence (the counter
+    // here leaves the later groups' loads in flight; every wave passes all NG barriers).
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"((NG - 1 - j) * T::kLoadsPerGroup)
                  : "memory");
     if (j >= count) return;  // wave-uniform

@@ -158,8 +158,8 @@ __global__ __launch_bounds__(64 * WN) void gemm_wide_kernel(const int8_t* __rest
   // MFMAs of g, then the scale of g+2 (loaded in the previous step) goes to
   // LDS.  The wait before that store also retires the DMA of g+1 (loads
   // complete in order) and leaves the DMA of g+2 and the scale load of g+3
-  // in flight, so the barrier at the top of the next step publishes every
-  // wave's pieces of g+1.  `pending` holds the scale of g+2 and `fresh`
+  // in flight; lgkmcnt(0) and the barrier at the top of the next step
+  // complete direct_load_sync's sequence for every wave's pieces of g+1.  `pending` holds the scale of g+2 and `fresh`
   // receives that of g+3; the caller alternates the two registers.
   auto step = [&](int g, int cur, int fill, int& pending, int& fresh) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -349,9 +349,12 @@ hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a, int tokens) {
 // M=2048 has only 64 tiles of 128 x 256): a block of four waves owns one
 // 128-token x 64-row output tile and wave w walks the contiguous group range
 // [w*per, (w+1)*per), per = ceil(G/4).  Each wave stages its own operands
-// (its own two-stage ring of direct-to-LDS loads, no block barrier in the
-// loop: no other wave reads them) and runs the same fixed-order MFMA/fold
-// units as gemm_wide_kernel.  The four partial tiles are then added in wave
+// (its own two-stage ring of direct-to-LDS loads) and runs the same
+// fixed-order MFMA/fold units as gemm_wide_kernel.  A stage is read after the
+// loading wave's vmcnt wait, lgkmcnt(0) and a workgroup barrier
+// (direct_load_sync), so every wave runs `per` steps: a wave with fewer
+// groups (or none) loads again and skips the compute in the steps it lacks,
+// and reaches every barrier.  The four partial tiles are then added in wave
 // order through LDS - the order the CPU oracle restates as orc_gemm_split(4):
 // each range an fmaf chain, total = ((s0 + s1) + s2) + s3 - scaled by s_x and
 // biased, and stored as 16-byte vectors.
@@ -416,7 +419,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   };
   // The row scale of a group (lane: row lane of the tile), written to LDS as
   // fp32 once every load of the wave has retired: the scale arrived and the
-  // stage just filled is complete.
+  // loads of the stage just filled are retired (direct_load_sync then makes
+  // that stage readable).
   auto scale_load = [&](int g) { return load_u16(s_buf, s_off, g * 2); };
   auto scale_store = [&](int& r, int stage) {
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(r)::"memory");
@@ -439,9 +443,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   }
   const int b_read = ((kb >> 1) * kSplitRows + col) * 16 + (kb & 1) * 8;
 
-  auto step = [&](int cur, int fill, int g_fill) {
-    int scale = scale_load(g_fill);
-    dma(g_fill, fill);
+  auto compute = [&](int cur) {
     const unsigned char* base = stages[wave][cur];
     const v4i zero = {0, 0, 0, 0};
     uint2 w[4];
@@ -491,20 +493,34 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
         a1 = na1;
       }
     }
-    scale_store(scale, fill);
   };
 
-  if (g_begin < g_end) {
-    {
-      int s0 = scale_load(g_begin);
-      dma(g_begin, 0);
-      scale_store(s0, 0);
-    }
-    int cur = 0;
-    for (int g = g_begin; g < g_end; ++g) {
-      step(cur, cur ^ 1, min(g + 1, g_end - 1));
-      cur ^= 1;
-    }
+  // One group step: the next group's loads into stage `fill`, then (a wave
+  // with a group left, `live`) the MFMAs and fold on stage `cur`, then the
+  // wait that retires the loads of `fill` and the workgroup barrier.
+  auto step = [&](int cur, int fill, int g_fill, bool live) {
+    int scale = scale_load(g_fill);
+    dma(g_fill, fill);
+    if (live) compute(cur);
+    scale_store(scale, fill);
+    direct_load_sync();
+  };
+
+  // Every wave runs `per` steps and passes every barrier; a wave whose range
+  // is shorter (or empty) loads its last group (or the matrix's last) again
+  // and skips the compute.
+  {
+    const int g0 = min(g_begin, groups - 1);
+    int s0 = scale_load(g0);
+    dma(g0, 0);
+    scale_store(s0, 0);
+    direct_load_sync();
+  }
+  int cur = 0;
+  for (int i = 0; i < per; ++i) {
+    const int g = g_begin + i;
+    step(cur, cur ^ 1, max(min(g + 1, g_end - 1), 0), g < g_end);
+    cur ^= 1;
   }
   // The last row of tiles; a wave without groups folds zeros.
 #pragma unroll
