@@ -501,13 +501,14 @@ def m_sweep(device, stream) -> dict:
         table[str(m)] = entry
     return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover,
             "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph, M >= 512 after 25 ms "
-                    "of the same calls; gemm_us for M <= 16 is the token GEMV (K a multiple of 256)"}
+                    "of the same calls; gemm_us for M = 1 is the decode GEMV on the pre-quantized row, for "
+                    "M = 2..16 the token GEMV (K a multiple of 256)"}
 
 
 def stress_tokens(matrices, stress, stream, replays: int) -> dict:
     """Cold-cache GEMM with M = 1..16 tokens on the two stress shapes (8 rotating copies per shape, one
-    HIP graph of 8 calls, median of `replays` replays): the token GEMV where the tokens' q8 rows fit in
-    LDS, the skinny kernel otherwise; beside it the M = 1 GEMV on pre-quantized input."""
+    HIP graph of 8 calls, median of `replays` replays): M = 1 runs the decode GEMV (plan 0), M = 2..16 the
+    token GEMV (plan = its K-splits); beside it the M = 1 GEMV on pre-quantized input called directly."""
     import numpy as np
     import torch
 
@@ -529,7 +530,7 @@ def stress_tokens(matrices, stress, stream, replays: int) -> dict:
 
             t = time_graph(graph_of(run, stream), replays, 2, median=True) / len(matrices[shape])
             entry[str(m)] = {"us": round(t * 1e6, 3), "GBps": round(gemv_bytes(m, n, k) / t / 1e9, 1),
-                             "splits": runtime.gemm_plan(m, n, k)}
+                             "plan": runtime.gemm_plan(m, n, k)}
         q8, xsum, sx = ops.quantize_rows(torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32)).to(out.device))
 
         def gemv(q8=q8, xsum=xsum, sx=sx):

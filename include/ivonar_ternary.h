@@ -73,8 +73,10 @@ void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane);
 
 /* K-splits S of the token GEMM (gemm_tile_*) for m tokens: its fp32 order is S
  * contiguous ranges of the 128-input groups, each summed in ascending order,
- * then the S partial sums added in order (S = 1: one chain).  Uses the
- * current device's LDS size. */
+ * then the S partial sums added in order (S = 1: one chain).  S = 0: one
+ * token, which gemm_tile_* hands to the decode GEMV on the pre-quantized row
+ * (gemv_prequant_store's kernel), so its order is ivonar_gemv_plan's lane
+ * layout.  Uses the current device's LDS size. */
 int ivonar_gemm_plan(int m, int rows, int n);
 
 /* ------------------------------------------------------------ decode GEMV
@@ -119,10 +121,11 @@ hipError_t gemv_attn_residual_wide(hipStream_t stream, IVONAR_GEMV_ARGS);
 /* No reference counterpart; for callers that cannot allocate device memory
  * (code under graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  gemv_plain_store with the same arguments and results, except
- * that a row longer than 4096 inputs is quantized into a fixed 35,072-byte
- * array of the library's device code (one per device, set up on the first
- * call on each device) instead of the scratch gemv_plain_store allocates:
- * nothing is allocated or freed, by this call or the library.  n above
+ * that a row longer than 4096 inputs that the GEMV launch does not quantize
+ * itself (an input not 16-byte aligned) is quantized into a fixed
+ * 35,072-byte array of the library's device code (one per device, set up on
+ * the first call on each device) instead of the scratch gemv_plain_store
+ * allocates: nothing is allocated or freed, by this call or the library.  n above
  * 32768 returns hipErrorInvalidValue.  Every call on a device shares that
  * array, so calls that overlap on one device race (their outputs are
  * undefined); calls in one stream order are safe.  Nothing in the array

@@ -370,12 +370,14 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 
 }  // namespace
 
-// Kernel choice: the token GEMV for up to 16 tokens (K a multiple of 256; K
-// sliced across blocks where the tokens' q8 rows do not fit in LDS whole);
+// Kernel choice: the decode GEMV for one token; the token GEMV for up to 16
+// tokens (K a multiple of 256; K sliced across blocks where the tokens' q8
+// rows do not fit in LDS whole);
 // the skinny kernels up to 32 tokens; then the long-prompt
 // tilings; then the LDS-staged skinny kernel in 32-token slices up to
 // kSlicedTokens; otherwise the tiled kernel.
 int gemm_splits(int m, int rows, int n) {
+  if (m == 1 && gemv_prequant_applies(n)) return 0;
   const size_t lds = (size_t)max_lds_per_block();
   const TokenPlan tokens = token_gemv_plan(m, rows, n, device_cus(), lds);
   if (tokens.parts > 0) return tokens.parts * tokens.slices;
@@ -387,6 +389,27 @@ int gemm_splits(int m, int rows, int n) {
 
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (a.rows <= 0 || a.m <= 0) return hipSuccess;
+  if (a.m == 1 && gemv_prequant_applies(a.n)) {
+    // One token: the decode GEMV on the pre-quantized row (the q8 row layout
+    // is the same); the output stride does not matter for a single row.
+    GemvArgs g{};
+    g.mode = kPlain;
+    g.epi = a.epi;
+    g.q8_in = a.q8_in;
+    g.xsum_in = a.xsum_in;
+    g.scale_in = a.scale_in;
+    g.packed = a.packed;
+    g.scales = a.scales;
+    g.bias = a.bias;
+    g.output = a.output;
+    g.rows = a.rows;
+    g.n = a.n;
+    g.row_bytes = a.row_bytes;
+    g.groups = a.groups;
+    g.splits = 1;
+    g.head_dim = defines().head_dim;
+    return launch_gemv(stream, g);
+  }
   const size_t lds = (size_t)max_lds_per_block();
   const TokenPlan tokens = token_gemv_plan(a.m, a.rows, a.n, device_cus(), lds);
   if (tokens.parts > 0) return launch_token_gemv(stream, a, tokens);

@@ -858,6 +858,8 @@ int device_cus() {
 
 int gemv_fused_limit() { return kFusedLimit; }
 
+bool gemv_prequant_applies(int n) { return n > 0 && (size_t)ceil_div(n, kChunk) * (kChunk + 4) <= (size_t)kMaxLdsBytes; }
+
 void gemv_plan(int rows, int n, int* lanes, int* rows_per_lane) {
   (void)rows;
   const int chunks = ceil_div(n, kChunk);

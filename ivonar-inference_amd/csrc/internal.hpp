@@ -94,6 +94,8 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& a);
 // summation order): lanes per row (power of two in [2, 64]) and rows per lane.
 void gemv_plan(int rows, int n, int* lanes, int* rows_per_lane);
 int gemv_fused_limit();
+// Whether the decode GEMV takes a pre-quantized K = n row (its LDS bound).
+bool gemv_prequant_applies(int n);
 
 struct GemmArgs {
   int epi;  // kStore / kResidual / kSiluPair
@@ -122,7 +124,8 @@ bool gemm_split_applies(int m, int rows, int n);
 hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a);
 
 // K-splits of the GEMM for m tokens (its fp32 order: S contiguous group ranges,
-// each an fmaf chain, added in order); 1 = one chain over all groups.
+// each an fmaf chain, added in order); 1 = one chain over all groups; 0 = one
+// token, run by the decode GEMV (its order is the GEMV's lane layout).
 int gemm_splits(int m, int rows, int n);
 int max_lds_per_block();
 // Skinny token GEMM (m <= 32, and up to kSlicedTokens in 32-token slices):

@@ -48,19 +48,22 @@ class DeviceSampler:
 
     def configure_sampling(self, temperature: float, top_k: int, repetition_penalty: float = 1.0,
                            penalized_ids: Iterable[int] = ()) -> None:
-        """decoder.py:340-361: top_k outside 1..max_top_k means max_top_k; penalized ids start out seen."""
-        if temperature <= 0 or repetition_penalty <= 0:
+        """The rule of decoder.py:340-361: a non-positive temperature or penalty is a ValueError, a top_k
+        outside 1..max_top_k selects max_top_k, and the in-vocabulary ids of `penalized_ids` are marked
+        as already generated (the rest are ignored)."""
+        if any(value <= 0 for value in (temperature, repetition_penalty)):
             raise ValueError("temperature and repetition_penalty must be positive")
-        effective = int(top_k) if 0 < int(top_k) <= self.max_top_k else self.max_top_k
-        self.temperature.fill_(float(temperature))
-        self.penalty.fill_(float(repetition_penalty))
-        self.inverse_penalty.fill_(1.0 / float(repetition_penalty))
-        self.top_k.fill_(effective)
-        self.seen.zero_()
-        seeds = [int(token) for token in penalized_ids if 0 <= int(token) < self.vocab]
-        if seeds:
-            index = torch.tensor(sorted(set(seeds)), dtype=torch.int64, device=self.device)
-            self.seen.index_fill_(1, index, True)
+        k = int(top_k)
+        if not 1 <= k <= self.max_top_k:
+            k = self.max_top_k
+        penalty = float(repetition_penalty)
+        for buffer, value in ((self.temperature, float(temperature)), (self.penalty, penalty),
+                              (self.inverse_penalty, 1.0 / penalty), (self.top_k, k)):
+            buffer.fill_(value)
+        ids = torch.as_tensor([int(i) for i in penalized_ids], dtype=torch.int64)
+        marked = torch.zeros((1, self.vocab), dtype=torch.bool)
+        marked[0, ids[(ids >= 0) & (ids < self.vocab)]] = True
+        self.seen.copy_(marked)
 
     def launch(self, logits: Tensor, uniform: Tensor | None = None, token: Tensor | None = None,
                history: Tensor | None = None) -> None:

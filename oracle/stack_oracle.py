@@ -89,7 +89,8 @@ class StackOracle:
         q8, _, scale = self.oracle.quantize_rows(mode, x, k, aux=aux, eps=self.config.eps)
         partials = self.oracle.partials_i8(projection.values, T.q8_linear(q8[0], k))
         if tile:
-            order, param = 1, self._gemm_splits(TILE, projection.rows, k)
+            splits = self._gemm_splits(TILE, projection.rows, k)  # 0: one token, run as the decode GEMV
+            order, param = (1, splits) if splits else (0, self._gemv_lanes(projection.rows, k))
         else:
             order, param = 0, self._gemv_lanes(projection.rows, k)
         return self.oracle.finish(order, param, epi, partials, projection.scale_bits, scale, None, out, k,

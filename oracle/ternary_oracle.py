@@ -249,6 +249,8 @@ class Oracle:
 
     def gemm_split(self, epi: int, q8, xsum, scale_in, packed, scales_bits, bias, out: np.ndarray, n: int,
                    out_stride: int, m: int, splits: int) -> np.ndarray:
+        if splits < 1:
+            raise ValueError(f"a K-split order needs at least one split, not {splits}")
         packed = np.ascontiguousarray(packed)
         scales_bits = np.ascontiguousarray(scales_bits, dtype=np.uint16)
         self.lib.orc_gemm_split(epi, _ptr(np.ascontiguousarray(q8)), _ptr(np.ascontiguousarray(xsum)),
@@ -279,6 +281,8 @@ class Oracle:
     def finish(self, order: int, param: int, epi: int, partials: np.ndarray, scales_bits: np.ndarray, scale_in,
                bias, out: np.ndarray, k: int, out_stride: int) -> np.ndarray:
         """fp32 outputs from partials [m, rows, G]: order 0 = GEMV pairs (param = lanes), 1 = GEMM split."""
+        if order not in (0, 1) or param < 1:
+            raise ValueError(f"no fp32 order {order} with parameter {param}")
         partials = np.ascontiguousarray(partials, dtype=np.int32)
         if partials.ndim == 2:
             partials = partials[None]

@@ -118,3 +118,26 @@ def finish_all_rows(oracle, order: int, param: int, epi: int, codes: np.ndarray,
         partials = exact_partials(codes, q[start:stop])
         oracle.finish(order, param, epi, partials, scale_bits, sx[start:stop], bias, out[start:stop], k, out_stride)
     return out
+
+
+def token_gemm_order(m: int, rows: int, k: int) -> tuple[int, int]:
+    """(order, param) of gemm_tile_* for m tokens, as the oracle's finish takes them: the K-split the plan
+    reports (order 1), or for one token (plan 0) the decode GEMV's lanes (order 0), which then runs it."""
+    from ivonar_amd import runtime
+
+    splits = runtime.gemm_plan(m, rows, k)
+    if splits == 0:
+        return 0, runtime.gemv_plan(rows, k)[0]
+    return 1, splits
+
+
+def token_gemm_expected(oracle, epi: int, q8, xsum, sx, packed, scale_bits, bias, out: np.ndarray, k: int,
+                        out_stride: int, m: int) -> np.ndarray:
+    """gemm_tile_*'s outputs for m tokens in the fp32 order of the kernel that runs them."""
+    rows = packed.shape[0]
+    order, param = token_gemm_order(m, rows, k)
+    if order == 1:
+        return oracle.gemm_split(epi, q8, xsum, sx, packed, scale_bits, bias, out, k, out_stride, m, param)
+    assert m == 1 and out.shape[0] == 1
+    oracle.gemv_pairs(epi, q8[0], xsum[0], sx[0], packed, scale_bits, bias, out[0], k, param)
+    return out

@@ -24,7 +24,7 @@ import pytest
 
 import ternary_oracle as T
 from _util import (assert_bits_equal, assert_within, big_layer, device_matrix, finish_all_rows, reference_lanes,
-                   to_np)
+                   to_np, token_gemm_order)
 
 pytestmark = pytest.mark.gpu
 
@@ -158,8 +158,8 @@ def _sweep():
 def test_m_sweep_every_row(cuda, oracle, m):
     """K=4096->N=14336 with the sweep's statistics; every output row of every token bit-exact.
 
-    M=256 runs the 64-token long-prompt tiles (the 128-token grid has 112 blocks), M=512 and 2048
-    the 128-token tiles, M=128 the split-K kernel."""
+    M=1 runs the decode GEMV on the pre-quantized row, M=256 the 64-token long-prompt tiles (the
+    128-token grid has 112 blocks), M=512 and 2048 the 128-token tiles, M=128 the split-K kernel."""
     from ivonar_amd import ops, runtime
 
     print(f"m sweep m={m}", flush=True)
@@ -178,10 +178,13 @@ def test_m_sweep_every_row(cuda, oracle, m):
         assert splits == 1, "long-prompt tiles (one fmaf chain per output)"
     if m == 128:
         assert splits == 4, "split-K kernel"
+    if m == 1:
+        assert splits == 0, "one token runs the decode GEMV"
+    order, param = token_gemm_order(m, rows, k)
     q = T.q8_linear(q8, k)
-    expected = finish_all_rows(oracle, 1, splits, T.EPI_STORE, codes, q, scale_bits, sx, None,
+    expected = finish_all_rows(oracle, order, param, T.EPI_STORE, codes, q, scale_bits, sx, None,
                                np.zeros((m, rows), np.float32), k, rows)
-    assert_bits_equal(y, expected, f"gemm m={m} ({splits} splits), every row")
+    assert_bits_equal(y, expected, f"gemm m={m} (order {order}, {param}), every row")
     truth = T.truth_fp64(oracle.group_partials(q8[0], xsum[0], packed, rows, k), T.half_bits_to_float(scale_bits),
                          sx[0])
     assert_within(y[0], truth, what="token 0 vs fp64 truth")

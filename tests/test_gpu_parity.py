@@ -15,7 +15,7 @@ import pytest
 
 import ternary_oracle as T
 from _util import (ATOL, RTOL, assert_bits_equal, assert_within, device_matrix, finish_all_rows, make_layer,
-                   reference_lanes, to_np)
+                   reference_lanes, to_np, token_gemm_expected, token_gemm_order)
 
 pytestmark = pytest.mark.gpu
 
@@ -28,13 +28,15 @@ def _t(array, device):
     return torch.from_numpy(np.ascontiguousarray(array)).to(device)
 
 
-def _every_row(oracle, codes, x, k, scale_bits, bias, splits, epi=None, out=None, stride=None):
-    """The token GEMM's expected output for every token and row, in the kernel's split order."""
+def _every_row(oracle, codes, x, k, scale_bits, bias, plan, epi=None, out=None, stride=None):
+    """The token GEMM's expected output for every token and row, in the kernel's fp32 order: `plan` is
+    the K-splits of the split order, or (order, param) as token_gemm_order gives them."""
+    order, param = plan if isinstance(plan, tuple) else (1, plan)
     m, rows = x.shape[0], codes.shape[0]
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
     epi = T.EPI_STORE if epi is None else epi
     out = np.zeros((m, rows), np.float32) if out is None else out
-    return finish_all_rows(oracle, 1, splits, epi, codes, T.q8_linear(eq8, k), scale_bits, esx, bias, out, k,
+    return finish_all_rows(oracle, order, param, epi, codes, T.q8_linear(eq8, k), scale_bits, esx, bias, out, k,
                            rows if stride is None else stride)
 
 
@@ -350,10 +352,11 @@ def test_gemm_tile_store(cuda, oracle, m, k, rows):
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
     assert_bits_equal(to_np(q8), eq8, "tile q8")
-    splits = runtime.gemm_plan(m, rows, k)
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
-                                 np.zeros((m, rows), np.float32), k, rows, m, splits)
-    assert_bits_equal(y, expected, f"gemm vs oracle (kernel order, {splits} splits)")
+    expected = token_gemm_expected(oracle, T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, b,
+                                   np.zeros((m, rows), np.float32), k, rows, m)
+    assert_bits_equal(y, expected, f"gemm vs oracle (kernel order {token_gemm_order(m, rows, k)})")
+    if m == 1:
+        assert runtime.gemm_plan(m, rows, k) == 0, "one token runs the decode GEMV"
     ref = oracle.reforder(T.EPI_STORE, True, eq8, exsum, esx, packed, scale_bits, b, np.zeros((m, rows), np.float32),
                           k, reference_lanes(k, rows), rows, m)
     assert_within(y, ref, what="gemm vs reference-kernel order")
@@ -534,9 +537,9 @@ def test_gemm_large_tiles_every_token(cuda, oracle, m, k, rows):
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
-    splits = runtime.gemm_plan(m, rows, k)
-    expected = _every_row(oracle, codes, x, k, scale_bits, b, splits)
-    assert_bits_equal(y, expected, f"every token ({splits} splits)")
+    plan = token_gemm_order(m, rows, k)
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, plan)
+    assert_bits_equal(y, expected, f"every token (order {plan})")
 
 
 @pytest.mark.parametrize("m", [1, 3, 16, 32])
@@ -552,10 +555,9 @@ def test_gemm_small_m_split_order(cuda, oracle, m, k, rows):
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
-    splits = runtime.gemm_plan(m, rows, k)
-    expected = oracle.gemm_split(T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, None,
-                                 np.zeros((m, rows), np.float32), k, rows, m, splits)
-    assert_bits_equal(y, expected, f"skinny gemm ({splits} splits)")
+    expected = token_gemm_expected(oracle, T.EPI_STORE, eq8, exsum, esx, packed, scale_bits, None,
+                                   np.zeros((m, rows), np.float32), k, rows, m)
+    assert_bits_equal(y, expected, f"skinny gemm (order {token_gemm_order(m, rows, k)})")
     q, s = T.quantize_closed_form(x[0])
     truth = T.truth_fp64(T.group_partials_int64(codes, q), T.half_bits_to_float(scale_bits), s)
     assert_within(y[0], truth, what="skinny gemm vs fp64 truth")
@@ -583,8 +585,8 @@ def test_gemm_skinny_kernels(cuda, oracle, m, k, rows, bias, splits):
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     if m > 16:  # up to 16 tokens the few-token GEMV runs (its own plan, tests/test_gpu_tokens.py)
         assert runtime.gemm_plan(m, rows, k) == splits
-    splits = runtime.gemm_plan(m, rows, k)
-    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, splits), f"every token ({splits} splits)")
+    plan = token_gemm_order(m, rows, k)
+    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, plan), f"every token (order {plan})")
 
 
 # Prompts of 33..512 tokens that neither long-prompt tiling takes (few row blocks, few groups) run the

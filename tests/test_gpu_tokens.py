@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import ternary_oracle as T
-from _util import assert_bits_equal, assert_within, device_matrix, finish_all_rows, make_layer, to_np
+from _util import assert_bits_equal, assert_within, device_matrix, finish_all_rows, make_layer, to_np, token_gemm_order
 
 pytestmark = pytest.mark.gpu
 
@@ -44,10 +44,11 @@ def _case(oracle, cuda, m, k, rows, bias, seed, epilogue="store", pad=0):
         (m, stride), np.float32)
     out = _t(base, cuda)
     ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
-    splits = runtime.gemm_plan(m, rows, k)
+    order, param = token_gemm_order(m, rows, k)
+    splits = param if order == 1 else runtime.gemm_plan(m, rows, k)
     epi = {"store": T.EPI_STORE, "residual": T.EPI_RESIDUAL, "silu_pair": T.EPI_SILU_PAIR}[epilogue]
     q = T.q8_linear(eq8, k)
-    expected = finish_all_rows(oracle, 1, splits, epi, codes, q, scale_bits, esx, b, base.copy(), k, stride)
+    expected = finish_all_rows(oracle, order, param, epi, codes, q, scale_bits, esx, b, base.copy(), k, stride)
     got = to_np(out)
     assert_bits_equal(got, expected, f"token gemv m={m} k={k} rows={rows} ({splits} splits)")
     if pad:
@@ -62,7 +63,8 @@ def _case(oracle, cuda, m, k, rows, bias, seed, epilogue="store", pad=0):
 # (m, k, rows, bias, K-splits of the plan on a 256-CU device): the plan takes the longest span range
 # per wave that still gives every CU eight waves, else one span per wave.
 @pytest.mark.parametrize("m,k,rows,bias,splits", [
-    (1, 1024, 4096, False, 4),     # 4 spans, 1 per wave
+    (1, 1024, 4096, False, 0),     # one token: the decode GEMV (plan 0, its lane order)
+    (2, 1024, 4096, False, 4),     # 4 spans, 1 per wave
     (5, 4096, 1000, True, 16),     # ragged rows, 16 waves per row tile
     (3, 8192, 8200, True, 4),      # 8 spans per wave, ragged rows
     (8, 2048, 16384, False, 2),    # 4 spans per wave
@@ -202,10 +204,10 @@ def test_token_gemm_padded_scale_rows(cuda, oracle, m, k, rows, extra):
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     eq8, _, esx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
     out = ops.gemm(matrix, q8, xsum, sx)
-    splits = runtime.gemm_plan(m, rows, k)
-    expected = finish_all_rows(oracle, 1, splits, T.EPI_STORE, codes, T.q8_linear(eq8, k), scale_bits, esx, b,
+    order, param = token_gemm_order(m, rows, k)
+    expected = finish_all_rows(oracle, order, param, T.EPI_STORE, codes, T.q8_linear(eq8, k), scale_bits, esx, b,
                                np.zeros((m, rows), np.float32), k, rows)
-    assert_bits_equal(to_np(out), expected, f"padded scales m={m} k={k} rows={rows} ({splits} splits)")
+    assert_bits_equal(to_np(out), expected, f"padded scales m={m} k={k} rows={rows} (order {order}, {param})")
 
 
 @pytest.mark.parametrize("k", [1024, 8192, 28672])

@@ -69,7 +69,8 @@ def test_host_only_calls():
     assert lib.ivonar_define(b"GEMV_WAIT_SPINS", 1) != 0  # no in-launch wait to bound any more
     assert lib.ivonar_error_string(1)
     assert runtime.gemm_plan(2048, 4096, 1024) == 1
-    assert runtime.gemm_plan(1, 4096, 1024) >= 1
+    assert runtime.gemm_plan(1, 4096, 1024) == 0  # one token: the decode GEMV
+    assert runtime.gemm_plan(2, 4096, 1024) >= 1
     for n, expected in [(8, 2), (64, 2), (100, 2), (1024, 16), (4096, 64), (8192, 64), (28672, 64)]:
         lanes, per_lane = runtime.gemv_plan(100, n)
         assert lanes == expected and per_lane == 2
@@ -172,3 +173,26 @@ def test_decoder_refuses_a_cpu_device():
     weights = decoder_stack(StackConfig(vocab=64, hidden=128, layers=1, dense=256), seed=0)
     with pytest.raises(KernelError):
         StackDecoder(weights, "cpu")
+
+
+def test_sampling_rule_on_host_buffers():
+    """configure_sampling's rule (decoder.py:340-361) on host-resident buffers: the top-k clamp, the
+    penalized ids marked as seen (out-of-vocabulary ids ignored), and the error on a non-positive value."""
+    from ivonar_amd.sampling import DeviceSampler
+
+    sampler = object.__new__(DeviceSampler)
+    sampler.vocab, sampler.max_top_k, sampler.device = 10, 4, torch.device("cpu")
+    sampler.temperature, sampler.penalty, sampler.inverse_penalty = torch.ones(1), torch.ones(1), torch.ones(1)
+    sampler.top_k = torch.ones(1, dtype=torch.int64)
+    sampler.seen = torch.ones((1, 10), dtype=torch.bool)
+    sampler.configure_sampling(0.5, 0, 2.0, penalized_ids=[3, 3, -1, 10, 9])
+    assert sampler.top_k.item() == 4 and sampler.temperature.item() == 0.5
+    assert sampler.penalty.item() == 2.0 and sampler.inverse_penalty.item() == 0.5
+    assert sampler.seen[0].nonzero().flatten().tolist() == [3, 9]
+    sampler.configure_sampling(1.0, 3)
+    assert sampler.top_k.item() == 3 and not sampler.seen.any()
+    sampler.configure_sampling(1.0, 5)
+    assert sampler.top_k.item() == 4
+    for temperature, penalty in ((0.0, 1.0), (1.0, -2.0)):
+        with pytest.raises(ValueError):
+            sampler.configure_sampling(temperature, 3, penalty)
