@@ -138,6 +138,7 @@ class StackDecoder:
         self._tile = self._build_tile()
         self._first = self._head + self._select(self.burst - 1)  # after the last tile
         self._graph: torch.cuda.CUDAGraph | None = None
+        self._tile_graph: torch.cuda.CUDAGraph | None = None
         self.position = 0
 
     # ------------------------------------------------------------------ launch builders
@@ -284,7 +285,10 @@ class StackDecoder:
             self.tile_tokens.zero_()
             self.tile_tokens[:count].copy_(chunk)
             self.tile_valid.fill_(count)
-            self._run(self._tile)
+            if self._tile_graph is not None:
+                self._tile_graph.replay()  # one replay per tile (kernel_decoder.py:444-447)
+            else:
+                self._run(self._tile)
         self._run(self._first)
         self.position = 0
         return self.logits
@@ -299,7 +303,10 @@ class StackDecoder:
     def capture(self) -> bool:
         """Records one burst of decode steps into a HIP graph (kernel_decoder.py:694-719).  With sampling,
         the uniforms are drawn inside the graph, fresh on every replay; the sampler's `seen` is restored
-        after the warm-up and the capture, as the ring is."""
+        after the warm-up and the capture, as the ring is.  Then records the prefill tile program as a
+        second graph (kernel_decoder.py:482-509), which prefill() replays once per 32-token tile after
+        filling the device buffers tile_tokens and tile_valid; the residual the last prefill left is
+        restored after its warm-up and capture."""
         if self.position % self.burst != 0:
             raise KernelError("capture at a burst boundary")
         saved = self.history.clone()
@@ -323,7 +330,24 @@ class StackDecoder:
         if seen is not None:
             self.sampler.seen.copy_(seen)
         self._graph = graph
+        self._tile_graph = self._capture_tile(stream)
         return True
+
+    def _capture_tile(self, stream: torch.cuda.Stream) -> torch.cuda.CUDAGraph:
+        residual, valid = self.residual.clone(), self.tile_valid.clone()
+        self.tile_valid.fill_(TILE)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            self._run(self._tile)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            self._run(self._tile)
+        torch.cuda.synchronize(self.device)
+        self.residual.copy_(residual)
+        self.tile_valid.copy_(valid)
+        return graph
 
     @torch.no_grad()
     def advance_many(self, count: int) -> list[int]:

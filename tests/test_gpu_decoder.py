@@ -120,3 +120,19 @@ def test_sampled_tokens_match_the_oracle(cuda, name):
     assert tokens == expected
     seen = np.flatnonzero(decoder.sampler.seen.cpu().numpy().reshape(-1))
     assert set(seen.tolist()) == {3, 17} | set(tokens)
+
+
+def test_prefill_tile_graph_matches_the_oracle(pair):
+    """After capture() every 32-token tile of a prefill is one replay of the captured tile program: the
+    logits stay bit-exact for prompts of 40, 1 and 32 tokens (two replays, then one, with eager decode steps
+    between), and greedy steps after a graph prefill give the oracle's tokens."""
+    decoder, oracle = pair
+    decoder.prefill(prompt_ids(decoder.config.vocab, 8, seed=9))
+    decoder.capture()
+    assert decoder._tile_graph is not None
+    for length in (40, 1, 32):
+        prompt = prompt_ids(decoder.config.vocab, length, seed=100 + length)
+        logits = decoder.prefill(prompt).cpu().numpy()
+        np.testing.assert_array_equal(logits, oracle.prefill_logits(prompt), err_msg=f"prompt of {length}")
+        first = int(decoder.history[decoder.burst - 1])
+        assert [first] + decoder.advance_many(3) == oracle.generate(prompt, 4)
