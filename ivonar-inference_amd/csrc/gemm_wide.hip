@@ -345,37 +345,66 @@ hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a, int tokens) {
   return launch_wide_shape<EPI, 8, 4>(stream, a);
 }
 
+// Block -> output tile of the split-K kernel.  Blocks are dispatched to the
+// device's 8 XCDs round robin (block b on XCD b % 8), each XCD with its own
+// L2; this mapping gives each XCD a run of consecutive tiles in token-major
+// order (all row tiles of one token tile, then the next), so the q8 rows and
+// weight rows an XCD's blocks read stay in that XCD's L2 (K=4096 -> N=1024 at
+// M=2048: 1 MB of q8 and the whole 1 MB matrix per XCD; 23.6 -> 21 us).
+constexpr int kXcds = 8;
+__device__ __forceinline__ void xcd_tile(int& tile_x, int& tile_y) {
+  const int nx = gridDim.x, nb = gridDim.x * gridDim.y;
+  const int b = blockIdx.x + nx * blockIdx.y;
+  const int q = nb / kXcds, r = nb % kXcds;
+  const int xcd = b % kXcds, idx = b / kXcds;
+  const int t = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+  tile_x = t % nx;
+  tile_y = t / nx;
+}
+
 // Split-K variant for long prompts with few output rows (K=4096 -> N=1024 at
 // M=2048 has only 64 tiles of 128 x 256): a block of four waves owns one
-// 128-token x 64-row output tile and wave w walks the contiguous group range
-// [w*per, (w+1)*per), per = ceil(G/4).  Each wave stages its own operands
-// (its own two-stage ring of direct-to-LDS loads) and runs the same
-// fixed-order MFMA/fold units as gemm_wide_kernel.  A stage is read after the
+// 16*MT-token x 64-row output tile and wave w walks the contiguous group
+// range [w*per, (w+1)*per), per = ceil(G/4).  Each wave stages its own
+// operands (its own two-stage ring of direct-to-LDS loads) and runs the same
+// fixed-order MFMA/fold units as gemm_wide_kernel; the direct-to-LDS loads of
+// the next group are spread over the first units (one per MFMA unit), so
+// that a load instruction that waits for the memory pipeline to accept it
+// stalls the wave while its MFMAs run (issued back to back before the MFMAs,
+// they took 0.85 us of a 1.9 us step at M=512).  A stage is read after the
 // loading wave's vmcnt wait, lgkmcnt(0) and a workgroup barrier
 // (direct_load_sync), so every wave runs `per` steps: a wave with fewer
 // groups (or none) loads again and skips the compute in the steps it lacks,
 // and reaches every barrier.  The four partial tiles are then added in wave
 // order through LDS - the order the CPU oracle restates as orc_gemm_split(4):
 // each range an fmaf chain, total = ((s0 + s1) + s2) + s3 - scaled by s_x and
-// biased, and stored as 16-byte vectors.
+// biased, and stored as 16-byte vectors.  MT (8, 4 or 2: 128, 64 or 32 token
+// rows) is chosen by the launcher so that the grid fills the CUs; it does not
+// change the order.
 constexpr int kSplitWaves = 4;
-constexpr int kSplitTokens = 128;
 constexpr int kSplitRows = 64;
-constexpr int kSplitStage = kSplitTokens * 128 + kSplitRows * 32;  // A then B, one group
-constexpr int kSplitDmaA = kSplitTokens * 8 / 64;                  // 16-byte pieces per lane and group
-constexpr int kSplitPitch = 68;                                    // floats per token row of a partial tile
+constexpr int kSplitPitch = 68;  // floats per token row of a partial tile
 
-template <int EPI>
+template <int MT>
+struct SplitTile {
+  static constexpr int kTokens = 16 * MT;
+  static constexpr int kStage = kTokens * 128 + kSplitRows * 32;  // A then B, one group
+  static constexpr int kDmaA = kTokens * 8 / 64;                  // 16-byte pieces per lane and group
+  static constexpr int kDma = kDmaA + 2;                          // direct-to-LDS loads per lane and group
+  static_assert(kDma <= 8 * MT, "one load per MFMA unit at most");
+};
+
+template <int EPI, int MT>
 __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8_t* __restrict__ q8,
                                                                      const float* __restrict__ scale_in,
                                                                      const uint8_t* __restrict__ packed,
                                                                      const uint16_t* __restrict__ scales,
                                                                      const float* __restrict__ bias,
                                                                      float* __restrict__ output, GemmArgs a) {
-  constexpr int MT = kSplitTokens / 16;
-  __shared__ __align__(16) unsigned char stages[kSplitWaves][2][kSplitStage];
+  using T = SplitTile<MT>;
+  __shared__ __align__(16) unsigned char stages[kSplitWaves][2][T::kStage];
   __shared__ __align__(16) float row_scales[kSplitWaves][2][kSplitRows];
-  static_assert(kSplitWaves * kSplitTokens * kSplitPitch * 4 <= (int)sizeof(stages), "partial tiles fit");
+  static_assert(kSplitWaves * T::kTokens * kSplitPitch * 4 <= (int)sizeof(stages), "partial tiles fit");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -383,8 +412,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   const int chunks = (a.n + kChunk - 1) / kChunk;
   const int groups = (a.n + kGroup - 1) / kGroup;
   const int q8_stride = chunks * kChunk;
-  const int token0 = blockIdx.y * kSplitTokens;
-  const int row0 = blockIdx.x * kSplitRows;
+  int tile_x, tile_y;
+  xcd_tile(tile_x, tile_y);
+  const int token0 = tile_y * T::kTokens;
+  const int row0 = tile_x * kSplitRows;
   const int per = (groups + kSplitWaves - 1) / kSplitWaves;
   const int g_begin = min(wave * per, groups), g_end = min(g_begin + per, groups);
   constexpr int kPast = 0x7FFFFFF0;
@@ -406,16 +437,18 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   const int b_off = (row0 + lane) * a.row_bytes;
   const int s_off = (row0 + lane) * a.groups * 2;
 
-  auto dma = [&](int g, int stage) {
-    const bool second_live = 2 * g + 1 < chunks;
+  // Direct-to-LDS load j (< kDma) of group g into stage `stage`: A pieces
+  // first, then the two B pieces.
+  auto dma = [&](int g, int stage, int j) {
     const unsigned base = __builtin_amdgcn_readfirstlane(lds_address(stages[wave][stage]));
-#pragma unroll
-    for (int j = 0; j < kSplitDmaA; ++j) {
+    if (j < T::kDmaA) {
+      const bool second_live = 2 * g + 1 < chunks;
       const int live = a_base[j & 1] + j * a_step;
       dma16(q8_buf, base + j * 64 * 16, second_live || !a_second[j & 1] ? live : kPast, g * kGroup);
+    } else {
+      const int jb = j - T::kDmaA;
+      dma16(w_buf, base + T::kTokens * 128 + jb * 64 * 16, b_off + jb * 16, g * 32);
     }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(w_buf, base + kSplitTokens * 128 + j * 64 * 16, b_off + j * 16, g * 32);
   };
   // The row scale of a group (lane: row lane of the tile), written to LDS as
   // fp32 once every load of the wave has retired: the scale arrived and the
@@ -443,14 +476,16 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   }
   const int b_read = ((kb >> 1) * kSplitRows + col) * 16 + (kb & 1) * 8;
 
-  auto compute = [&](int cur) {
+  // The MFMAs and fold of the group in stage `cur`, with the loads of group
+  // g_fill into stage `fill` issued one per unit.
+  auto compute = [&](int cur, int g_fill, int fill) {
     const unsigned char* base = stages[wave][cur];
     const v4i zero = {0, 0, 0, 0};
     uint2 w[4];
     float sc[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      w[nt] = *reinterpret_cast<const uint2*>(base + kSplitTokens * 128 + b_read + nt * 16 * 16);
+      w[nt] = *reinterpret_cast<const uint2*>(base + T::kTokens * 128 + b_read + nt * 16 * 16);
       sc[nt] = row_scales[wave][cur][col + nt * 16];
     }
     auto operands = [&](int mt, v4i& a0, v4i& a1) {
@@ -477,6 +512,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
                           (int)signed_codes(x, 3)};
         }
         p[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? a1 : a0, bf[h][nt], h ? p[nt] : zero, 0, 0, 0);
+        if (mt * 8 + u < T::kDma) dma(g_fill, fill, mt * 8 + u);
         const int ft = u >> 1, fi = (u & 1) * 2;
         acc[fold_row][ft][fi] = __builtin_fmaf((float)prev[ft][fi], prev_sc[ft], acc[fold_row][ft][fi]);
         acc[fold_row][ft][fi + 1] = __builtin_fmaf((float)prev[ft][fi + 1], prev_sc[ft], acc[fold_row][ft][fi + 1]);
@@ -495,13 +531,17 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
     }
   };
 
-  // One group step: the next group's loads into stage `fill`, then (a wave
-  // with a group left, `live`) the MFMAs and fold on stage `cur`, then the
-  // wait that retires the loads of `fill` and the workgroup barrier.
+  // One group step: the next group's loads into stage `fill` (inside the
+  // MFMAs of stage `cur` when the wave has a group left, `live`; else on
+  // their own), then the wait that retires them and the workgroup barrier.
   auto step = [&](int cur, int fill, int g_fill, bool live) {
     int scale = scale_load(g_fill);
-    dma(g_fill, fill);
-    if (live) compute(cur);
+    if (live) {
+      compute(cur, g_fill, fill);
+    } else {
+#pragma unroll
+      for (int j = 0; j < T::kDma; ++j) dma(g_fill, fill, j);
+    }
     scale_store(scale, fill);
     direct_load_sync();
   };
@@ -512,7 +552,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   {
     const int g0 = min(g_begin, groups - 1);
     int s0 = scale_load(g0);
-    dma(g0, 0);
+#pragma unroll
+    for (int j = 0; j < T::kDma; ++j) dma(g0, 0, j);
     scale_store(s0, 0);
     direct_load_sync();
   }
@@ -529,10 +570,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
     for (int i = 0; i < 4; ++i) acc[MT - 1][nt][i] = __builtin_fmaf((float)prev[nt][i], prev_sc[nt], acc[MT - 1][nt][i]);
 
   // Partial tiles of the four waves into LDS (the stages are free once every
-  // wave is here), then wave w finishes tokens 32w .. 32w + 31.
+  // wave is here), then wave w finishes tokens 4*MT*w .. 4*MT*w + 4*MT - 1.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   float* tiles = reinterpret_cast<float*>(&stages[0][0][0]);
-  float* own = tiles + wave * kSplitTokens * kSplitPitch;
+  float* own = tiles + wave * T::kTokens * kSplitPitch;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -552,13 +593,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   const bool vec4 = (a.out_stride & 3) == 0 && (base_addr & 15) == 0;
   const bool vec2 = (a.out_stride & 1) == 0 && (base_addr & 7) == 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int tl = wave * 32 + j * 4 + (lane >> 4);
+  for (int j = 0; j < MT; ++j) {
+    const int tl = wave * 4 * MT + j * 4 + (lane >> 4);
     const int t = token0 + tl;
     f4v total = *reinterpret_cast<const f4v*>(tiles + tl * kSplitPitch + r4);
 #pragma unroll
     for (int w = 1; w < kSplitWaves; ++w)
-      total = total + *reinterpret_cast<const f4v*>(tiles + (w * kSplitTokens + tl) * kSplitPitch + r4);
+      total = total + *reinterpret_cast<const f4v*>(tiles + (w * T::kTokens + tl) * kSplitPitch + r4);
     if (t >= a.m) continue;
     const float sx = scale_in[t];
     float y[4];
@@ -596,12 +637,34 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   }
 }
 
-template <int EPI>
-hipError_t launch_split_epi(hipStream_t stream, const GemmArgs& a) {
-  const dim3 grid(ceil_div(a.rows, kSplitRows), ceil_div(a.m, kSplitTokens));
-  hipLaunchKernelGGL((gemm_split_kernel<EPI>), grid, dim3(64 * kSplitWaves), 0, stream, a.q8_in, a.scale_in,
+// Token rows per split-K tile: the largest of 128, 64, 32 whose grid keeps
+// three quarters of the CUs busy (else 32).  K=4096 -> N=1024 at M=512: 32
+// (256 blocks), 11.4 us against 19.1 us with 128 (64 blocks); K=4096 ->
+// N=14336 at M=128: 128 (224 blocks), 20.4 us against 24.5 us with 64.
+int split_tokens(int m, int rows) {
+  const long long row_tiles = ceil_div(rows, kSplitRows);
+  const int busy = device_cus() * 3 / 4;
+  for (int tokens : {128, 64}) {
+    if (row_tiles * ceil_div(m, tokens) >= busy) return tokens;
+  }
+  return 32;
+}
+
+template <int EPI, int MT>
+hipError_t launch_split_shape(hipStream_t stream, const GemmArgs& a) {
+  const dim3 grid(ceil_div(a.rows, kSplitRows), ceil_div(a.m, SplitTile<MT>::kTokens));
+  hipLaunchKernelGGL((gemm_split_kernel<EPI, MT>), grid, dim3(64 * kSplitWaves), 0, stream, a.q8_in, a.scale_in,
                      a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_split_epi(hipStream_t stream, const GemmArgs& a) {
+  switch (split_tokens(a.m, a.rows)) {
+    case 128: return launch_split_shape<EPI, 8>(stream, a);
+    case 64: return launch_split_shape<EPI, 4>(stream, a);
+    default: return launch_split_shape<EPI, 2>(stream, a);
+  }
 }
 
 }  // namespace
@@ -648,7 +711,7 @@ hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
 // Measured: K=4096 -> N=1024 at M=2048 25.0 us and K=4096 -> N=14336 at
 // M=128 22.0 us, against 45.4 and 42.6 us for the 64 x 64-wave-tile kernel.
 bool gemm_split_applies(int m, int rows, int n) {
-  const long long tiles = (long long)ceil_div(rows, kSplitRows) * ceil_div(m, kSplitTokens);
+  const long long tiles = (long long)ceil_div(rows, kSplitRows) * ceil_div(m, 128);
   return m > 32 && gemm_wide_tokens(m, rows, n) == 0 && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
 }
 

@@ -228,7 +228,7 @@ def test_ternary_linear_forward(cuda, oracle, m):
 
 
 @pytest.mark.parametrize("shape", [(1024, 4096), (4096, 1024)])
-@pytest.mark.parametrize("length", [32, 128, 2048])
+@pytest.mark.parametrize("length", [32, 128, 512, 2048])
 def test_prefill_outlier_channels_every_row(cuda, oracle, shape, length):
     """Prompts with the bench's outlier channels, as one launch and as the reference's 32-token tiles."""
     import torch

@@ -748,10 +748,12 @@ def test_gemm_wide_64_token_tiles_long_k(cuda, oracle, epilogue):
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
-# Long prompts with few output rows run the split-K kernel (four waves per 128 x 64 tile, each a
-# contiguous quarter of the groups, added in order): its plan reports 4 splits.  Ragged tokens and
-# rows, an odd chunk count with a group count not divisible by four, bias, and both epilogues.
-# Prompts of 33..127 tokens fill one partial token tile (the rows past the prompt read zeros).
+# Long prompts with few output rows run the split-K kernel (four waves per 128, 64 or 32-token x 64-row
+# tile, each a contiguous quarter of the groups, added in order): its plan reports 4 splits.  Ragged
+# tokens and rows, an odd chunk count with a group count not divisible by four, bias, and both
+# epilogues; the cases cover all three token tiles (M=2048 and 70 tokens over 14336 rows: 128; 1000
+# tokens and the epilogues: 64; 33 and 127 tokens: 32).  Prompts of 33..127 tokens fill one partial
+# token tile (the rows past the prompt read zeros).
 @pytest.mark.parametrize("m,k,rows,bias", [(1000, 4160, 1000, True), (2048, 2048, 1024, False),
                                           (2048, 4096, 1024, True), (33, 2048, 2048, False),
                                           (70, 4096, 14336, True), (127, 2176, 3000, False)])
