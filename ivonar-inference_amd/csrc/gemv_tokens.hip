@@ -23,8 +23,8 @@
 // quantizer's layout, 8-byte pieces gathered into MFMA operand order) and the
 // group q sums into LDS once, after its waves have issued their first weight
 // loads; all waves then read their operands from LDS.  Weights stream through
-// a register ring UW spans deep; all scales of the wave's range are loaded up
-// front.
+// a register ring UW spans deep (kRing); all scales of the wave's range are
+// loaded up front.
 //
 // Long rows.  Where the tokens' whole q8 rows do not fit in LDS, K is cut
 // into `slices` equal span ranges, one per block row of the grid (grid y):
@@ -50,7 +50,11 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxTokens = 16;
 constexpr int kMaxWaves = 16;
-constexpr int kRing = 8;            // spans of weights in flight per wave
+// Spans of weights in flight per wave.  Deeper rings only queue loads the
+// CU cannot take yet (the wave then stalls at issue): 1..16 tokens over
+// K=8192 -> N=28672 and K=28672 -> N=8192 take 3-6% longer with 8 spans than
+// with 4, and 10-20% longer with 16; 2, 3, 5 and 6 are within 2% of 4.
+constexpr int kRing = 4;
 constexpr int kSeedsPerThread = 4;  // group q sums each thread copies
 constexpr int kSpanBytes = 64;
 constexpr int kMaxSlices = 16;
