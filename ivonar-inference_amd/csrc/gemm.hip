@@ -382,7 +382,7 @@ int gemm_splits(int m, int rows, int n) {
   const TokenPlan tokens = token_gemv_plan(m, rows, n, device_cus(), lds);
   if (tokens.parts > 0) return tokens.parts * tokens.slices;
   if (gemm_wide_tokens(m, rows, n) > 0) return 1;
-  if (gemm_split_applies(m, rows, n)) return 4;
+  if (gemm_split_applies(m, rows, n)) return split_waves(m, rows, n);
   const SkinnyPlan plan = skinny_plan(m, rows, n, lds);
   return plan.splits > 0 ? plan.splits : 1;
 }

@@ -363,9 +363,10 @@ __device__ __forceinline__ void xcd_tile(int& tile_x, int& tile_y) {
 }
 
 // Split-K variant for long prompts with few output rows (K=4096 -> N=1024 at
-// M=2048 has only 64 tiles of 128 x 256): a block of four waves owns one
-// 16*MT-token x 64-row output tile and wave w walks the contiguous group
-// range [w*per, (w+1)*per), per = ceil(G/4).  Each wave stages its own
+// M=2048 has only 64 tiles of 128 x 256): a block of SW waves (4, or 8 with
+// 32-token tiles and at least 32 groups) owns one 16*MT-token x 64-row output
+// tile and wave w walks the contiguous group range [w*per, (w+1)*per),
+// per = ceil(G/SW).  Each wave stages its own
 // operands (its own two-stage ring of direct-to-LDS loads) and runs the same
 // fixed-order MFMA/fold units as gemm_wide_kernel; the direct-to-LDS loads of
 // the next group are spread over the first units (one per MFMA unit), so
@@ -375,13 +376,16 @@ __device__ __forceinline__ void xcd_tile(int& tile_x, int& tile_y) {
 // loading wave's vmcnt wait, lgkmcnt(0) and a workgroup barrier
 // (direct_load_sync), so every wave runs `per` steps: a wave with fewer
 // groups (or none) loads again and skips the compute in the steps it lacks,
-// and reaches every barrier.  The four partial tiles are then added in wave
-// order through LDS - the order the CPU oracle restates as orc_gemm_split(4):
-// each range an fmaf chain, total = ((s0 + s1) + s2) + s3 - scaled by s_x and
+// and reaches every barrier.  The SW partial tiles are then added in wave
+// order through LDS - the order the CPU oracle restates as orc_gemm_split(SW):
+// each range an fmaf chain, total = ((s0 + s1) + s2) + ... - scaled by s_x and
 // biased, and stored as 16-byte vectors.  MT (8, 4 or 2: 128, 64 or 32 token
 // rows) is chosen by the launcher so that the grid fills the CUs; it does not
-// change the order.
-constexpr int kSplitWaves = 4;
+// change the order.  Eight waves halve each wave's dependent steps and put two
+// waves on each SIMD; with 32- and 64-token tiles each wave keeps three stages
+// (two groups in flight).  K=4096 -> N=1024 at M=512: 11.4 us with four waves
+// and two stages, 10.9 with eight waves, 10.5 with three stages; at M=1024
+// (64-token tiles, four waves) 14.9 -> 14.0 us.
 constexpr int kSplitRows = 64;
 constexpr int kSplitPitch = 68;  // floats per token row of a partial tile
 
@@ -394,17 +398,19 @@ struct SplitTile {
   static_assert(kDma <= 8 * MT, "one load per MFMA unit at most");
 };
 
-template <int EPI, int MT>
-__global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8_t* __restrict__ q8,
+template <int EPI, int MT, int SW, int NS>
+__global__ __launch_bounds__(64 * SW) void gemm_split_kernel(const int8_t* __restrict__ q8,
                                                                      const float* __restrict__ scale_in,
                                                                      const uint8_t* __restrict__ packed,
                                                                      const uint16_t* __restrict__ scales,
                                                                      const float* __restrict__ bias,
                                                                      float* __restrict__ output, GemmArgs a) {
   using T = SplitTile<MT>;
-  __shared__ __align__(16) unsigned char stages[kSplitWaves][2][T::kStage];
-  __shared__ __align__(16) float row_scales[kSplitWaves][2][kSplitRows];
-  static_assert(kSplitWaves * T::kTokens * kSplitPitch * 4 <= (int)sizeof(stages), "partial tiles fit");
+  static_assert(NS == 2 || NS == 3, "two or three stages per wave");
+  __shared__ __align__(16) unsigned char stages[SW][NS][T::kStage];
+  __shared__ __align__(16) float row_scales[SW][NS][kSplitRows];
+  static_assert(SW * T::kTokens * kSplitPitch * 4 <= (int)sizeof(stages), "partial tiles fit");
+  static_assert(T::kTokens % (4 * SW) == 0, "each wave finishes whole rows of four tokens");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -416,7 +422,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   xcd_tile(tile_x, tile_y);
   const int token0 = tile_y * T::kTokens;
   const int row0 = tile_x * kSplitRows;
-  const int per = (groups + kSplitWaves - 1) / kSplitWaves;
+  const int per = (groups + SW - 1) / SW;
   const int g_begin = min(wave * per, groups), g_end = min(g_begin + per, groups);
   constexpr int kPast = 0x7FFFFFF0;
 
@@ -531,37 +537,85 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
     }
   };
 
-  // One group step: the next group's loads into stage `fill` (inside the
-  // MFMAs of stage `cur` when the wave has a group left, `live`; else on
-  // their own), then the wait that retires them and the workgroup barrier.
-  auto step = [&](int cur, int fill, int g_fill, bool live) {
-    int scale = scale_load(g_fill);
-    if (live) {
-      compute(cur, g_fill, fill);
-    } else {
+  if constexpr (NS == 2) {
+    // One group step: the next group's loads into stage `fill` (inside the
+    // MFMAs of stage `cur` when the wave has a group left, `live`; else on
+    // their own), then the wait that retires them and the workgroup barrier.
+    auto step = [&](int cur, int fill, int g_fill, bool live) {
+      int scale = scale_load(g_fill);
+      if (live) {
+        compute(cur, g_fill, fill);
+      } else {
 #pragma unroll
-      for (int j = 0; j < T::kDma; ++j) dma(g_fill, fill, j);
-    }
-    scale_store(scale, fill);
-    direct_load_sync();
-  };
+        for (int j = 0; j < T::kDma; ++j) dma(g_fill, fill, j);
+      }
+      scale_store(scale, fill);
+      direct_load_sync();
+    };
 
-  // Every wave runs `per` steps and passes every barrier; a wave whose range
-  // is shorter (or empty) loads its last group (or the matrix's last) again
-  // and skips the compute.
-  {
-    const int g0 = min(g_begin, groups - 1);
-    int s0 = scale_load(g0);
+    // Every wave runs `per` steps and passes every barrier; a wave whose range
+    // is shorter (or empty) loads its last group (or the matrix's last) again
+    // and skips the compute.
+    {
+      const int g0 = min(g_begin, groups - 1);
+      int s0 = scale_load(g0);
 #pragma unroll
-    for (int j = 0; j < T::kDma; ++j) dma(g0, 0, j);
-    scale_store(s0, 0);
-    direct_load_sync();
-  }
-  int cur = 0;
-  for (int i = 0; i < per; ++i) {
-    const int g = g_begin + i;
-    step(cur, cur ^ 1, max(min(g + 1, g_end - 1), 0), g < g_end);
-    cur ^= 1;
+      for (int j = 0; j < T::kDma; ++j) dma(g0, 0, j);
+      scale_store(s0, 0);
+      direct_load_sync();
+    }
+    int cur = 0;
+    for (int i = 0; i < per; ++i) {
+      const int g = g_begin + i;
+      step(cur, cur ^ 1, max(min(g + 1, g_end - 1), 0), g < g_end);
+      cur ^= 1;
+    }
+  } else {
+    // Three stages, two groups in flight: step i computes stage i % 3 while
+    // the loads of group i + 2 of the wave's range (and its scale) go to stage
+    // (i + 2) % 3.  Its end retires the loads of group i + 1, issued one step
+    // earlier (those of group i + 2, issued after them, stay in flight:
+    // vmcnt(kDma + 1)), writes that group's scale to LDS and passes rule 5's
+    // barrier.  The scales of groups i + 1 and i + 2 sit in two registers that
+    // swap roles from step to step (the loop is unrolled by two), so no copy
+    // ever reads a register whose load is still in flight.
+    //
+    // A step past the wave's range (a wave with fewer groups, or none) runs
+    // the same code on the range's last group again (the matrix's last group
+    // for an empty range) with its scale written as 0: every fold of that
+    // step is fmaf(P, 0, acc) with P a finite integer, which returns acc
+    // unchanged (acc starts at +0 and no fmaf of finite values with positive
+    // scales makes it -0), so the sums are those of the range alone.  With no
+    // branch between the live and the padding steps, every path issues the
+    // same loads before each counter wait.
+    auto gload = [&](int i) { return max(min(g_begin + i, g_end - 1), 0); };
+    auto retire = [&](int& pending, int stage, bool live) {
+      asm volatile("s_waitcnt vmcnt(%1)" : "+v"(pending) : "n"(T::kDma + 1) : "memory");
+      row_scales[wave][stage][lane] = live ? h2f((uint16_t)pending) : 0.0f;
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    int sa = scale_load(gload(0));
+#pragma unroll
+    for (int j = 0; j < T::kDma; ++j) dma(gload(0), 0, j);
+    int sb = scale_load(gload(1));
+#pragma unroll
+    for (int j = 0; j < T::kDma; ++j) dma(gload(1), 1, j);
+    retire(sa, 0, g_begin < g_end);
+    auto step3 = [&](int i, int& pending, int& fresh) {
+      const int cur = i % 3, fill = (i + 2) % 3;
+      const int g_fill = gload(i + 2);
+      fresh = scale_load(g_fill);
+      compute(cur, g_fill, fill);
+      retire(pending, (i + 1) % 3, g_begin + i + 1 < g_end);
+    };
+    int i = 0;
+    for (; i + 1 < per; i += 2) {
+      step3(i, sb, sa);
+      step3(i + 1, sa, sb);
+    }
+    if (i < per) step3(i, sb, sa);
+    // The last scale loads keep their registers until they have landed.
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(sa), "+v"(sb)::"memory");
   }
   // The last row of tiles; a wave without groups folds zeros.
 #pragma unroll
@@ -569,8 +623,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[MT - 1][nt][i] = __builtin_fmaf((float)prev[nt][i], prev_sc[nt], acc[MT - 1][nt][i]);
 
-  // Partial tiles of the four waves into LDS (the stages are free once every
-  // wave is here), then wave w finishes tokens 4*MT*w .. 4*MT*w + 4*MT - 1.
+  // Partial tiles of the SW waves into LDS (the stages are free once every
+  // wave is here), then wave w finishes its kTokens / SW tokens.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   float* tiles = reinterpret_cast<float*>(&stages[0][0][0]);
   float* own = tiles + wave * T::kTokens * kSplitPitch;
@@ -592,13 +646,14 @@ __global__ __launch_bounds__(64 * kSplitWaves) void gemm_split_kernel(const int8
   const uintptr_t base_addr = reinterpret_cast<uintptr_t>(output);
   const bool vec4 = (a.out_stride & 3) == 0 && (base_addr & 15) == 0;
   const bool vec2 = (a.out_stride & 1) == 0 && (base_addr & 7) == 0;
+  constexpr int kOwn = T::kTokens / SW;  // tokens each wave finishes
 #pragma unroll
-  for (int j = 0; j < MT; ++j) {
-    const int tl = wave * 4 * MT + j * 4 + (lane >> 4);
+  for (int j = 0; j < kOwn / 4; ++j) {
+    const int tl = wave * kOwn + j * 4 + (lane >> 4);
     const int t = token0 + tl;
     f4v total = *reinterpret_cast<const f4v*>(tiles + tl * kSplitPitch + r4);
 #pragma unroll
-    for (int w = 1; w < kSplitWaves; ++w)
+    for (int w = 1; w < SW; ++w)
       total = total + *reinterpret_cast<const f4v*>(tiles + (w * T::kTokens + tl) * kSplitPitch + r4);
     if (t >= a.m) continue;
     const float sx = scale_in[t];
@@ -650,10 +705,25 @@ int split_tokens(int m, int rows) {
   return 32;
 }
 
-template <int EPI, int MT>
+}  // namespace
+
+// Waves (K-splits) per split-K tile: 8 with 32-token tiles when every wave
+// still gets 4 groups (the stages of 8 waves fit in LDS only at 32 tokens),
+// else 4.  The count is the order's split count, which ivonar_gemm_plan
+// reports.
+int split_waves(int m, int rows, int n) {
+  return split_tokens(m, rows) == 32 && ceil_div(n, kGroup) >= 32 ? 8 : 4;
+}
+
+namespace {
+
+// Three stages per wave where they fit in LDS (32 and 64-token tiles: 150 KB
+// with eight waves, 126 KB with four), two at 128 tokens.
+template <int EPI, int MT, int SW>
 hipError_t launch_split_shape(hipStream_t stream, const GemmArgs& a) {
+  constexpr int NS = MT <= 4 ? 3 : 2;
   const dim3 grid(ceil_div(a.rows, kSplitRows), ceil_div(a.m, SplitTile<MT>::kTokens));
-  hipLaunchKernelGGL((gemm_split_kernel<EPI, MT>), grid, dim3(64 * kSplitWaves), 0, stream, a.q8_in, a.scale_in,
+  hipLaunchKernelGGL((gemm_split_kernel<EPI, MT, SW, NS>), grid, dim3(64 * SW), 0, stream, a.q8_in, a.scale_in,
                      a.packed, a.scales, a.bias, a.output, a);
   return hipGetLastError();
 }
@@ -661,9 +731,11 @@ hipError_t launch_split_shape(hipStream_t stream, const GemmArgs& a) {
 template <int EPI>
 hipError_t launch_split_epi(hipStream_t stream, const GemmArgs& a) {
   switch (split_tokens(a.m, a.rows)) {
-    case 128: return launch_split_shape<EPI, 8>(stream, a);
-    case 64: return launch_split_shape<EPI, 4>(stream, a);
-    default: return launch_split_shape<EPI, 2>(stream, a);
+    case 128: return launch_split_shape<EPI, 8, 4>(stream, a);
+    case 64: return launch_split_shape<EPI, 4, 4>(stream, a);
+    default:
+      if (split_waves(a.m, a.rows, a.n) == 8) return launch_split_shape<EPI, 2, 8>(stream, a);
+      return launch_split_shape<EPI, 2, 4>(stream, a);
   }
 }
 
@@ -712,7 +784,7 @@ hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {
 // M=128 22.0 us, against 45.4 and 42.6 us for the 64 x 64-wave-tile kernel.
 bool gemm_split_applies(int m, int rows, int n) {
   const long long tiles = (long long)ceil_div(rows, kSplitRows) * ceil_div(m, 128);
-  return m > 32 && gemm_wide_tokens(m, rows, n) == 0 && tiles >= 32 && ceil_div(n, kGroup) >= 4 * kSplitWaves;
+  return m > 32 && gemm_wide_tokens(m, rows, n) == 0 && tiles >= 32 && ceil_div(n, kGroup) >= 16;
 }
 
 hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a) {

@@ -121,6 +121,7 @@ hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a);
 // Long-prompt token GEMM split four ways along K (few output rows); its fp32
 // order is four contiguous group ranges added in order.
 bool gemm_split_applies(int m, int rows, int n);
+int split_waves(int m, int rows, int n);  // K-splits of the split-K kernel (4 or 8)
 hipError_t launch_gemm_split(hipStream_t stream, const GemmArgs& a);
 
 // K-splits of the GEMM for m tokens (its fp32 order: S contiguous group ranges,

@@ -748,16 +748,21 @@ def test_gemm_wide_64_token_tiles_long_k(cuda, oracle, epilogue):
     assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
-# Long prompts with few output rows run the split-K kernel (four waves per 128, 64 or 32-token x 64-row
-# tile, each a contiguous quarter of the groups, added in order): its plan reports 4 splits.  Ragged
-# tokens and rows, an odd chunk count with a group count not divisible by four, bias, and both
-# epilogues; the cases cover all three token tiles (M=2048 and 70 tokens over 14336 rows: 128; 1000
-# tokens and the epilogues: 64; 33 and 127 tokens: 32).  Prompts of 33..127 tokens fill one partial
-# token tile (the rows past the prompt read zeros).
-@pytest.mark.parametrize("m,k,rows,bias", [(1000, 4160, 1000, True), (2048, 2048, 1024, False),
-                                          (2048, 4096, 1024, True), (33, 2048, 2048, False),
-                                          (70, 4096, 14336, True), (127, 2176, 3000, False)])
-def test_gemm_split_k_edges(cuda, oracle, m, k, rows, bias):
+# Long prompts with few output rows run the split-K kernel (S waves per 128, 64 or 32-token x 64-row
+# tile, each a contiguous 1/S of the groups, added in order): its plan reports S = 4, or 8 for 32-token
+# tiles with at least 32 groups.  Ragged tokens and rows, an odd chunk count with a group count not
+# divisible by four, bias, and both epilogues; the cases cover all three token tiles (M=2048 and 70
+# tokens over 14336 rows: 128 with two stages; 1000 and 1024 tokens and the epilogues: 64 with three
+# stages; 33, 127, 300 and 512 tokens: 32 with three stages), eight waves (512 and 300 tokens; at
+# K=4160 the eighth wave's range is empty and the seventh has 3 of 5 groups, so padding steps run
+# with zero scales).  Prompts of 33..127 tokens fill one partial token tile (the rows past the prompt
+# read zeros).
+@pytest.mark.parametrize("m,k,rows,bias,splits", [(1000, 4160, 1000, True, 4), (2048, 2048, 1024, False, 4),
+                                                 (2048, 4096, 1024, True, 4), (33, 2048, 2048, False, 4),
+                                                 (70, 4096, 14336, True, 4), (127, 2176, 3000, False, 4),
+                                                 (512, 4096, 1024, True, 8), (300, 4160, 1000, False, 8),
+                                                 (1024, 4096, 1024, False, 4)])
+def test_gemm_split_k_edges(cuda, oracle, m, k, rows, bias, splits):
     from ivonar_amd import ops, runtime
 
     rng = np.random.default_rng(m * 3 + k + rows)
@@ -766,8 +771,8 @@ def test_gemm_split_k_edges(cuda, oracle, m, k, rows, bias):
     matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
     q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
-    assert runtime.gemm_plan(m, rows, k) == 4
-    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, 4), "every token (4 splits)")
+    assert runtime.gemm_plan(m, rows, k) == splits
+    assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, splits), f"every token ({splits} splits)")
     sample = np.unique(np.array([0, 1, 31, 32, 95, 127, 128, 129, m // 2, m - 2, m - 1]) % m)
     eq8, exsum, esx = oracle.quantize_rows(T.MODE_PLAIN, x[sample], k)
     ref = oracle.reforder(T.EPI_STORE, True, eq8, exsum, esx, packed, scale_bits, b,
