@@ -341,6 +341,7 @@ hipError_t launch_wide_shape(hipStream_t stream, const GemmArgs& a) {
 
 template <int EPI>
 hipError_t launch_wide_epi(hipStream_t stream, const GemmArgs& a, int tokens) {
+  if (tokens == 32) return launch_wide_shape<EPI, 2, 4>(stream, a);
   if (tokens == 64) return launch_wide_shape<EPI, 4, 4>(stream, a);
   return launch_wide_shape<EPI, 8, 4>(stream, a);
 }
@@ -741,7 +742,8 @@ hipError_t launch_split_epi(hipStream_t stream, const GemmArgs& a) {
 
 }  // namespace
 
-// Token tile of the long-prompt kernel (0: it does not apply).  128 tokens x
+// Token tile of the long-prompt kernel (0: it does not apply; 32 below 2048
+// inputs where 64-token tiles leave CUs idle, see the end).  128 tokens x
 // 256 rows from 2048 inputs on, where the loop dominates: it pays from about
 // 192 blocks (three quarters of the CUs busy; K=4096 -> N=14336 at M=512, 224
 // blocks: 60.8 us against 66.7 us for the 64 x 64-wave-tile kernel).  Below
@@ -763,7 +765,12 @@ int gemm_wide_tokens(int m, int rows, int n) {
     return fits64 && row_blocks * ceil_div(m, 64) >= 192 ? 64 : 0;
   }
   const bool fits = WideTile<4, 4>::kLdsBytes <= max_lds_per_block();
-  return fits && row_blocks * ceil_div(m, 64) >= 96 ? 64 : 0;
+  if (!fits || row_blocks * ceil_div(m, 64) < 96) return 0;
+  // 32-token tiles where 64-token tiles leave CUs idle (K=1024 -> N=4096 at
+  // M=512: 256 blocks, 10.0 us against 12.5 us with 128 blocks of 64 tokens;
+  // K=1024 -> N=8192 at M=256: 9.6 against 12.3 us), though each expanded
+  // weight fragment then feeds two MFMA rows instead of four.
+  return row_blocks * ceil_div(m, 64) < 192 && row_blocks * ceil_div(m, 32) >= 192 ? 32 : 64;
 }
 
 hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a) {

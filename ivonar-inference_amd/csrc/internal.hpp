@@ -116,7 +116,7 @@ struct GemmArgs {
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a);
 // Long-prompt token GEMM (64- or 128-token wave tiles, LDS DMA staging); same
 // fp32 order as the tiled GEMM.
-int gemm_wide_tokens(int m, int rows, int n);  // token tile (128 or 64), 0 = does not apply
+int gemm_wide_tokens(int m, int rows, int n);  // token tile (128, 64 or 32), 0 = does not apply
 hipError_t launch_gemm_wide(hipStream_t stream, const GemmArgs& a);
 // Long-prompt token GEMM split four ways along K (few output rows); its fp32
 // order is four contiguous group ranges added in order.

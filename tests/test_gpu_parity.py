@@ -656,9 +656,9 @@ def test_gemm_skinny_four_row_tiles_epilogues(cuda, oracle, epilogue):
 
 
 # Long prompts with many row blocks run the long-prompt kernel (m >= 128; 128-token x 256-row tiles
-# from 2048 inputs on with >= 192 blocks, 64-token tiles below with >= 96 blocks): ragged token and
-# row counts, an odd chunk count, a single-chunk K, bias, and every epilogue with a padded output
-# stride.
+# from 2048 inputs on with >= 192 blocks, 64-token tiles below with >= 96 blocks, 32-token tiles where
+# 64-token tiles give fewer than 192: 700 tokens over 4096 rows): ragged token and row counts, an odd
+# chunk count, a single-chunk K, bias, and every epilogue with a padded output stride.
 @pytest.mark.parametrize("m,k,rows,bias", [(1000, 1088, 8200, True), (2048, 64, 4096, False),
                                           (128, 4096, 65536, False), (1537, 1100, 5120, True),
                                           (700, 1024, 4096, True), (130, 1024, 24576, False)])
@@ -673,6 +673,31 @@ def test_gemm_wide_tiles_edges(cuda, oracle, m, k, rows, bias):
     y = to_np(ops.gemm(matrix, q8, xsum, sx))
     assert runtime.gemm_plan(m, rows, k) == 1
     assert_bits_equal(y, _every_row(oracle, codes, x, k, scale_bits, b, 1), "every token")
+
+
+@pytest.mark.parametrize("epilogue", ["store", "residual", "silu_pair"])
+def test_gemm_wide_32_token_tiles_epilogues(cuda, oracle, epilogue):
+    """32-token long-prompt tiles (K=1024 -> N=8192 at 200 tokens: 128 blocks of 64 tokens, 224 of 32)
+    with a ragged last tile, a bias and a padded output stride."""
+    import torch
+    from ivonar_amd import ops, runtime
+
+    rng = np.random.default_rng(98 + len(epilogue))
+    m, k, rows = 200, 1024, 8192
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
+    q8, xsum, sx = ops.quantize_rows(_t(x, cuda))
+    width = rows // 2 if epilogue == "silu_pair" else rows
+    stride = width + 3
+    base = rng.standard_normal((m, stride)).astype(np.float32)
+    out = _t(base, cuda)
+    ops.gemm(matrix, q8, xsum, sx, out=out, epilogue=epilogue, out_stride=stride)
+    assert runtime.gemm_plan(m, rows, k) == 1
+    epi = {"store": T.EPI_STORE, "residual": T.EPI_RESIDUAL, "silu_pair": T.EPI_SILU_PAIR}[epilogue]
+    expected = _every_row(oracle, codes, x, k, scale_bits, b, 1, epi, base.copy(), stride)
+    assert_bits_equal(to_np(out), expected, epilogue)
+    assert torch.equal(out[:, width:], _t(base[:, width:], cuda)), "the GEMM wrote past its output width"
 
 
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
