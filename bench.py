@@ -11,10 +11,12 @@ launch stream around each replay: ``ms_per_step`` is the median replay / K.
 ``value`` is algorithmic bytes / second over the timed steps:
 bytes(M,N,K) = N*ceil(K/4) + 2*N*ceil(K/128) + 4*M*K + 4*M*N.
 
-Also reported on the same line: the GEMV kernel alone (pre-quantized
-activations) as the roofline figure, from the dispatch durations of a
-rocprofv3 kernel-trace pass the bench runs itself, with the HIP-event time
-per call inside a graph of 8 back-to-back calls beside it; the
+Also reported on the same line: the roofline figure of the kernel the
+headline times (the launch gemv_plain_store makes, quantizing the row in
+every block), from the dispatch durations of a rocprofv3 kernel-trace pass
+the bench runs itself, with the HIP-event time per call inside a graph of 8
+back-to-back calls beside it, and the same figures for the GEMV alone on
+pre-quantized activations (`roofline.prequant`); the
 single-linear case (K=1024 -> N=4096), the 32-token prefill tile GEMM TOPS,
 and the CPU baseline (the reference's numba GEMV restated in C++/OpenMP)
 on a bounded sample of the same workload.
@@ -63,10 +65,11 @@ def parse() -> argparse.Namespace:
 
 
 def probe_gemv_stress(calls: int) -> None:
-    """GEMV kernel alone (pre-quantized input) on both stress shapes, cycling 8 copies, then the
-    streaming-read kernel once over each copy's packed bytes (58.7 MB launches); then PROBE_BIG_READS
-    streaming reads of one 1 GiB buffer; then a 512 MiB device copy of known size that calibrates the
-    FETCH_SIZE / WRITE_SIZE counters."""
+    """On both stress shapes, cycling 8 copies: `calls` launches of gemv_plain_store (the launch quantizes
+    the fp32 row itself: the kernel the headline times), then `calls` launches of the GEMV on
+    pre-quantized input, then the streaming-read kernel once over each copy's packed bytes (58.7 MB
+    launches); then PROBE_BIG_READS streaming reads of one 1 GiB buffer; then a 512 MiB device copy of
+    known size that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
     import torch
 
     from ivonar_amd import ops, runtime, synthetic
@@ -83,8 +86,12 @@ def probe_gemv_stress(calls: int) -> None:
 
     for layer, x in synthetic.stress_layers(seed=3):
         mats = device_copies(layer, device, ROTATING_COPIES)
-        q8, xsum, sx = ops.quantize_rows(torch.from_numpy(x).to(device))
+        xd = torch.from_numpy(x).to(device)
+        q8, xsum, sx = ops.quantize_rows(xd)
         out = torch.empty(layer.rows, dtype=torch.float32, device=device)
+        torch.cuda.synchronize()
+        for call in range(calls):
+            ops.gemv(mats[call % ROTATING_COPIES], xd[0], out=out)
         torch.cuda.synchronize()
         for call in range(calls):
             ops.gemv_prequant(mats[call % ROTATING_COPIES], q8, xsum, sx, out=out)
@@ -345,7 +352,7 @@ def measure_traffic(calls: int = 8) -> dict:
             if counter not in row:
                 continue
             if "gemv_kernel" in row["kernel"] or "gemv_rows_kernel" in row["kernel"]:
-                gemv.setdefault(row["grid"], []).append(row[counter])
+                gemv.setdefault((_short_name(row["kernel"]), row["grid"]), []).append(row[counter])
             elif "stream_read" in row["kernel"]:
                 reads.append(row[counter])
             else:
@@ -355,8 +362,11 @@ def measure_traffic(calls: int = 8) -> dict:
         readings[counter] = {"factor": (512 * 1024) / max(other),
                              "per_grid": {grid: sum(v) / len(v) for grid, v in gemv.items()}, "reads": reads}
     fetch, write = readings["FETCH_SIZE"], readings["WRITE_SIZE"]
-    per_launch = [fetch["per_grid"][grid] * fetch["factor"] * 1024 + write["per_grid"].get(grid, 0.0) * write["factor"] * 1024
-                  for grid in fetch["per_grid"]]
+    launch_bytes = {key: fetch["per_grid"][key] * fetch["factor"] * 1024 + write["per_grid"].get(key, 0.0) * write["factor"] * 1024
+                    for key in fetch["per_grid"]}
+    # the quantizing kernels (QUANT true: the kernel the headline times) and the pre-quantized ones
+    per_launch = [v for (name, _), v in launch_bytes.items() if name.endswith("true>")]
+    prequant_launch = [v for (name, _), v in launch_bytes.items() if not name.endswith("true>")]
     # streaming-read launches: the last PROBE_BIG_READS read the 1 GiB buffer, the others one packed copy each
     reads = [v * fetch["factor"] * 1024 for v in fetch["reads"]]
     read_fetch = None
@@ -365,9 +375,22 @@ def measure_traffic(calls: int = 8) -> dict:
         read_fetch = {"copy_launch_bytes": round(sum(small) / len(small)), "one_GiB_launch_bytes": round(sum(big) / len(big)),
                       "note": "FETCH_SIZE x factor per streaming-read dispatch: 58.7 MB packed-copy launches and "
                               "1 GiB launches (1,073,741,824 bytes read)"}
+    if not per_launch or not prequant_launch:
+        return {"error": "the counter passes did not find both the quantizing and the pre-quantized GEMV"}
     return {"bytes_per_launch": sum(per_launch) / len(per_launch),
             "fetch_factor": round(fetch["factor"], 4), "write_factor": round(write["factor"], 4),
-            "per_launch": [round(v) for v in per_launch], "stream_read_fetch": read_fetch}
+            "per_launch": {f"{name} [{grid}]": round(v) for (name, grid), v in launch_bytes.items()},
+            "prequant_bytes_per_launch": sum(prequant_launch) / len(prequant_launch),
+            "stream_read_fetch": read_fetch}
+
+
+def _short_name(kernel: str) -> str:
+    """`gemv_rows_kernel<0, 7, true, true>` from a demangled kernel name (template kernels carry a `void `
+    return type in the trace, the others do not)."""
+    name = kernel.strip()
+    if name.startswith("void "):
+        name = name[len("void "):]
+    return name.replace("ivo::(anonymous namespace)::", "").split("(")[0].strip()
 
 
 def measure_trace(calls: int = 32) -> dict:
@@ -404,8 +427,8 @@ def measure_trace(calls: int = 32) -> dict:
             return {"error": f"unexpected kernel_stats.csv columns {reader.fieldnames}"}
         for row in reader:
             if "gemv" in row["Name"]:
-                name = row["Name"].replace("void ivo::(anonymous namespace)::", "").split("(")[0]
-                kernels[name] = {"calls": int(row["Calls"]), "average_us": round(float(row["AverageNs"]) / 1e3, 3)}
+                kernels[_short_name(row["Name"])] = {"calls": int(row["Calls"]),
+                                                     "average_us": round(float(row["AverageNs"]) / 1e3, 3)}
     # streaming reads, per dispatch in launch order: one per packed copy of each shape, then the 1 GiB reads
     reads = []
     for path in sorted(Path(out).rglob("*kernel_trace.csv")):
@@ -601,37 +624,59 @@ def main() -> None:
     step_seconds = seconds / steps
     value = bytes_per_step / step_seconds / 1e9
 
-    # ---- dominant kernel alone: GEMV on pre-quantized activations ----------------------------
-    # Per call inside a HIP graph of 8 back-to-back calls (one per rotating copy), events on the launch
-    # stream around each replay; the inter-launch gap a decode sequence also pays is included.  The
-    # kernel-trace pass below gives the dispatch durations alone.
-    kernel = {}
+    # ---- the kernels per shape: the headline's (quantize + GEMV in one launch) and the GEMV alone on
+    # pre-quantized activations.  Per call inside a HIP graph of 8 back-to-back calls (one per rotating
+    # copy), events on the launch stream around each replay; the inter-launch gap a decode sequence also
+    # pays is included.  The kernel-trace pass below gives the dispatch durations alone.
+    kernel, prequant_kernel = {}, {}
+    replays = max(20, args.steps // ROTATING_COPIES)
     for shape, (layer, x) in enumerate(stress):
         q8, xsum, sx = ops.quantize_rows(inputs[shape].reshape(1, -1))
         b = gemv_bytes(1, layer.rows, layer.in_features)
+
+        def plain(shape=shape):
+            for copy in range(ROTATING_COPIES):
+                ops.gemv(matrices[shape][copy], inputs[shape], out=outputs[shape])
 
         def prequant(shape=shape, q8=q8, xsum=xsum, sx=sx):
             for copy in range(ROTATING_COPIES):
                 ops.gemv_prequant(matrices[shape][copy], q8, xsum, sx, out=outputs[shape])
 
-        g = graph_of(prequant, stream)
-        t = time_graph(g, max(20, args.steps // ROTATING_COPIES), 2, median=True) / ROTATING_COPIES
-        kernel[f"{layer.in_features}x{layer.rows}"] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
+        name = f"{layer.in_features}x{layer.rows}"
+        t = time_graph(graph_of(plain, stream), replays, 2, median=True) / ROTATING_COPIES
+        kernel[name] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
+        t = time_graph(graph_of(prequant, stream), replays, 2, median=True) / ROTATING_COPIES
+        prequant_kernel[name] = {"us": t * 1e6, "GBps": b / t / 1e9, "bytes": b}
     # the same shapes with 1..16 tokens through the gemm_tile_store path (token GEMV / skinny kernel)
     results["stress_tokens"] = stress_tokens(matrices, stress, stream, max(20, args.steps // ROTATING_COPIES))
     kernel_bytes = sum(v["bytes"] for v in kernel.values())
-    kernel_seconds = sum(v["us"] for v in kernel.values()) / 1e6
-    achieved_graph = kernel_bytes / kernel_seconds / 1e9
-    achieved, timing = achieved_graph, ("algorithmic bytes / time per call: median of >= 20 replays of a HIP graph "
-                                        "of 8 back-to-back calls (one per rotating copy), events on the launch "
-                                        "stream, inter-launch gaps included (the kernel-trace pass failed)")
-    if trace and trace.get("kernels"):
-        calls = sum(v["calls"] for v in trace["kernels"].values())
-        mean_us = sum(v["calls"] * v["average_us"] for v in trace["kernels"].values()) / calls
-        achieved = (kernel_bytes / len(kernel)) / (mean_us * 1e-6) / 1e9
-        timing = ("algorithmic bytes per launch / mean dispatch duration of the GEMV kernels in the rocprofv3 "
-                  "kernel-trace pass (kernel_trace); achieved_graph is the HIP-event time per call inside a graph "
-                  "of 8 back-to-back calls, median of >= 20 replays, inter-launch gaps included")
+
+    def graph_rate(per_shape: dict) -> float:
+        return kernel_bytes / (sum(v["us"] for v in per_shape.values()) / 1e6) / 1e9
+
+    def trace_rate(quant: bool):
+        """Algorithmic bytes per launch over the mean dispatch duration of the quantizing (or the
+        pre-quantized) GEMV kernels in the kernel-trace pass, or None."""
+        if not trace or not trace.get("kernels"):
+            return None
+        chosen = {k: v for k, v in trace["kernels"].items() if k.endswith("true>") == quant}
+        if not chosen:
+            return None
+        calls = sum(v["calls"] for v in chosen.values())
+        mean_us = sum(v["calls"] * v["average_us"] for v in chosen.values()) / calls
+        return (kernel_bytes / len(kernel)) / (mean_us * 1e-6) / 1e9
+
+    achieved_graph, prequant_graph = graph_rate(kernel), graph_rate(prequant_kernel)
+    achieved, prequant_achieved = trace_rate(True), trace_rate(False)
+    timing = ("algorithmic bytes per launch / mean dispatch duration of the quantizing GEMV kernels "
+              "(gemv_rows_kernel<..., true>, what gemv_plain_store launches) in the rocprofv3 kernel-trace pass "
+              "(kernel_trace); achieved_graph is the HIP-event time per call inside a graph of 8 back-to-back "
+              "calls, median of >= 20 replays, inter-launch gaps included")
+    if achieved is None:
+        achieved, prequant_achieved = achieved_graph, prequant_graph
+        timing = ("algorithmic bytes / time per call: median of >= 20 replays of a HIP graph of 8 back-to-back calls "
+                  "(one per rotating copy), events on the launch stream, inter-launch gaps included (the "
+                  "kernel-trace pass failed)")
     ceiling = read_ceiling(matrices, stream)
     results["checkpoint_validate"] = validate_throughput(matrices, stream)
     copy = copy_bandwidth(device, stream)
@@ -713,7 +758,19 @@ def main() -> None:
             "traffic": None if not traffic or "error" in traffic else round(traffic["bytes_per_launch"]),
             "traffic_detail": traffic,
             "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
-            "kernel": "gemv_rows_kernel, two steps per row at K=8192 and seven at K=28672 (pre-quantized activations)",
+            "kernel": ("gemv_rows_kernel<0, STEPS, true, true>: the launch gemv_plain_store makes, quantizing the "
+                       "fp32 row in every block; two steps per row at K=8192 and seven at K=28672"),
+            "prequant": {
+                "kernel": "gemv_rows_kernel<0, STEPS, true, false>: the same GEMV on pre-quantized activations",
+                "achieved": round(prequant_achieved, 2),
+                "frac": round(prequant_achieved / HBM_PEAK_GBS, 4),
+                "achieved_graph": round(prequant_graph, 2),
+                "frac_graph": round(prequant_graph / HBM_PEAK_GBS, 4),
+                "traffic": (None if not traffic or "error" in traffic
+                            else round(traffic["prequant_bytes_per_launch"])),
+                "per_shape": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)}
+                              for k, v in prequant_kernel.items()},
+            },
             "read_ceiling": ceiling,
             "graph_frac_of_read_ceiling": round(achieved_graph / ceiling["GBps"], 4),
             "frac_of_read_ceiling_trace": (round(achieved / trace["stream_read"]["copy_launch_GBps"], 4)
