@@ -48,6 +48,7 @@ from .sampling import DeviceSampler
 from .synthetic import LinearStackWeights
 
 TILE = 32
+SELF_CHECK_TOLERANCE = 0.25  # kernel_decoder.py:38
 THREADS = 256
 HEAD_LANES = 4
 CHUNK = 64
@@ -368,6 +369,44 @@ class StackDecoder:
             if sampling:
                 self.drawn_uniforms.append(float(self.uniforms[slot]))
         return tokens
+
+    def reset(self) -> None:
+        """Back to an empty sequence (decoder.py:463-466): position 0, an empty token ring, no token seen."""
+        self.position = 0
+        self.history.zero_()
+        if self.sampler is not None:
+            self.sampler.seen.zero_()
+
+    @torch.no_grad()
+    def self_check(self) -> None:
+        """Runs one prompt through the prefill tiles and through single decode steps and requires both to
+        agree (kernel_decoder.py:524-549), so a GPU the kernels do not run correctly on fails while loading.
+
+        The prompt has TILE + TILE // 2 + 1 random ids in [2, vocab): prefill() takes it whole (the tile
+        GEMMs), then the first id alone, after which every further id is written into the ring slot the
+        next step reads and one step consumes it (the GEMVs).  Both end with the logits of the prompt's last
+        id; they must be finite, not all zero, and within a relative norm of SELF_CHECK_TOLERANCE, and the
+        token the last step selected must lie in the vocabulary.  The decoder is reset afterwards.  Raises
+        KernelError."""
+        vocab = int(self.config.vocab)
+        length = TILE + TILE // 2 + 1
+        ids = torch.randint(2, max(vocab, 3), (length,), generator=torch.Generator().manual_seed(0)) % vocab
+        whole = self.prefill(ids).clone()
+        self.prefill(ids[:1])
+        for index in range(1, length):
+            self.history[(self.position - 1) % self.burst].fill_(int(ids[index]))
+            self.step()
+        stepped = self.logits.clone()
+        selected = int(self.history[(self.position - 1) % self.burst])
+        self.reset()
+        scale = float(whole.norm())
+        if not (bool(torch.isfinite(whole).all()) and bool(torch.isfinite(stepped).all())) or scale == 0.0:
+            raise KernelError("the ternary kernels produced invalid numbers on this GPU")
+        difference = float((whole - stepped).norm()) / scale
+        if difference > SELF_CHECK_TOLERANCE:
+            raise KernelError(f"the ternary kernels disagree with themselves on this GPU ({difference:.1e})")
+        if not 0 <= selected < vocab:
+            raise KernelError("the ternary sampler returned an invalid token on this GPU")
 
     @torch.no_grad()
     def generate(self, prompt_ids, count: int) -> list[int]:

@@ -136,3 +136,45 @@ def test_prefill_tile_graph_matches_the_oracle(pair):
         np.testing.assert_array_equal(logits, oracle.prefill_logits(prompt), err_msg=f"prompt of {length}")
         first = int(decoder.history[decoder.burst - 1])
         assert [first] + decoder.advance_many(3) == oracle.generate(prompt, 4)
+
+
+def test_self_check_passes_and_resets(pair):
+    """The load-time self-check (kernel_decoder.py:524-549): the prompt through the tile GEMMs and through
+    single GEMV steps agree; afterwards the decoder is at position 0 with an empty ring and still gives the
+    oracle's logits."""
+    decoder, oracle = pair
+    decoder.self_check()
+    assert decoder.position == 0
+    assert int(decoder.history.abs().sum()) == 0
+    prompt = prompt_ids(decoder.config.vocab, 33, seed=21)
+    np.testing.assert_array_equal(decoder.prefill(prompt).cpu().numpy(), oracle.prefill_logits(prompt))
+
+
+def test_self_check_refuses_invalid_or_disagreeing_results(pair, monkeypatch):
+    """Failures forced from the host: a prefill whose logits are not finite, then single steps whose logits
+    are scaled away from the prefill's, each raise KernelError with the reference's message."""
+    import torch
+    from ivonar_amd.runtime import KernelError
+
+    decoder, _ = pair
+    real_prefill, real_step = decoder.prefill, decoder.step
+
+    def nan_prefill(ids):
+        out = real_prefill(ids)
+        out.fill_(float("nan"))
+        return out
+
+    monkeypatch.setattr(decoder, "prefill", nan_prefill)
+    with pytest.raises(KernelError, match="invalid numbers"):
+        decoder.self_check()
+    monkeypatch.setattr(decoder, "prefill", real_prefill)
+
+    def scaled_step():
+        real_step()
+        decoder.logits.mul_(torch.tensor(3.0, device=decoder.logits.device))
+
+    monkeypatch.setattr(decoder, "step", scaled_step)
+    with pytest.raises(KernelError, match="disagree"):
+        decoder.self_check()
+    monkeypatch.setattr(decoder, "step", real_step)
+    decoder.self_check()
