@@ -24,7 +24,13 @@
 // group q sums into LDS once, after its waves have issued their first weight
 // loads; all waves then read their operands from LDS.  Weights stream through
 // a register ring UW spans deep (kRing); all scales of the wave's range are
-// loaded up front.
+// loaded up front.  What the block's epilogue reads from global memory (token
+// scales, biases, residual bases) is loaded before the block barrier, so the
+// last step is not followed by a load round trip (K=8192 -> N=28672, 8
+// rotating copies: M=2 18.0 -> 17.4 us, M=4 19.4-19.9 -> 17.7, M=16 20.9-21.4
+// -> 20.0).  (Staging the block's scales in LDS instead, one 16-byte piece
+// per thread, saved another 0.3-0.5 us at M=2..4 but pushed M=16 over the
+// LDS budget into two K slices, 1.6 us slower; not kept.)
 //
 // Long rows.  Where the tokens' whole q8 rows do not fit in LDS, K is cut
 // into `slices` equal span ranges, one per block row of the grid (grid y):
@@ -170,6 +176,36 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
     const int p = j * nthr + tid;
     *(p < seeds ? lseed + p : reinterpret_cast<int*>(dump)) = seed_value[j];
   }
+  // What the epilogue reads from global memory (token scales, biases, the
+  // residual base), loaded now (after the fill registers are free) so that
+  // the block's last step is not followed by a load round trip: output
+  // o = tid + j * nthr of the block (at most kEpiOutputs per thread).
+  const int tiles = sh.tiles_per_block;
+  constexpr int kEpiOutputs = 4;
+  float epi_sx[kEpiOutputs], epi_b0[kEpiOutputs], epi_b1[kEpiOutputs], epi_base[kEpiOutputs];
+  if constexpr (EPI != kSlicePartials) {
+#pragma unroll
+    for (int j = 0; j < kEpiOutputs; ++j) {
+      const int o = tid + j * nthr;
+      if constexpr (EPI == kSiluPair) {
+        const int pair = o & 7, t = (o >> 3) & 15, tl = o >> 7;
+        const int r0 = (blockIdx.x * tiles + tl) * 16 + 2 * pair;
+        epi_sx[j] = scale_in[min(t, m - 1)];
+        epi_b0[j] = bias != nullptr ? bias[min(r0, sh.rows - 1)] : 0.0f;
+        epi_b1[j] = bias != nullptr ? bias[min(r0 + 1, sh.rows - 1)] : 0.0f;
+        epi_base[j] = 0.0f;
+      } else {
+        const int r = o & 15, t = (o >> 4) & 15, tl = o >> 8;
+        const int out_row = (blockIdx.x * tiles + tl) * 16 + r;
+        epi_sx[j] = scale_in[min(t, m - 1)];
+        epi_b0[j] = bias != nullptr ? bias[min(out_row, sh.rows - 1)] : 0.0f;
+        epi_b1[j] = 0.0f;
+        const bool owned = o < tiles * 256 && t < m && out_row < sh.rows;
+        epi_base[j] = EPI == kResidual && owned ? output[(size_t)t * sh.out_stride + out_row] : 0.0f;
+      }
+    }
+  }
+
   // Only the LDS stores are waited for: the weight loads stay in flight.
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -228,10 +264,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   for (int v = 0; v < 4; ++v) partial[(wave * 16 + 4 * kb + v) * 16 + c] = acc[v];
   __syncthreads();
 
-  const int tiles = sh.tiles_per_block;
   if constexpr (EPI == kSiluPair) {
     // Output j of a token pairs gate row 2j and up row 2j + 1 of the tile.
-    for (int o = tid; o < tiles * 16 * 8; o += nthr) {
+#pragma unroll
+    for (int j = 0; j < kEpiOutputs; ++j) {
+      const int o = tid + j * nthr;
+      if (o >= tiles * 16 * 8) break;
       const int pair = o & 7, t = (o >> 3) & 15, tl = o >> 7;
       const int r0 = (blockIdx.x * tiles + tl) * 16 + 2 * pair;
       float y[2];
@@ -240,23 +278,26 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
         const float* src = partial + ((tl * sh.parts) * 16 + t) * 16 + 2 * pair + e;
         float total = src[0];
         for (int p = 1; p < sh.parts; ++p) total = total + src[p * 256];
-        y[e] = total * scale_in[min(t, m - 1)];
-        if (bias != nullptr) y[e] = y[e] + bias[min(r0 + e, sh.rows - 1)];
+        y[e] = total * epi_sx[j];
+        if (bias != nullptr) y[e] = y[e] + (e ? epi_b1[j] : epi_b0[j]);
       }
       if (t < m && r0 + 1 < sh.rows) output[(size_t)t * sh.out_stride + (r0 >> 1)] = ivo_silu(y[0]) * y[1];
     }
   } else {
-    for (int o = tid; o < tiles * 256; o += nthr) {
+#pragma unroll
+    for (int j = 0; j < kEpiOutputs; ++j) {
+      const int o = tid + j * nthr;
+      if (o >= tiles * 256) break;
       const int r = o & 15, t = (o >> 4) & 15, tl = o >> 8;
       const int out_row = (blockIdx.x * tiles + tl) * 16 + r;
       const float* src = partial + ((tl * sh.parts) * 16 + t) * 16 + r;
       float total = src[0];
       for (int p = 1; p < sh.parts; ++p) total = total + src[p * 256];
-      float y = total * scale_in[min(t, m - 1)];
-      if (bias != nullptr) y = y + bias[min(out_row, sh.rows - 1)];
+      float y = total * epi_sx[j];
+      if (bias != nullptr) y = y + epi_b0[j];
       if (t < m && out_row < sh.rows) {
         float* dst = output + (size_t)t * sh.out_stride + out_row;
-        if constexpr (EPI == kResidual) *dst = *dst + y;
+        if constexpr (EPI == kResidual) *dst = epi_base[j] + y;
         else *dst = y;
       }
     }
