@@ -370,7 +370,9 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 
 }  // namespace
 
-// Kernel choice: the decode GEMV for one token; the token GEMV for up to 16
+// Kernel choice: the decode GEMV for one token, and for two tokens with
+// 4097..32768 inputs (the long-row GEMV over both tokens' copies: each
+// token's outputs are those of its own GEMV); the token GEMV for up to 16
 // tokens (K a multiple of 256; K sliced across blocks where the tokens' q8
 // rows do not fit in LDS whole);
 // the skinny kernels up to 32 tokens; then the long-prompt
@@ -378,6 +380,7 @@ hipError_t launch_epi(hipStream_t stream, const GemmArgs& a) {
 // kSlicedTokens; otherwise the tiled kernel.
 int gemm_splits(int m, int rows, int n) {
   if (m == 1 && gemv_prequant_applies(n)) return 0;
+  if (gemv_tokens_apply(m, n)) return 0;
   const size_t lds = (size_t)max_lds_per_block();
   const TokenPlan tokens = token_gemv_plan(m, rows, n, device_cus(), lds);
   if (tokens.parts > 0) return tokens.parts * tokens.slices;
@@ -389,9 +392,12 @@ int gemm_splits(int m, int rows, int n) {
 
 hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
   if (a.rows <= 0 || a.m <= 0) return hipSuccess;
-  if (a.m == 1 && gemv_prequant_applies(a.n)) {
+  const bool tokens_gemv = gemv_tokens_apply(a.m, a.n);
+  if ((a.m == 1 && gemv_prequant_applies(a.n)) || tokens_gemv) {
     // One token: the decode GEMV on the pre-quantized row (the q8 row layout
     // is the same); the output stride does not matter for a single row.
+    // Two tokens of long rows: the long-row GEMV over each token's copy,
+    // outputs out_stride floats apart.
     GemvArgs g{};
     g.mode = kPlain;
     g.epi = a.epi;
@@ -408,6 +414,7 @@ hipError_t launch_gemm(hipStream_t stream, const GemmArgs& a) {
     g.groups = a.groups;
     g.splits = 1;
     g.head_dim = defines().head_dim;
+    if (tokens_gemv) return launch_gemv_tokens(stream, g, a.m, a.out_stride);
     return launch_gemv(stream, g);
   }
   const size_t lds = (size_t)max_lds_per_block();

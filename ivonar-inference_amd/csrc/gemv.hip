@@ -63,6 +63,7 @@ struct GemvShape {
   int lanes, lane_shift, iters;
   int exact;  // every lane's chunks exist (C is a multiple of lanes): no per-chunk masks
   int split;  // the activations are nibble-split quads (the two-pass path's own scratch)
+  int out_stride;  // floats between the output rows of consecutive tokens (several tokens only)
 };
 
 struct GemvPtrs {
@@ -532,18 +533,34 @@ struct RowStep {
 // build disassembles these kernels and checks every VGPR access against the
 // loads in flight (asmcheck.py).  Lane layout and fp32 order are those of
 // gemv_kernel (orc_gemv_pairs).
-template <int EPI, int STEPS, bool EXACT, bool QUANT>
+//
+// MT = 2 (two pre-quantized tokens, the gemm_tile_* entry points' m = 2 on
+// long rows): the block copies both tokens' rows into LDS and every step's
+// weights feed one fmaf chain per token, each in the one-token kernel's order,
+// so a token's outputs are those of its own GEMV.  Each step ends with the
+// tokens' sums tied in registers before its refill loads go out; left free,
+// the compiler finished the second token's products after the refill and kept
+// copies of the step's weights (35 instead of 10 VGPRs per step, spills from
+// six steps on, and register copies of refilled steps ahead of their waits).
+template <int EPI, int STEPS, bool EXACT, bool QUANT, int MT = 1>
 __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8_t* __restrict__ packed,
                                                         const uint16_t* __restrict__ scales,
                                                         const float* __restrict__ bias, float* __restrict__ output,
                                                         int32_t* __restrict__ partials, GemvShape sh) {
   constexpr int kBlock = 512;  // one block of 8 waves per CU: up to 256 VGPRs for the steps in flight
   constexpr int kCopy = 4;     // int4 words of the q8 row per thread: rows up to 32768 inputs
-  constexpr int kSide = 2;     // loads of a row pair besides its steps: bias and residual base
+  // Loads of a row pair besides its steps: the bias and one residual base per token.
+  constexpr int kSide = 1 + MT;
+  static_assert(MT == 1 || (!QUANT && EPI != kPartials), "several tokens: pre-quantized rows and an output epilogue");
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int chunks = (sh.n + kChunk - 1) / kChunk;
-  int4* lds_q = reinterpret_cast<int4*>(lds_raw);  // quad w of chunk u at w*C + u
-  int* lds_x = reinterpret_cast<int*>(lds_raw + (size_t)chunks * kChunk);
+  // Token t's copy: quad w of chunk u at lds_q(t)[w*C + u], then minus its chunk sums.
+  const int token_bytes = rows_dump_offset(chunks);
+  auto lds_q_of = [&](int t) { return reinterpret_cast<int4*>(lds_raw + t * token_bytes); };
+  auto lds_x_of = [&](int t) { return reinterpret_cast<int*>(lds_raw + t * token_bytes + (size_t)chunks * kChunk); };
+  int4* lds_q = lds_q_of(0);
+  int* lds_x = lds_x_of(0);
+  unsigned char* lds_dump = lds_raw + MT * token_bytes;
   const int4* gq = reinterpret_cast<const int4*>(in.q8_in);
   const int tid = threadIdx.x;
   const int sub = tid & 63;  // 64 lanes per row: lane = sub, one row slot per wave
@@ -551,8 +568,13 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   const int words = chunks * 4;
   constexpr bool kScales = EPI != kPartials;  // the partials export passes no scales
   static_assert(!(QUANT && EPI == kPartials), "the partials export reads a pre-quantized row");
-  float sx = 1.0f;
-  if constexpr (!QUANT) sx = kScales ? *in.scale_in : 1.0f;
+  float sx[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) sx[t] = 1.0f;
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) sx[t] = kScales ? in.scale_in[t] : 1.0f;
+  }
 
   // Loads that a layout does not need still go out, from the first bytes of
   // the packed matrix (the one operand every entry point passes), so that the
@@ -590,17 +612,32 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
       const int u = min(step * 64 + sub, chunks - 1);
       const int r0 = min(row_pair * kRows, sh.rows - 1), r1 = min(row_pair * kRows + 1, sh.rows - 1);
       const int own = (sub & 1) ? r1 : r0;
-      st.w0 = load_b128(packed + (size_t)own * sh.row_bytes + (size_t)u * 16);
-      st.w1 = load_b128(packed + (size_t)((sub & 1) ? r0 : r1) * sh.row_bytes + (size_t)u * 16);
-      st.s = load_u16(kScales ? static_cast<const void*>(scales + (size_t)own * sh.groups + (u >> 1))
-                              : static_cast<const void*>(packed));
+      const uint8_t* p0 = packed + (size_t)own * sh.row_bytes + (size_t)u * 16;
+      const uint8_t* p1 = packed + (size_t)((sub & 1) ? r0 : r1) * sh.row_bytes + (size_t)u * 16;
+      const void* ps = kScales ? static_cast<const void*>(scales + (size_t)own * sh.groups + (u >> 1))
+                               : static_cast<const void*>(packed);
+      st.w0 = load_b128(p0);
+      st.w1 = load_b128(p1);
+      st.s = load_u16(ps);
     }
   };
-  // Bias and residual base of the lane's own row.
-  auto issue_side = [&](int row_pair, int& b, int& base) {
+  // Bias and residual bases (token t at output + t * out_stride) of the lane's own row.
+  auto issue_side = [&](int row_pair, int& b, int (&base)[MT]) {
     const int own = min(row_pair * kRows + (sub & 1), sh.rows - 1);
     b = load_b32(bias != nullptr ? static_cast<const void*>(bias + own) : static_cast<const void*>(packed));
-    base = load_b32(EPI == kResidual ? static_cast<const void*>(output + own) : static_cast<const void*>(packed));
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      base[t] = load_b32(EPI == kResidual ? static_cast<const void*>(output + (size_t)t * sh.out_stride + own)
+                                          : static_cast<const void*>(packed));
+  };
+  // The wait that covers the side loads, repeated per register group so that
+  // every register it covers is tied to a wait instruction (repeating a wait
+  // whose count is already reached costs one instruction).
+  auto side_wait = [&](int& b, int (&base)[MT], auto count_c) {
+    constexpr int count = decltype(count_c)::value;
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b), "+v"(base[0]) : "n"(count) : "memory");
+#pragma unroll
+    for (int t = 1; t < MT; ++t) asm volatile("s_waitcnt vmcnt(%1)" : "+v"(base[t]) : "n"(count) : "memory");
   };
 
   RowStep st[STEPS];
@@ -617,25 +654,38 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   it = __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / 64) + (tid >> 6));  // wave-uniform
   pb = pair_base(it);
   if constexpr (!QUANT) {
-    v4i32 qv[kCopy];
-    int xv;
+    // Token t's q8 row: chunks * 64 bytes at q8_in + t * chunks * 64, its
+    // chunk sums at xsum_in + t * chunks.
+    v4i32 qv[MT][kCopy];
+    int xv[MT];
 #pragma unroll
-    for (int k = 0; k < kCopy; ++k) qv[k] = load_b128(gq + min(k * kBlock + tid, words - 1));
-    xv = load_b32(in.xsum_in + min(tid, chunks - 1));
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int k = 0; k < kCopy; ++k) qv[t][k] = load_b128(gq + (size_t)t * words + min(k * kBlock + tid, words - 1));
+      xv[t] = load_b32(in.xsum_in + (size_t)t * chunks + min(tid, chunks - 1));
+    }
     issue_step(st[0], pb, it, std::integral_constant<int, 0>{});
     // The copy's loads are older than step 0's three.
-    asm volatile("s_waitcnt vmcnt(3)" : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]), "+v"(xv) : : "memory");
-    int4* dump = reinterpret_cast<int4*>(lds_raw + rows_dump_offset(chunks));
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      asm volatile("s_waitcnt vmcnt(3)" : "+v"(qv[t][0]), "+v"(qv[t][1]), "+v"(qv[t][2]), "+v"(qv[t][3]), "+v"(xv[t])
+                   : : "memory");
+    int4* dump = reinterpret_cast<int4*>(lds_dump);
     static_for<kCopy>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
       const int e = k * kBlock + tid;
-      // Caller q8 quads are split here, once per block (the scratch's arrive split).
-      const int4 quad = __builtin_bit_cast(int4, qv[k]);
-      const int4 stored = sh.split ? quad : split_quad(quad);
-      *(e < words ? lds_q + (e & 3) * chunks + (e >> 2) : dump) = stored;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        // Caller q8 quads are split here, once per block (the scratch's arrive split).
+        const int4 quad = __builtin_bit_cast(int4, qv[t][k]);
+        const int4 stored = sh.split ? quad : split_quad(quad);
+        *(e < words ? lds_q_of(t) + (e & 3) * chunks + (e >> 2) : dump) = stored;
+      }
       if constexpr (k + 1 < STEPS) issue_step(st[k + 1], pb, it, std::integral_constant<int, k + 1>{});
     });
-    *(tid < chunks ? lds_x + tid : reinterpret_cast<int*>(dump)) = -xv;  // minus the chunk sums
+#pragma unroll
+    for (int t = 0; t < MT; ++t)  // minus the chunk sums
+      *(tid < chunks ? lds_x_of(t) + tid : reinterpret_cast<int*>(dump)) = -xv[t];
     static_for<STEPS>([&](auto sc) {
       if constexpr (decltype(sc)::value > kCopy) issue_step(st[sc], pb, it, sc);
     });
@@ -662,8 +712,8 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     static_for<kMid + 1>([&](auto sc) {
       if constexpr (decltype(sc)::value > 0) issue_step(st[sc], pb, it, sc);
     });
-    float* slots = reinterpret_cast<float*>(lds_raw + rows_dump_offset(chunks) + 16);
-    sx = quantize_row_split<kBlock, kX>(xv, sh.n, chunks, reinterpret_cast<int*>(lds_q), lds_x, slots, [&](auto kc) {
+    float* slots = reinterpret_cast<float*>(lds_dump + 16);
+    sx[0] = quantize_row_split<kBlock, kX>(xv, sh.n, chunks, reinterpret_cast<int*>(lds_q), lds_x, slots, [&](auto kc) {
       constexpr int k = decltype(kc)::value;
       if constexpr (k % 2 == 0 && k / 2 + kMid + 1 < STEPS)
         issue_step(st[k / 2 + kMid + 1], pb, it, std::integral_constant<int, k / 2 + kMid + 1>{});
@@ -673,26 +723,48 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
 
   const int4 qr_unused[1][4] = {};
   const int xr_unused[1] = {0};
-  auto compute = [&](const RowStep& step, float& acc, int row0, auto step_c) {
+  // The same weights against each token's copy, one fmaf chain per token.
+  auto compute = [&](const RowStep& step, float (&acc)[MT], int row0, auto step_c) {
     Step<1> view;
     view.w[0][0] = __builtin_bit_cast(uint4, step.w0);
     view.w[0][1] = __builtin_bit_cast(uint4, step.w1);
     view.s[0] = (uint16_t)step.s;
-    compute_step<EPI, 1, false, 64, EXACT, true, true>(view, qr_unused, xr_unused, lds_q, lds_x, acc, partials, sh, row0,
-                                                 decltype(step_c)::value, sub, chunks);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      // The token's copy is addressed through an opaque offset: its quads are
+      // the same at every row pair, and left visible the compiler keeps them
+      // in registers across the loop (16 VGPRs per step and token).
+      int toff = t * token_bytes;
+      if constexpr (MT > 1) asm volatile("" : "+v"(toff));
+      const int4* q = reinterpret_cast<const int4*>(lds_raw + toff);
+      const int* x = reinterpret_cast<const int*>(lds_raw + toff + chunks * kChunk);
+      compute_step<EPI, 1, false, 64, EXACT, true, true>(view, qr_unused, xr_unused, q, x, acc[t], partials, sh, row0,
+                                                       decltype(step_c)::value, sub, chunks);
+    }
+    if constexpr (MT > 1) {
+      // Every token's sum of this step is complete before the step's
+      // registers are refilled (otherwise the compiler may finish the later
+      // tokens after the refill loads and keep copies of the step's weights).
+#pragma unroll
+      for (int t = 0; t < MT; ++t) asm volatile("" : "+v"(acc[t]));
+    }
   };
-  auto epilogue = [&](float acc, int row0, int b_side, int base_side) {
+  auto epilogue = [&](float (&acc)[MT], int row0, int b_side, const int (&base_side)[MT]) {
     if constexpr (EPI != kPartials) {
-      acc = pair_tree_sum(acc, 64);
-      const int row = row0 + (sub & 1);
-      float y = acc * 0.0625f * sx;  // the folded sums carry chunk_code_dot's factor 16
-      if (bias != nullptr) y = y + __int_as_float(b_side);
-      if constexpr (EPI == kSiluPair) {
-        const float up = __int_as_float(pair_swap(__float_as_int(y)));
-        if (sub == 0 && row + 1 < sh.rows) output[row >> 1] = ivo_silu(y) * up;
-      } else if (sub < 2 && row < sh.rows) {
-        if constexpr (EPI == kStore) output[row] = y;
-        else output[row] = __int_as_float(base_side) + y;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const float total = pair_tree_sum(acc[t], 64);
+        const int row = row0 + (sub & 1);
+        float y = total * 0.0625f * sx[t];  // the folded sums carry chunk_code_dot's factor 16
+        if (bias != nullptr) y = y + __int_as_float(b_side);
+        float* out = output + (size_t)t * sh.out_stride;
+        if constexpr (EPI == kSiluPair) {
+          const float up = __int_as_float(pair_swap(__float_as_int(y)));
+          if (sub == 0 && row + 1 < sh.rows) out[row >> 1] = ivo_silu(y) * up;
+        } else if (sub < 2 && row < sh.rows) {
+          if constexpr (EPI == kStore) out[row] = y;
+          else out[row] = __int_as_float(base_side[t]) + y;
+        }
       }
     }
   };
@@ -701,11 +773,13 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     while (it + waves < sh.iters) {
       const int row0 = it * kRows;
       const int it_next = it + waves;
-      // This row pair's bias and residual base, younger than its steps' weights.
-      int b_side, base_side;
+      // This row pair's bias and residual bases, younger than its steps' weights.
+      int b_side, base_side[MT];
       issue_side(it, b_side, base_side);
       pb = pair_base(it_next);
-      float acc = 0.0f;
+      float acc[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
       static_for<STEPS>([&](auto s) {
         asm volatile("s_waitcnt vmcnt(%3)"
                      : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
@@ -716,15 +790,17 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
         __builtin_amdgcn_sched_barrier(0);
       });
       // Younger than the side loads: the STEPS refills of the next row pair.
-      asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b_side), "+v"(base_side) : "n"(3 * STEPS) : "memory");
+      side_wait(b_side, base_side, std::integral_constant<int, 3 * STEPS>{});
       epilogue(acc, row0, b_side, base_side);
       it = it_next;
     }
     // The wave's last row pair: no refills, so fewer loads are younger than each step.
     const int row0 = it * kRows;
-    int b_side, base_side;
+    int b_side, base_side[MT];
     issue_side(it, b_side, base_side);
-    float acc = 0.0f;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
     static_for<STEPS>([&](auto s) {
       asm volatile("s_waitcnt vmcnt(%3)"
                    : "+v"(st[s].w0), "+v"(st[s].w1), "+v"(st[s].s)
@@ -733,7 +809,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
       compute(st[s], acc, row0, s);
       __builtin_amdgcn_sched_barrier(0);
     });
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(b_side), "+v"(base_side)::"memory");
+    side_wait(b_side, base_side, std::integral_constant<int, 0>{});
     epilogue(acc, row0, b_side, base_side);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // a wave with no row pair still has its first loads out
@@ -791,6 +867,35 @@ void launch_rows(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const
     }
   }
   launch_rows_as<EPI, STEPS, false>(stream, p, a, sh, blocks, lds);
+}
+
+// Several tokens through the long-row kernel (pre-quantized rows): the same
+// grid, MT copies of the activations in LDS.
+template <int EPI, int STEPS, int MT>
+void launch_rows_tokens(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh) {
+  const int cus = device_cus();
+  const int cap = (STEPS == 2 ? kRowsBlocksPerCu2 : 1) * cus;
+  const int blocks = ceil_div(sh.iters, 8) < cap ? ceil_div(sh.iters, 8) : cap;
+  const size_t lds = (size_t)MT * rows_dump_offset((sh.n + kChunk - 1) / kChunk) + 16;
+  if (sh.exact)
+    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, true, false, MT>), dim3(blocks), dim3(512), lds, stream, p,
+                       a.packed, a.scales, a.bias, a.output, a.partials, sh);
+  else
+    hipLaunchKernelGGL((gemv_rows_kernel<EPI, STEPS, false, false, MT>), dim3(blocks), dim3(512), lds, stream, p,
+                       a.packed, a.scales, a.bias, a.output, a.partials, sh);
+}
+
+template <int EPI, int MT>
+void launch_tokens_steps(hipStream_t stream, const GemvPtrs& p, const GemvArgs& a, const GemvShape& sh, int steps) {
+  switch (steps) {
+    case 2: launch_rows_tokens<EPI, 2, MT>(stream, p, a, sh); break;
+    case 3: launch_rows_tokens<EPI, 3, MT>(stream, p, a, sh); break;
+    case 4: launch_rows_tokens<EPI, 4, MT>(stream, p, a, sh); break;
+    case 5: launch_rows_tokens<EPI, 5, MT>(stream, p, a, sh); break;
+    case 6: launch_rows_tokens<EPI, 6, MT>(stream, p, a, sh); break;
+    case 7: launch_rows_tokens<EPI, 7, MT>(stream, p, a, sh); break;
+    default: launch_rows_tokens<EPI, 8, MT>(stream, p, a, sh); break;
+  }
 }
 
 // Steps per pipeline item of the rolling layout (rows of more than 8 steps):
@@ -893,6 +998,7 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
   // Dead lanes exist when the last step is partial (items never hold dead steps).
   sh.exact = chunks % lanes == 0;
   sh.split = 0;
+  sh.out_stride = 0;
   const int cus = device_cus();
   const bool roll = !fused && steps > 8;  // the rolling layout (2..8 steps: the long-row kernel sizes its own grid)
   int blocks = ceil_div(sh.iters, (roll ? block_threads<true>() : kThreads) / 64);
@@ -938,6 +1044,48 @@ hipError_t launch_gemv(hipStream_t stream, const GemvArgs& in) {
     case kResidual: return launch_nj<kPlain, kResidual, false>(stream, p, a, sh, blocks, lds, steps, quant);
     case kSiluPair: return launch_nj<kPlain, kSiluPair, false>(stream, p, a, sh, blocks, lds, steps, quant);
     case kPartials: return launch_nj<kPlain, kPartials, false>(stream, p, a, sh, blocks, lds, steps, quant);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool gemv_tokens_apply(int m, int n) {
+  if (m < 2 || m > kGemvTokensMax || n <= 64 * kChunk) return false;
+  const int chunks = ceil_div(n, kChunk);
+  return ceil_div(chunks, 64) <= 8 && (size_t)m * rows_dump_offset(chunks) + 16 <= (size_t)max_lds_per_block();
+}
+
+hipError_t launch_gemv_tokens(hipStream_t stream, const GemvArgs& a, int m, int out_stride) {
+  if (a.rows <= 0) return hipSuccess;
+  if (!gemv_tokens_apply(m, a.n) || a.q8_in == nullptr || a.xsum_in == nullptr || a.scale_in == nullptr)
+    return hipErrorInvalidValue;
+  const int chunks = ceil_div(a.n, kChunk);
+  int lanes, rows_per_lane;
+  gemv_plan(a.rows, a.n, &lanes, &rows_per_lane);
+  GemvShape sh{};
+  sh.rows = a.rows;
+  sh.n = a.n;
+  sh.row_bytes = a.row_bytes;
+  sh.groups = a.groups;
+  sh.splits = 1;
+  sh.head_dim = a.head_dim;
+  sh.lanes = lanes;
+  sh.lane_shift = __builtin_ctz((unsigned)lanes);
+  sh.iters = ceil_div(a.rows, (64 / lanes) * rows_per_lane);
+  sh.exact = chunks % lanes == 0;
+  sh.split = 0;
+  sh.out_stride = out_stride;
+  const int steps = ceil_div(chunks, lanes);
+  const GemvPtrs p{nullptr, nullptr, a.q8_in, a.xsum_in, a.scale_in};
+  auto go = [&](auto epi_c) -> hipError_t {
+    constexpr int EPI = decltype(epi_c)::value;
+    static_assert(kGemvTokensMax == 2, "one token count compiled");
+    launch_tokens_steps<EPI, 2>(stream, p, a, sh, steps);
+    return hipGetLastError();
+  };
+  switch (a.epi) {
+    case kStore: return go(std::integral_constant<int, kStore>{});
+    case kResidual: return go(std::integral_constant<int, kResidual>{});
+    case kSiluPair: return go(std::integral_constant<int, kSiluPair>{});
     default: return hipErrorInvalidValue;
   }
 }

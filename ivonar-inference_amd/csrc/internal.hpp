@@ -89,6 +89,12 @@ struct GemvArgs {
   int head_dim;
 };
 hipError_t launch_gemv(hipStream_t stream, const GemvArgs& a);
+// Two tokens of pre-quantized rows through the long-row GEMV (4097..32768
+// inputs): each token's outputs are bit-identical to the one-token GEMV's on
+// its row.  (Three tokens this way ran slower than the token GEMV.)
+constexpr int kGemvTokensMax = 2;
+bool gemv_tokens_apply(int m, int n);
+hipError_t launch_gemv_tokens(hipStream_t stream, const GemvArgs& a, int m, int out_stride);
 
 // Lane layout the decode GEMV uses for a K-wide row (also defines its fp32
 // summation order): lanes per row (power of two in [2, 64]) and rows per lane.

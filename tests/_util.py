@@ -122,7 +122,8 @@ def finish_all_rows(oracle, order: int, param: int, epi: int, codes: np.ndarray,
 
 def token_gemm_order(m: int, rows: int, k: int) -> tuple[int, int]:
     """(order, param) of gemm_tile_* for m tokens, as the oracle's finish takes them: the K-split the plan
-    reports (order 1), or for one token (plan 0) the decode GEMV's lanes (order 0), which then runs it."""
+    reports (order 1), or for plan 0 (one token, or two tokens of 4097..32768 inputs) the decode
+    GEMV's lanes (order 0): the GEMV then runs each token's row."""
     from ivonar_amd import runtime
 
     splits = runtime.gemm_plan(m, rows, k)
@@ -138,6 +139,6 @@ def token_gemm_expected(oracle, epi: int, q8, xsum, sx, packed, scale_bits, bias
     order, param = token_gemm_order(m, rows, k)
     if order == 1:
         return oracle.gemm_split(epi, q8, xsum, sx, packed, scale_bits, bias, out, k, out_stride, m, param)
-    assert m == 1 and out.shape[0] == 1
-    oracle.gemv_pairs(epi, q8[0], xsum[0], sx[0], packed, scale_bits, bias, out[0], k, param)
+    for t in range(m):
+        oracle.gemv_pairs(epi, q8[t], xsum[t], sx[t], packed, scale_bits, bias, out[t], k, param)
     return out

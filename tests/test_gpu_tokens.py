@@ -3,7 +3,8 @@ tokens' q8 rows within the LDS budget (the gemm_tile_* entry points route those 
 
 Every output of every token is checked bit for bit against the oracle's split order (S = the library's
 plan, contiguous group ranges folded in order and added in order), and token 0 within rel 1e-5 / abs 1e-6
-of the fp64 truth.  Cases: the planner's span choices (1, 2, 4, 8, 14 and 16 spans per wave), ragged row
+of the fp64 truth.  Two tokens of 4097..32768 inputs run the long-row decode GEMV over each token's copy
+(plan 0) and are checked in its lane order.  Cases: the planner's span choices (1, 2, 4, 8, 14 and 16 spans per wave), ragged row
 counts, a bias, both epilogues with a padded output stride, token counts that are not a multiple of four
 (the last lane group's slots past M), and rows too long for the tokens' q8 bytes in LDS, where K is cut
 into 2, 4 or 8 slices across blocks and a second kernel adds the wave chains in order."""
@@ -66,9 +67,9 @@ def _case(oracle, cuda, m, k, rows, bias, seed, epilogue="store", pad=0):
     (1, 1024, 4096, False, 0),     # one token: the decode GEMV (plan 0, its lane order)
     (2, 1024, 4096, False, 4),     # 4 spans, 1 per wave
     (5, 4096, 1000, True, 16),     # ragged rows, 16 waves per row tile
-    (3, 8192, 8200, True, 4),      # 8 spans per wave, ragged rows
+    (4, 8192, 8200, True, 4),      # 8 spans per wave, ragged rows
     (8, 2048, 16384, False, 2),    # 4 spans per wave
-    (2, 28672, 8192, False, 7),    # the long-row stress shape, 16 spans per wave
+    (4, 28672, 8192, False, 7),    # the long-row stress shape, 16 spans per wave
     (16, 8192, 2000, False, 16),   # 2 spans per wave, 128 KB of token bytes
     (4, 28672, 1000, True, 14),    # 8 spans per wave (no range reaches eight waves per CU)
     (4, 7168, 16384, False, 2),    # 14 spans per wave
@@ -78,6 +79,39 @@ def _case(oracle, cuda, m, k, rows, bias, seed, epilogue="store", pad=0):
 def test_token_gemv_store(cuda, oracle, m, k, rows, bias, splits):
     got = _case(oracle, cuda, m, k, rows, bias, seed=m * 1009 + k + rows)
     assert got == splits
+
+
+# (m, k, rows, bias): two tokens of 4097..32768 inputs run the long-row decode GEMV over each token's copy
+# (plan 0): every token's outputs in its own GEMV's lane order.  K a multiple of 4096 (no clamped chunks)
+# and not (4160, 6000, 20000: the last step's lanes partly dead), 2..8 steps per row, ragged row counts,
+# one row pair per wave and several.  Three tokens stay on the token GEMV.
+@pytest.mark.parametrize("m,k,rows,bias", [
+    (2, 8192, 28672, False),   # the stress shape, two blocks per CU
+    (2, 8192, 1000, True),
+    (2, 28672, 8192, False),   # the other stress shape, seven steps per row
+    (2, 28672, 130, True),
+    (2, 4160, 700, True),      # two steps, the second with one live lane pair
+    (2, 6000, 4097, False),
+    (2, 20000, 3001, True),    # five steps
+    (2, 32768, 514, False),    # eight steps, 68 KB of copies in LDS
+])
+def test_gemv_tokens_store(cuda, oracle, m, k, rows, bias):
+    assert _case(oracle, cuda, m, k, rows, bias, seed=m * 211 + k + rows) == 0
+
+
+def test_three_tokens_stay_on_the_token_gemv(cuda):
+    from ivonar_amd import runtime
+
+    assert runtime.gemm_plan(2, 1000, 8192) == 0
+    assert runtime.gemm_plan(3, 1000, 8192) > 0
+    assert runtime.gemm_plan(2, 1000, 4096) > 0, "4096 inputs and fewer: the token GEMV"
+
+
+@pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
+@pytest.mark.parametrize("m,k,rows", [(2, 8192, 1000), (2, 28672, 514), (2, 6000, 258)])
+def test_gemv_tokens_epilogues(cuda, oracle, epilogue, m, k, rows):
+    assert _case(oracle, cuda, m, k, rows, True, seed=m * 37 + k + rows + (5 if epilogue == "residual" else 0),
+                 epilogue=epilogue, pad=3) == 0
 
 
 @pytest.mark.parametrize("epilogue", ["residual", "silu_pair"])
@@ -191,7 +225,8 @@ class _PaddedScales:
 # (m, k, rows): the token GEMV in one slice and in K slices, the skinny kernel, the 32-token slices and the
 # long-prompt and split-K tilings, all with one or three unused scale groups per row.
 @pytest.mark.parametrize("m,k,rows", [(5, 4096, 1000), (12, 28672, 4100), (3, 1024, 300), (32, 4096, 1024),
-                                      (100, 2048, 700), (512, 4096, 1024), (300, 4096, 14336)])
+                                      (100, 2048, 700), (512, 4096, 1024), (300, 4096, 14336), (2, 8192, 1000),
+                                      (2, 20480, 300)])
 @pytest.mark.parametrize("extra", [1, 2])
 def test_token_gemm_padded_scale_rows(cuda, oracle, m, k, rows, extra):
     from ivonar_amd import ops, runtime
