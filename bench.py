@@ -365,8 +365,8 @@ def measure_traffic(calls: int = 8) -> dict:
     launch_bytes = {key: fetch["per_grid"][key] * fetch["factor"] * 1024 + write["per_grid"].get(key, 0.0) * write["factor"] * 1024
                     for key in fetch["per_grid"]}
     # the quantizing kernels (QUANT true: the kernel the headline times) and the pre-quantized ones
-    per_launch = [v for (name, _), v in launch_bytes.items() if name.endswith("true>")]
-    prequant_launch = [v for (name, _), v in launch_bytes.items() if not name.endswith("true>")]
+    per_launch = [v for (name, _), v in launch_bytes.items() if _quantizing(name)]
+    prequant_launch = [v for (name, _), v in launch_bytes.items() if not _quantizing(name)]
     # streaming-read launches: the last PROBE_BIG_READS read the 1 GiB buffer, the others one packed copy each
     reads = [v * fetch["factor"] * 1024 for v in fetch["reads"]]
     read_fetch = None
@@ -385,12 +385,20 @@ def measure_traffic(calls: int = 8) -> dict:
 
 
 def _short_name(kernel: str) -> str:
-    """`gemv_rows_kernel<0, 7, true, true>` from a demangled kernel name (template kernels carry a `void `
+    """`gemv_rows_kernel<0, 7, true, true, 1>` from a demangled kernel name (template kernels carry a `void `
     return type in the trace, the others do not)."""
     name = kernel.strip()
     if name.startswith("void "):
         name = name[len("void "):]
     return name.replace("ivo::(anonymous namespace)::", "").split("(")[0].strip()
+
+
+def _quantizing(name: str) -> bool:
+    """Whether a `gemv_rows_kernel<EPI, STEPS, EXACT, QUANT, TOKENS>` name is the quantizing launch (QUANT true)."""
+    if "<" not in name or ">" not in name:
+        return False
+    args = [a.strip() for a in name[name.index("<") + 1:name.rindex(">")].split(",")]
+    return len(args) >= 4 and args[3] == "true"
 
 
 def measure_trace(calls: int = 32) -> dict:
@@ -525,13 +533,15 @@ def m_sweep(device, stream) -> dict:
     return {"shape": f"{k}x{n}", "by_m": table, "gemm_faster_from_m": crossover,
             "note": "weights warm in the caches; 20 (M <= 128) or 4 calls per HIP graph, M >= 512 after 25 ms "
                     "of the same calls; gemm_us for M = 1 is the decode GEMV on the pre-quantized row, for "
-                    "M = 2..16 the token GEMV (K a multiple of 256)"}
+                    "M = 2 the two-token GEMV on rows of 4097..32768 inputs, else for M = 2..16 the token GEMV "
+                    "(K a multiple of 256)"}
 
 
 def stress_tokens(matrices, stress, stream, replays: int) -> dict:
     """Cold-cache GEMM with M = 1..16 tokens on the two stress shapes (8 rotating copies per shape, one
-    HIP graph of 8 calls, median of `replays` replays): M = 1 runs the decode GEMV (plan 0), M = 2..16 the
-    token GEMV (plan = its K-splits); beside it the M = 1 GEMV on pre-quantized input called directly."""
+    HIP graph of 8 calls, median of `replays` replays): M = 1 runs the decode GEMV and M = 2 the two-token
+    GEMV (plan 0), M = 4..16 the token GEMV (plan = its K-splits); beside it the M = 1 GEMV on pre-quantized
+    input called directly."""
     import numpy as np
     import torch
 
@@ -564,6 +574,7 @@ def stress_tokens(matrices, stress, stream, replays: int) -> dict:
         entry["gemv_m1_us"] = round(t1 * 1e6, 3)
         entry["m16_over_gemv_m1"] = round(entry["16"]["us"] / entry["gemv_m1_us"], 3)
         entry["m16_over_m1"] = round(entry["16"]["us"] / entry["1"]["us"], 3)
+        entry["m2_over_gemv_m1"] = round(entry["2"]["us"] / entry["gemv_m1_us"], 3)
         table[f"{k}x{n}"] = entry
     return {"by_shape": table, "timing": "median of HIP-graph replays of 8 calls (one per rotating copy), per call"}
 
@@ -659,7 +670,7 @@ def main() -> None:
         pre-quantized) GEMV kernels in the kernel-trace pass, or None."""
         if not trace or not trace.get("kernels"):
             return None
-        chosen = {k: v for k, v in trace["kernels"].items() if k.endswith("true>") == quant}
+        chosen = {k: v for k, v in trace["kernels"].items() if _quantizing(k) == quant}
         if not chosen:
             return None
         calls = sum(v["calls"] for v in chosen.values())
@@ -758,10 +769,10 @@ def main() -> None:
             "traffic": None if not traffic or "error" in traffic else round(traffic["bytes_per_launch"]),
             "traffic_detail": traffic,
             "algorithmic_bytes_per_launch": kernel_bytes // len(kernel),
-            "kernel": ("gemv_rows_kernel<0, STEPS, true, true>: the launch gemv_plain_store makes, quantizing the "
+            "kernel": ("gemv_rows_kernel<0, STEPS, true, true, 1>: the launch gemv_plain_store makes, quantizing the "
                        "fp32 row in every block; two steps per row at K=8192 and seven at K=28672"),
             "prequant": {
-                "kernel": "gemv_rows_kernel<0, STEPS, true, false>: the same GEMV on pre-quantized activations",
+                "kernel": "gemv_rows_kernel<0, STEPS, true, false, 1>: the same GEMV on pre-quantized activations",
                 "achieved": round(prequant_achieved, 2),
                 "frac": round(prequant_achieved / HBM_PEAK_GBS, 4),
                 "achieved_graph": round(prequant_graph, 2),
