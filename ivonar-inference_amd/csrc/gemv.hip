@@ -419,20 +419,29 @@ __device__ __forceinline__ void static_for(F&& f) {
 //
 // Layout: the lanes 4g .. 4g + 3 hold the four float4 of one 16-input quad g;
 // q8 word k of the quad holds inputs 4b + k at byte b, so lane j (= t & 3)
-// forms word j from byte j of each of the four lanes' packed bytes (three DPP
-// quad permutations), then the split word j with the word of lane j ^ 2.  The
-// bytes are biased (b = q + 128 = q ^ 0x80), which keeps the low nibble of q
-// and flips bit 3 of the high one: one XOR with 0x88888888 fixes the split
-// words of high nibbles.
-template <int T, int X, typename Step>
+// forms word j from byte j of each of the four lanes' q bytes: three DPP quad
+// permutations bring the other lanes' bytes over and two v_perm_b32 place
+// byte j of each at byte i of the word (source lane i).  The split word j then
+// takes nibbles of its own word and of the word of lane j ^ 2 (see
+// split_quad_word): one rotate and one bitfield insert with per-lane constants.
+// The converted bytes are biased (b = q + 128); one XOR with 0x80 per byte
+// gives q itself.  The chunk sums are dot products of the q bytes with -1 (the
+// LDS copy holds minus the sums) added over the chunk's 16 lanes.
+//
+// ALL: every float4 of the X per thread lies inside the row's chunks (the
+// rows of exact long-row launches), so no store is predicated.
+template <int T, int X, bool ALL, typename Step>
 __device__ __forceinline__ float quantize_row_split(v4f32 (&xv)[X], int n, int chunks, int* lds_words, int* lds_x,
                                                     float* slots, Step&& step) {
+  static_assert(T % 16 == 0, "a row of 16 float4 per chunk starts at a multiple of 16 lanes");
   const int tid = threadIdx.x;
   const int n4 = n >> 2;
   const int j = tid & 3;
+  if (n4 < X * T) {  // zeros past the row (uniform: only rows that are not a whole number of blocks)
 #pragma unroll
-  for (int k = 0; k < X; ++k)
-    if (k * T + tid >= n4) xv[k] = v4f32{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < X; ++k)
+      if (k * T + tid >= n4) xv[k] = v4f32{0.0f, 0.0f, 0.0f, 0.0f};
+  }
   float amax = 0.0f;
 #pragma unroll
   for (int k = 0; k < X; ++k)
@@ -445,9 +454,20 @@ __device__ __forceinline__ float quantize_row_split(v4f32 (&xv)[X], int n, int c
   for (int w = 1; w < T / 64; ++w) amax = fmaxf(amax, slots[w]);
   const float scale = fmaxf(amax / 127.0f, 1e-5f);
   const float inv = 1.0f / scale;
-  const unsigned own_shift = 8 * j;
-  const unsigned shift1 = 8 * (1 ^ j), shift2 = 8 * (2 ^ j), shift3 = 8 * (3 ^ j);
-  const unsigned high_fix = j < 2 ? 0x88888888u : 0u;
+  // Per-lane constants: v_perm_b32 selectors (byte values 0..3 pick from the
+  // second operand, 4..7 from the first, 0x0C gives zero) and the split's
+  // rotation and nibble mask.
+  unsigned sel_near = 0x0C0C0C0Cu, sel_far = 0x0C0C0C0Cu;
+  sel_near = (sel_near & ~(0xFFu << (8 * j))) | ((unsigned)j << (8 * j));                  // own byte j at j
+  sel_near = (sel_near & ~(0xFFu << (8 * (j ^ 1)))) | ((unsigned)(4 + j) << (8 * (j ^ 1)));  // lane j^1's at j^1
+  sel_far = (sel_far & ~(0xFFu << (8 * (j ^ 2)))) | ((unsigned)j << (8 * (j ^ 2)));          // lane j^2's at j^2
+  sel_far = (sel_far & ~(0xFFu << (8 * (j ^ 3)))) | ((unsigned)(4 + j) << (8 * (j ^ 3)));    // lane j^3's at j^3
+  const unsigned rot = j < 2 ? 4u : 28u;
+  const unsigned nibbles = j < 2 ? 0x0F0F0F0Fu : 0xF0F0F0F0u;
+  // float4 f = k*T + tid is quad g = f >> 2 (chunk g >> 2, quad g & 3) and
+  // chunk f >> 4: both advance by a constant per k.
+  int* word_dst = lds_words + ((((tid >> 2) & 3) * chunks + (tid >> 4)) << 2) + j;
+  int* sum_dst = lds_x + (tid >> 4);
   static_for<X>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     const int f = k * T + tid;
@@ -464,26 +484,23 @@ __device__ __forceinline__ float quantize_row_split(v4f32 (&xv)[X], int n, int c
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = (float)((int)__builtin_rintf(xv[k][e] / scale) + 128);
     }
-    unsigned packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[0], 0, 0u);
-    packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[1], 1, packed4);
-    packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[2], 2, packed4);
-    packed4 = __builtin_amdgcn_cvt_pk_u8_f32(v[3], 3, packed4);
-    // Word j of the quad: byte j of lane 4g + i's bytes at byte i.
-    const unsigned p1 = (unsigned)__builtin_amdgcn_mov_dpp((int)packed4, 0xB1, 0xF, 0xF, false);  // lane ^ 1
-    const unsigned p2 = (unsigned)__builtin_amdgcn_mov_dpp((int)packed4, 0x4E, 0xF, 0xF, false);  // lane ^ 2
-    const unsigned p3 = (unsigned)__builtin_amdgcn_mov_dpp((int)packed4, 0x1B, 0xF, 0xF, false);  // lane ^ 3
-    unsigned word = __builtin_amdgcn_ubfe(packed4, own_shift, 8) << own_shift;
-    word |= __builtin_amdgcn_ubfe(p1, own_shift, 8) << shift1;
-    word |= __builtin_amdgcn_ubfe(p2, own_shift, 8) << shift2;
-    word |= __builtin_amdgcn_ubfe(p3, own_shift, 8) << shift3;
+    unsigned biased = __builtin_amdgcn_cvt_pk_u8_f32(v[0], 0, 0u);
+    biased = __builtin_amdgcn_cvt_pk_u8_f32(v[1], 1, biased);
+    biased = __builtin_amdgcn_cvt_pk_u8_f32(v[2], 2, biased);
+    biased = __builtin_amdgcn_cvt_pk_u8_f32(v[3], 3, biased);
+    const unsigned q4 = biased ^ 0x80808080u;  // the four q bytes
+    const unsigned p1 = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+    const unsigned p2 = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+    const unsigned p3 = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x1B, 0xF, 0xF, false);  // lane ^ 3
+    const unsigned word = __builtin_amdgcn_perm(p1, q4, sel_near) | __builtin_amdgcn_perm(p3, p2, sel_far);
     const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp((int)word, 0x4E, 0xF, 0xF, false);  // lane ^ 2
-    const unsigned split = split_quad_word(word, partner, j) ^ high_fix;
-    // Chunk sums: the 16 float4 of chunk f / 16 sit in one 16-lane row.
-    const int sum = chunk_lane_sum((int)__builtin_amdgcn_udot4(packed4, 0x01010101u, 0u, false) - 4 * 128);
-    if (f < chunks * 16) {
-      const int g = f >> 2;  // quad g: chunk g / 4, quad g % 4
-      lds_words[(((g & 3) * chunks + (g >> 2)) << 2) + j] = (int)split;
-      if ((tid & 15) == 0) lds_x[f >> 4] = -sum;
+    const unsigned turned = __builtin_amdgcn_alignbit(word, word, rot);
+    const unsigned split = (turned & nibbles) | (partner & ~nibbles);
+    // Minus the chunk sums: the 16 float4 of chunk f / 16 sit in one 16-lane row.
+    const int neg_sum = chunk_lane_sum(sdot4(q4, -1, 0));
+    if (ALL || f < chunks * 16) {
+      word_dst[k * (T / 4)] = (int)split;
+      if ((tid & 15) == 0) sum_dst[k * (T / 16)] = neg_sum;
     }
     step(kc);
   });
@@ -713,7 +730,8 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
       if constexpr (decltype(sc)::value > 0) issue_step(st[sc], pb, it, sc);
     });
     float* slots = reinterpret_cast<float*>(lds_dump + 16);
-    sx[0] = quantize_row_split<kBlock, kX>(xv, sh.n, chunks, reinterpret_cast<int*>(lds_q), lds_x, slots, [&](auto kc) {
+    sx[0] = quantize_row_split<kBlock, kX, EXACT>(xv, sh.n, chunks, reinterpret_cast<int*>(lds_q), lds_x, slots,
+                                                   [&](auto kc) {
       constexpr int k = decltype(kc)::value;
       if constexpr (k % 2 == 0 && k / 2 + kMid + 1 < STEPS)
         issue_step(st[k / 2 + kMid + 1], pb, it, std::integral_constant<int, k / 2 + kMid + 1>{});
