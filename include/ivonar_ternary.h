@@ -74,9 +74,10 @@ void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane);
 /* K-splits S of the token GEMM (gemm_tile_*) for m tokens: its fp32 order is S
  * contiguous ranges of the 128-input groups, each summed in ascending order,
  * then the S partial sums added in order (S = 1: one chain).  S = 0: one
- * token, which gemm_tile_* hands to the decode GEMV on the pre-quantized row
- * (gemv_prequant_store's kernel), so its order is ivonar_gemv_plan's lane
- * layout.  Uses the current device's LDS size. */
+ * token, or two tokens of 4097..32768 inputs, which gemm_tile_* hands to the
+ * decode GEMV on each pre-quantized row (gemv_prequant_store's kernel), so
+ * each token's order is ivonar_gemv_plan's lane layout.  Uses the current
+ * device's LDS size. */
 int ivonar_gemm_plan(int m, int rows, int n);
 
 /* ------------------------------------------------------------ decode GEMV
