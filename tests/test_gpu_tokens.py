@@ -154,14 +154,14 @@ def test_token_gemv_sliced_stress_shapes(cuda, oracle):
 
 
 def test_token_gemv_graph_replays(cuda, oracle):
-    """One-slice and sliced token GEMVs captured in a HIP graph replay bit-identically to the eager calls,
-    with eager calls of the same kernels (on the default stream) between the replays."""
+    """One-slice and sliced token GEMVs and the two-token GEMV captured in a HIP graph replay bit-identically
+    to the eager calls, with eager calls of the same kernels (on the default stream) between the replays."""
     import torch
     from ivonar_amd import ops, runtime
 
     rng = np.random.default_rng(77)
     cases = []
-    for m, k, rows in ((5, 4096, 1000), (16, 28672, 512)):
+    for m, k, rows in ((5, 4096, 1000), (16, 28672, 512), (2, 8192, 1000)):
         codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=True)
         matrix = device_matrix(packed, scale_bits, k, bias=b, device=cuda)
         q8, xsum, sx = ops.quantize_rows(_t(rng.standard_normal((m, k)).astype(np.float32), cuda))
@@ -169,6 +169,7 @@ def test_token_gemv_graph_replays(cuda, oracle):
         cases.append((matrix, (q8, xsum, sx), other, torch.empty((m, rows), dtype=torch.float32, device=cuda),
                       torch.empty((m, rows), dtype=torch.float32, device=cuda)))
     assert runtime.gemm_plan(16, 512, 28672) == 56
+    assert runtime.gemm_plan(2, 1000, 8192) == 0
 
     def step():
         for matrix, (q8, xsum, sx), _, out, _ in cases:
