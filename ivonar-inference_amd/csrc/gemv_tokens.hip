@@ -36,7 +36,9 @@
 // into `slices` equal span ranges, one per block row of the grid (grid y):
 // a block then copies and reads only its slice's q8 bytes and q sums, and
 // its waves write their fp32 chains to the scratch ([slice * parts + part]
-// [token][row]) instead of adding them; token_finish_kernel adds them.
+// [token][row]) instead of adding them; the last of a tile group's slices to
+// arrive adds them (token_finish_kernel, in a launch of its own, where the
+// tile groups outnumber the scratch's counters).
 //
 // fp32 order (the CPU oracle's orc_gemm_split with S = PARTS * slices): each
 // wave folds its groups' partials into one fmaf chain per output in ascending
@@ -69,6 +71,12 @@ constexpr int kSlicePartials = 100;  // EPI of a sliced launch: wave chains to t
 struct TokenShape {
   int rows, n, row_bytes, groups, m, parts, tiles_per_block, out_stride;
   int slice_groups;  // groups per K slice (= groups when the grid has one slice)
+  // K-sliced launches: the epilogue the last slice of a tile group applies
+  // after adding the chains itself (kStore, kResidual, kSiluPair), with one
+  // arrival counter per tile group in `counters`; -1: token_finish_kernel
+  // adds them in a launch of its own.
+  int finish_epi;
+  unsigned* counters;
 };
 
 // 2-bit field f of each byte of w, as an int8 code 0..2.
@@ -248,14 +256,73 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
   }
 
   if constexpr (EPI == kSlicePartials) {
-    // Chain of lane (c, kb) for tokens 4kb + v of row c, to [slice * parts + part][token][row].
+    // Chain of lane (c, kb) for tokens 4kb + v of row c, to [slice * parts + part][token][row],
+    // stored device-coherent (performed past the XCD's L2) for the in-kernel finish.
     const int out_row = tile * 16 + c;
     const int chain = blockIdx.y * sh.parts + part;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int t = 4 * kb + v;
-      if (t < m && out_row < sh.rows) chains[((size_t)chain * m + t) * sh.rows + out_row] = acc[v];
+      if (t < m && out_row < sh.rows)
+        __hip_atomic_store(chains + ((size_t)chain * m + t) * sh.rows + out_row, acc[v], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (sh.finish_epi < 0) return;
+    // In-kernel finish.  Every thread's chains are performed device-wide
+    // before the block counts itself in; the block whose count is the last of
+    // the tile group's slices then reads all of the group's chains (after its
+    // count returned, device-coherent) and finishes them as
+    // token_finish_kernel does, then clears the counter for the next launch.
+    // No block waits for another.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int* last_slot = reinterpret_cast<int*>(dump);
+    if (tid == 0)
+      *last_slot = __hip_atomic_fetch_add(sh.counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   gridDim.y - 1;
+    __syncthreads();
+    if (*last_slot == 0) return;
+    const int chain_count = (int)gridDim.y * sh.parts;
+    const size_t stride = (size_t)m * sh.rows;
+    const int tiles = sh.tiles_per_block;
+    // The chains are loaded eight at a time before they are added (in chain
+    // order), so a row's loads share one round trip per eight.
+    auto total_of = [&](int t, int r) {
+      const float* src = chains + (size_t)t * sh.rows + r;
+      float total = 0.0f;
+      for (int k0 = 0; k0 < chain_count; k0 += 8) {
+        float part[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          part[j] = k0 + j < chain_count
+                        ? __hip_atomic_load(src + (size_t)(k0 + j) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (k0 + j < chain_count) total = k0 + j == 0 ? part[0] : total + part[j];
+      }
+      float y = total * scale_in[t];
+      if (bias != nullptr) y = y + bias[r];
+      return y;
+    };
+    if (sh.finish_epi == kSiluPair) {
+      for (int o = tid; o < tiles * 8 * m; o += nthr) {
+        const int pair = o & 7, rest = o >> 3, tl = rest % tiles, t = rest / tiles;
+        const int r0 = (blockIdx.x * tiles + tl) * 16 + 2 * pair;
+        if (r0 + 1 < sh.rows) output[(size_t)t * sh.out_stride + (r0 >> 1)] = ivo_silu(total_of(t, r0)) * total_of(t, r0 + 1);
+      }
+    } else {
+      for (int o = tid; o < tiles * 16 * m; o += nthr) {
+        const int r = o & 15, rest = o >> 4, tl = rest % tiles, t = rest / tiles;
+        const int out_row = (blockIdx.x * tiles + tl) * 16 + r;
+        if (out_row >= sh.rows) continue;
+        float* dst = output + (size_t)t * sh.out_stride + out_row;
+        const float y = total_of(t, out_row);
+        if (sh.finish_epi == kResidual) *dst = *dst + y;
+        else *dst = y;
+      }
+    }
+    if (tid == 0) __hip_atomic_store(sh.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 
@@ -355,10 +422,11 @@ hipError_t launch_part(hipStream_t stream, const GemmArgs& a, const TokenShape& 
 }
 
 template <int EPI>
-hipError_t launch_epi(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan, float* chains) {
+hipError_t launch_epi(hipStream_t stream, const GemmArgs& a, const TokenPlan& plan, float* chains,
+                      unsigned* counters = nullptr, int finish_epi = -1) {
   const int groups = a.n / kGroup;
   TokenShape sh{a.rows, a.n, a.row_bytes, a.groups, a.m, plan.parts, plan.tiles_per_block, a.out_stride,
-                groups / plan.slices};
+                groups / plan.slices, finish_epi, counters};
   const int threads = 64 * plan.parts * plan.tiles_per_block;
   const dim3 blocks(ceil_div(ceil_div(a.rows, 16), plan.tiles_per_block), plan.slices);
   switch (plan.part_spans) {
@@ -440,6 +508,11 @@ hipError_t launch_token_gemv(hipStream_t stream, const GemmArgs& a, const TokenP
   Scratch* work = nullptr;
   hipError_t status = scratch_for_stream(stream, &work);
   if (status != hipSuccess) return status;
+  // The last slice of each tile group finishes it in the same launch when the
+  // group count fits the scratch's counters; otherwise a second kernel does.
+  const int tile_groups = ceil_div(ceil_div(a.rows, 16), plan.tiles_per_block);
+  if (work->sync != nullptr && tile_groups <= kTokenFinishCounters)
+    return launch_epi<kSlicePartials>(stream, a, plan, work->token_partials, work->sync, a.epi);
   status = launch_epi<kSlicePartials>(stream, a, plan, work->token_partials);
   if (status != hipSuccess) return status;
   const int chains = plan.parts * plan.slices;

@@ -33,12 +33,15 @@ struct Scratch {
   int capacity_chunks = 0;
   float* token_partials = nullptr;  // fp32 wave partials of the K-sliced token GEMV
   // Counters that start and end every launch at zero (kSyncBytes): the
-  // argmax's block count.
+  // argmax's block count and the sliced token GEMV's tile-group arrivals.
   unsigned* sync = nullptr;
 };
 constexpr int kSyncBytes = 4096;
 // The argmax's block count, in the last 128-byte line of the sync region.
 constexpr int kArgmaxCountWord = kSyncBytes / 4 - 32;
+// Arrival counters of the K-sliced token GEMV's tile groups: the sync
+// region's words 0 .. kTokenFinishCounters - 1.
+constexpr int kTokenFinishCounters = kArgmaxCountWord;
 // Capacity of Scratch::token_partials (floats; 16 MB per device).
 constexpr long long kTokenPartialFloats = 4LL << 20;
 hipError_t scratch_for_stream(hipStream_t stream, Scratch** out);
