@@ -236,6 +236,14 @@ hipError_t ivonar_validate_ternary(hipStream_t stream, const uint8_t* packed, lo
 int ivonar_stream_read_sink_words(void);
 hipError_t ivonar_stream_read(hipStream_t stream, const void* data, long long bytes, unsigned* sink);
 
+/* Test export (no reference counterpart): the largest number of row-tile
+ * groups whose K-sliced token GEMV is finished inside its own launch (by the
+ * last slice of each group); larger calls add the slices' chains in a second
+ * kernel.  Default and maximum 992; 0 makes every K-sliced call take the
+ * second kernel.  Process-wide; returns the previous value, or -1 (and
+ * changes nothing) for a value outside 0..992. */
+int ivonar_token_finish_limit(int groups);
+
 #ifdef __cplusplus
 }
 #endif

@@ -266,6 +266,11 @@ void ivonar_gemv_plan(int rows, int n, int* lanes, int* rows_per_lane) { gemv_pl
 
 int ivonar_gemm_plan(int m, int rows, int n) { return gemm_splits(m, rows, n); }
 
+int ivonar_token_finish_limit(int groups) {
+  if (groups < 0 || groups > kTokenFinishCounters) return -1;
+  return defines().token_finish_groups.exchange(groups);
+}
+
 #define GEMV_PASS_ENTRY(MODE, EPI, PREQUANT)                                                                      \
   gemv_entry(stream, MODE, EPI, PREQUANT, input, aux, q8_in, xsum_in, scale_in, packed, scales, bias, output, rows, \
              n, row_bytes, groups, splits, eps)

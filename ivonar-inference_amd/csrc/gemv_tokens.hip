@@ -511,7 +511,7 @@ hipError_t launch_token_gemv(hipStream_t stream, const GemmArgs& a, const TokenP
   // The last slice of each tile group finishes it in the same launch when the
   // group count fits the scratch's counters; otherwise a second kernel does.
   const int tile_groups = ceil_div(ceil_div(a.rows, 16), plan.tiles_per_block);
-  if (work->sync != nullptr && tile_groups <= kTokenFinishCounters)
+  if (work->sync != nullptr && tile_groups <= defines().token_finish_groups && tile_groups <= kTokenFinishCounters)
     return launch_epi<kSlicePartials>(stream, a, plan, work->token_partials, work->sync, a.epi);
   status = launch_epi<kSlicePartials>(stream, a, plan, work->token_partials);
   if (status != hipSuccess) return status;

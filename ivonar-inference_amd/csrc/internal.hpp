@@ -22,6 +22,9 @@ struct Defines {
   std::atomic<int> tile{32};
   std::atomic<int> max_chunks{70};
   std::atomic<int> max_topk{256};
+  // Tile groups of a K-sliced token GEMV finished in-launch (at most the
+  // scratch's counters; ivonar_token_finish_limit).
+  std::atomic<int> token_finish_groups{992};
 };
 Defines& defines();
 
@@ -42,6 +45,7 @@ constexpr int kArgmaxCountWord = kSyncBytes / 4 - 32;
 // Arrival counters of the K-sliced token GEMV's tile groups: the sync
 // region's words 0 .. kTokenFinishCounters - 1.
 constexpr int kTokenFinishCounters = kArgmaxCountWord;
+static_assert(kTokenFinishCounters == 992, "the default of Defines::token_finish_groups");
 // Capacity of Scratch::token_partials (floats; 16 MB per device).
 constexpr long long kTokenPartialFloats = 4LL << 20;
 hipError_t scratch_for_stream(hipStream_t stream, Scratch** out);

@@ -106,6 +106,8 @@ def library() -> ctypes.CDLL:
             lib.ivonar_gemm_plan.restype = c_int
             lib.ivonar_stream_read_sink_words.argtypes = []
             lib.ivonar_stream_read_sink_words.restype = c_int
+            lib.ivonar_token_finish_limit.argtypes = [c_int]
+            lib.ivonar_token_finish_limit.restype = c_int
             for name, argtypes in SIGNATURES.items():
                 function = getattr(lib, name)
                 function.argtypes = [c_void_p, *argtypes]

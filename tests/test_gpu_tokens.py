@@ -147,6 +147,23 @@ def test_token_gemv_sliced_epilogues(cuda, oracle, epilogue):
                  pad=3) == 56
 
 
+@pytest.mark.parametrize("epilogue", ["store", "residual", "silu_pair"])
+def test_token_gemv_sliced_second_kernel(cuda, oracle, epilogue):
+    """With the in-launch finish switched off (ivonar_token_finish_limit(0), as for calls with more row-tile
+    groups than the scratch has counters), the K-sliced token GEMV adds its chains in token_finish_kernel:
+    the same bits in the same order."""
+    from ivonar_amd import runtime
+
+    lib = runtime.library()
+    previous = lib.ivonar_token_finish_limit(0)
+    assert previous == 992
+    try:
+        assert _case(oracle, cuda, 16, 28672, 514, True, seed=63, epilogue=epilogue,
+                     pad=0 if epilogue == "store" else 3) == 56
+    finally:
+        assert lib.ivonar_token_finish_limit(previous) == 0
+
+
 def test_token_gemv_sliced_stress_shapes(cuda, oracle):
     """K=28672 -> N=8192 with 8 and 16 tokens: two and four slices of two or four waves per row tile."""
     assert _case(oracle, cuda, 8, 28672, 8192, False, seed=7) == 8

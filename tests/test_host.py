@@ -56,6 +56,18 @@ def test_reference_kernel_names_are_all_present():
     assert all(name in runtime.SIGNATURES for name in reference)
 
 
+def test_token_finish_limit_range():
+    """The in-launch finish limit of the K-sliced token GEMV: 0..992, returning the previous value."""
+    from ivonar_amd import runtime
+
+    lib = runtime.library()
+    assert lib.ivonar_token_finish_limit(992) == 992
+    assert lib.ivonar_token_finish_limit(993) == -1
+    assert lib.ivonar_token_finish_limit(-1) == -1
+    assert lib.ivonar_token_finish_limit(0) == 992
+    assert lib.ivonar_token_finish_limit(992) == 0
+
+
 def test_host_only_calls():
     from ivonar_amd import runtime
 
