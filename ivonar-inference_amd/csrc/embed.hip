@@ -119,8 +119,9 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
     for (int w = 1; w < kArgmaxThreads / 64; ++w) b.take(best_value[w], best_index[w]);
     int last = 1;
     if (gridDim.x > 1) {
-      __hip_atomic_store(part_value + blockIdx.x, b.value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(part_index + blockIdx.x, b.index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // The hand-over of store_device (ternary_device.hpp), one thread per block.
+      store_device(part_value + blockIdx.x, b.value);
+      store_device(part_index + blockIdx.x, b.index);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the pair is performed device-wide before the count
       last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     }
@@ -133,8 +134,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
   // count returned, device-coherent).
   Best f{-__builtin_inff(), n};
   for (int blk = tid; blk < (int)gridDim.x; blk += 64)
-    f.take(__hip_atomic_load(part_value + blk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-           __hip_atomic_load(part_index + blk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    f.take(load_device(part_value + blk), load_device(part_index + blk));
   wave_best(f);
   if (tid == 0) {
     *out = f.index < n ? f.index : 0;

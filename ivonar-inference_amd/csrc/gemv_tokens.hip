@@ -264,16 +264,15 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
     for (int v = 0; v < 4; ++v) {
       const int t = 4 * kb + v;
       if (t < m && out_row < sh.rows)
-        __hip_atomic_store(chains + ((size_t)chain * m + t) * sh.rows + out_row, acc[v], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        store_device(chains + ((size_t)chain * m + t) * sh.rows + out_row, acc[v]);
     }
     if (sh.finish_epi < 0) return;
-    // In-kernel finish.  Every thread's chains are performed device-wide
-    // before the block counts itself in; the block whose count is the last of
-    // the tile group's slices then reads all of the group's chains (after its
-    // count returned, device-coherent) and finishes them as
-    // token_finish_kernel does, then clears the counter for the next launch.
-    // No block waits for another.
+    // In-kernel finish, by the hand-over of store_device (ternary_device.hpp).
+    // Every thread's chains are performed device-wide before the block counts
+    // itself in; the block whose count is the last of the tile group's slices
+    // then reads all of the group's chains (after its count returned,
+    // device-coherent) and finishes them as token_finish_kernel does, then
+    // clears the counter for the next launch.  No block waits for another.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     int* last_slot = reinterpret_cast<int*>(dump);
@@ -295,7 +294,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void token_gemv_kernel(const int8_t
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           part[j] = k0 + j < chain_count
-                        ? __hip_atomic_load(src + (size_t)(k0 + j) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        ? load_device(src + (size_t)(k0 + j) * stride)
                         : 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -418,7 +417,9 @@ hipError_t launch_part(hipStream_t stream, const GemmArgs& a, const TokenShape& 
   if (fill <= 4) return go(token_gemv_kernel<EPI, PART, 4>);
   if (fill <= 8) return go(token_gemv_kernel<EPI, PART, 8>);
   if (fill <= 12) return go(token_gemv_kernel<EPI, PART, 12>);
-  return go(token_gemv_kernel<EPI, PART, 16>);
+  // The plan gives 16-span waves at most 12 fill pieces (16 would spill).
+  if constexpr (PART == 16) return hipErrorInvalidValue;
+  else return go(token_gemv_kernel<EPI, PART, 16>);
 }
 
 template <int EPI>

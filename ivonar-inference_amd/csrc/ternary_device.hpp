@@ -465,9 +465,7 @@ __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int c
 // round trip, a block max and the divisions.  Writes the slice's q8 words
 // (split_quad_word form if `split`), its chunk sums and, from slice 0, the
 // token scale.  slots holds T/64 floats; all threads of the block call it.
-// COHERENT: the stores are device-coherent (agent-scope relaxed atomics, sc1),
-// complete device-wide once the storing wave's vmcnt reaches zero.
-template <int T, int ROUNDS = 8, bool COHERENT = false>
+template <int T, int ROUNDS = 8>
 __device__ __forceinline__ void quantize_plain_slice(const float* __restrict__ row, int n, int slice, bool split,
                                                      int8_t* __restrict__ q8, int32_t* __restrict__ xsum,
                                                      float* __restrict__ scale_out, float* slots) {
@@ -510,16 +508,39 @@ __device__ __forceinline__ void quantize_plain_slice(const float* __restrict__ r
   const int value = (int)word;
   const int total = chunk_lane_sum(word_sum(value));
   const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // lane ^ 2
-  auto put = [](auto* p, auto v) {
-    if constexpr (COHERENT) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
-  };
   if (u < chunks) {
     int32_t* q8w = reinterpret_cast<int32_t*>(q8);
-    put(q8w + u * 16 + (tid & 15), split ? (int)split_quad_word(word, partner, tid & 3) : value);
-    if ((tid & 15) == 0) put(xsum + u, total);
+    q8w[u * 16 + (tid & 15)] = split ? (int)split_quad_word(word, partner, tid & 3) : value;
+    if ((tid & 15) == 0) xsum[u] = total;
   }
-  if (slice == 0 && tid == 0) put(scale_out, scale);
+  if (slice == 0 && tid == 0) *scale_out = scale;
+}
+
+// Hand-over between the blocks of one launch (the argmax's per-block pairs,
+// the K-sliced token GEMV's chains), without any block waiting for another:
+// 1. every value goes out through store_device, an agent-scope store: on
+//    gfx950 a global store with the SC1 scope bit, written through the XCD's
+//    L2 to the device's coherence point;
+// 2. each storing wave waits for vmcnt(0), which counts such a store complete
+//    only once it is performed at that point, then the block barrier;
+// 3. one thread counts the block in with an agent-scope atomic add (performed
+//    at the same point, issued after the wait);
+// 4. the block that reads the final count issues its loads of the values only
+//    after the count returned, through load_device, agent-scope loads (SC1),
+//    served from the coherence point and not from a stale L2 or L1 line;
+//    it then resets the count for the next launch.
+// So every value is complete device-wide before any reader can learn that it
+// exists.  The compiler's full agent-scope release and acquire add an L2
+// writeback and invalidate, which matter only for data stored or loaded
+// without the scope bit (none is handed over here); one writeback per block
+// made such a launch tens of microseconds slower.
+template <typename V>
+__device__ __forceinline__ void store_device(V* p, V v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ V load_device(const V* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace ivo

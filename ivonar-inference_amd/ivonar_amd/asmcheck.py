@@ -205,22 +205,47 @@ def _llvm_tool(name: str) -> str:
     return str(path)
 
 
+def _device_code(obj: Path, tmp: str) -> Path | None:
+    """The gfx950 code object embedded in one of this build's object files (None: host-only object)."""
+    fatbin = Path(tmp) / "fatbin"
+    code = Path(tmp) / "code.o"
+    dumped = subprocess.run([_llvm_tool("llvm-objcopy"), f"--dump-section=.hip_fatbin={fatbin}", str(obj)],
+                            capture_output=True, text=True)
+    if dumped.returncode != 0:
+        if "not found" in dumped.stderr:
+            return None
+        raise RuntimeError(f"llvm-objcopy failed on {obj}: {dumped.stderr}")
+    subprocess.run([_llvm_tool("clang-offload-bundler"), "--unbundle", "--type=o", f"--input={fatbin}",
+                    f"--targets={TARGET}", f"--output={code}"], check=True, capture_output=True)
+    return code
+
+
 def disassemble_object(obj: Path) -> str:
     """gfx950 disassembly of the device code embedded in one of this build's object files."""
     with tempfile.TemporaryDirectory() as tmp:
-        fatbin = Path(tmp) / "fatbin"
-        code = Path(tmp) / "code.o"
-        dumped = subprocess.run([_llvm_tool("llvm-objcopy"), f"--dump-section=.hip_fatbin={fatbin}", str(obj)],
-                                capture_output=True, text=True)
-        if dumped.returncode != 0:
-            if "not found" in dumped.stderr:
-                return ""  # host-only object: no device code
-            raise RuntimeError(f"llvm-objcopy failed on {obj}: {dumped.stderr}")
-        subprocess.run([_llvm_tool("clang-offload-bundler"), "--unbundle", "--type=o", f"--input={fatbin}",
-                        f"--targets={TARGET}", f"--output={code}"], check=True, capture_output=True)
+        code = _device_code(obj, tmp)
+        if code is None:
+            return ""
         result = subprocess.run([_llvm_tool("llvm-objdump"), "-d", "--mcpu=gfx950", str(code)], check=True,
                                 capture_output=True, text=True)
         return result.stdout
+
+
+def kernels_with_scratch(obj: Path) -> list[tuple[str, int]]:
+    """Kernels of the object whose code object metadata asks for private (scratch) memory per lane:
+    register spills, which also make every dispatch set up scratch.  (name, bytes) pairs."""
+    with tempfile.TemporaryDirectory() as tmp:
+        code = _device_code(obj, tmp)
+        if code is None:
+            return []
+        notes = subprocess.run([_llvm_tool("llvm-readelf"), "--notes", str(code)], check=True,
+                               capture_output=True, text=True).stdout
+    found = []
+    for entry in notes.split(".name:")[1:]:
+        size = re.search(r"\.private_segment_fixed_size:\s+(\d+)", entry)
+        if size is not None and int(size.group(1)) > 0:
+            found.append((entry.split("\n", 1)[0].strip(), int(size.group(1))))
+    return found
 
 
 def check_object(obj: Path, name_filter: str | None = None) -> list[Hazard]:

@@ -81,13 +81,18 @@ def _compile(source: Path, output: Path, hipcc: str) -> None:
 
 
 def check_waits(objects) -> None:
-    """Refuse code whose hand-placed vmcnt waits leave a VGPR access ahead of its load (asmcheck)."""
-    from .asmcheck import check_object
+    """Refuse code whose hand-placed vmcnt waits leave a VGPR access ahead of its load (asmcheck), and
+    kernels that spill registers to scratch."""
+    from .asmcheck import check_object, kernels_with_scratch
 
     hazards = [hazard for obj in objects for hazard in check_object(Path(obj))]
     if hazards:
         listing = "\n".join(str(hazard) for hazard in hazards[:20])
         raise RuntimeError(f"{len(hazards)} VGPR accesses precede the wait for their load:\n{listing}")
+    spills = [entry for obj in objects for entry in kernels_with_scratch(Path(obj))]
+    if spills:
+        listing = "\n".join(f"{name}: {size} bytes" for name, size in spills[:20])
+        raise RuntimeError(f"{len(spills)} kernels spill registers to scratch:\n{listing}")
 
 
 def build(verbose: bool = False) -> Path:

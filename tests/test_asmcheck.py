@@ -112,3 +112,9 @@ def test_lds_dma_and_load_over_load_are_not_reported():
 def test_built_objects_have_no_early_reads():
     hazards = [h for obj in sorted(BUILD.glob("*.o")) for h in asmcheck.check_object(obj)]
     assert not hazards, "\n".join(map(str, hazards[:10]))
+
+
+@pytest.mark.skipif(not any(BUILD.glob("*.o")), reason="the HIP library has not been built here")
+def test_built_kernels_use_no_scratch():
+    spills = [entry for obj in sorted(BUILD.glob("*.o")) for entry in asmcheck.kernels_with_scratch(obj)]
+    assert not spills, spills[:10]
