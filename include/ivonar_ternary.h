@@ -43,7 +43,8 @@ extern "C" {
  * launch of its own (rows longer than 4096 inputs that the GEMV does not
  * quantize itself: NORM and ATTN rows, unaligned PLAIN rows, rows above
  * 32768 inputs), the 16 MB of fp32 wave chains of a K-sliced token GEMM
- * (1..16 tokens whose q8 rows exceed LDS) and the argmax's block count.
+ * (1..16 tokens whose q8 rows exceed LDS) with its per-group arrival counts,
+ * and the argmax's block count.
  * Besides it, every stream that makes such a call outside graph capture
  * gets a scratch of its own (about 17 MB, kept until the process ends) on
  * its first call, so eager calls on different streams never share one; a
@@ -52,8 +53,8 @@ extern "C" {
  * whatever thread calls.  Call once per device outside graph capture;
  * replaces the reference's compile_module set-up step
  * (kernels/runtime.py:301-324).  Calls with the device current.  Calling it
- * again clears the argmax counts of every scratch of the device, with no
- * call of the device in flight. */
+ * again clears the arrival counts (argmax, K-sliced token GEMV) of every
+ * scratch of the device, with no call of the device in flight. */
 hipError_t ivonar_init(int device);
 
 /* Process-wide values the reference passes as -D defines to NVRTC
