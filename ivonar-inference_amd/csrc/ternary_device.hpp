@@ -240,14 +240,14 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Block-wide max over the 4 waves; every thread gets the result.
+// Block-wide max over the 4 waves; every thread gets the result.  A block
+// reduces at most once into the same slots (one token row per block), so
+// no barrier follows the slot reads.
 __device__ __forceinline__ float block_max(float v, float* slots) {
   v = wave_max(v);
   if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
   __syncthreads();
-  const float peak = fmaxf(fmaxf(slots[0], slots[1]), fmaxf(slots[2], slots[3]));
-  __syncthreads();
-  return peak;
+  return fmaxf(fmaxf(slots[0], slots[1]), fmaxf(slots[2], slots[3]));
 }
 
 // The reference kernel's reduction tree for a sum of squares over a 256-thread
@@ -274,8 +274,7 @@ __device__ __forceinline__ float tree_reduce(float s, float* slots) {
   __syncthreads();
   float total = 0.0f;
   for (int w = 0; w < kThreads / 32; ++w) total = total + slots[w];
-  __syncthreads();
-  return total;
+  return total;  // used once per block, like block_max: no barrier after the reads
 }
 
 __device__ __forceinline__ float tree_sum_squares(const float* __restrict__ x, int n, float* slots) {
