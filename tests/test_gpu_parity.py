@@ -210,10 +210,11 @@ def test_gemv_long_rows_back_to_back(cuda, oracle, rows, k):
         assert_bits_equal(got[1, i], mine, f"unaligned input, call {i}")
 
 
-# Rows the GEMV quantizes inside its own launch (16-byte aligned PLAIN rows of 4097..32768 inputs), with
-# the values the in-block quantizer treats specially: its u = fma(x, 1/s, 128) rounding decides every
-# value except those within 2e-5 of a half-integer, which take the exact division.
-@pytest.mark.parametrize("k", [4100, 8192, 12288, 28672, 32768])
+# Rows the GEMV quantizes inside its own launch (16-byte aligned PLAIN rows of 4097..32768 inputs, and
+# rows of up to 4096 inputs through the fused prologue), with the values both quantizers treat
+# specially: their u = fma(x, 1/s, 128) rounding decides every value except those within 3e-5 of a
+# half-integer, which take the exact division.
+@pytest.mark.parametrize("k", [24, 1024, 1100, 4096, 4100, 8192, 12288, 28672, 32768])
 def test_gemv_in_launch_quantizer_edge_rows(cuda, oracle, k):
     """Zero row (scale floor 1e-5, every q 0), a row below the floor, exact ties x/s = j + 1/2 (s a power
     of two, so x/s is exact and rint goes to even), values one float step either side of those ties, -0.0
