@@ -22,7 +22,9 @@ on any path (a loop is iterated to a fixed point).
 
 The code object is taken from the build's object files
 (``.hip_fatbin`` section, gfx950 entry) and disassembled with ROCm's LLVM
-tools; only code compiled from this repository is read.
+tools; only code compiled from this repository is read.  The same code
+objects' metadata also names any kernel that asks for private (scratch)
+memory, i.e. spills registers (``kernels_with_scratch``).
 """
 
 from __future__ import annotations
