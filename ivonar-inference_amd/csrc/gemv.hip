@@ -235,7 +235,15 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
         reinterpret_cast<int*>(lds_q)[(w * chunks + u) * 4 + k] = value;
       }
     } else {
-      sx = quantize_row_to_lds<MODE>(src, chunks, reinterpret_cast<unsigned char*>(lds_q), slots);
+      // Each thread loads only the batches of 256 inputs a row can reach
+      // (the clamped loads past the row are not free): rows of fewer than 64
+      // lanes have at most 32 chunks (one step per lane), 2048 inputs, and
+      // rows of up to 1024 inputs (the decoder's model width) take a
+      // four-batch copy of the prologue (one block-uniform branch).
+      unsigned char* q = reinterpret_cast<unsigned char*>(lds_q);
+      if constexpr (LANES == 64) sx = quantize_row_to_lds<MODE, kBatch>(src, chunks, q, slots);
+      else if (sh.n <= 4 * kThreads) sx = quantize_row_to_lds<MODE, 4>(src, chunks, q, slots);
+      else sx = quantize_row_to_lds<MODE, kBatch / 2>(src, chunks, q, slots);
     }
     __syncthreads();
 #pragma unroll

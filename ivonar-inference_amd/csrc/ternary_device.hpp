@@ -406,46 +406,47 @@ __device__ __forceinline__ int chunk_lane_sum(int v) {
 }
 
 // Whole-block quantizer for one PLAIN or NORM token row of at most
-// kThreads * kBatch inputs that reads the row once: thread t holds inputs
+// kThreads * NB inputs that reads the row once: thread t holds inputs
 // t + 256*b in registers, which is also the reference's order for the
 // sum-of-squares partials (so the fp32 result is the same as row_scale's).
 // The q8 bytes go to LDS in the quad-planar layout (quad w of chunk u at
 // 16-byte slot w*C + u; word k of a quad holds inputs 16w + k + 4b' at byte
 // b'), zero past n up to C*64.  Returns the token scale.  All threads of the
 // block call it; it ends with the block's writes not yet fenced.
-template <int MODE>
+template <int MODE, int NB = kBatch>
 __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int chunks, unsigned char* lds_q,
                                                      float* slots) {
   static_assert(MODE == kPlain || MODE == kNorm, "register path for PLAIN and NORM rows");
+  static_assert(NB >= 1 && NB <= kBatch, "at most kBatch inputs per thread");
   const int tid = threadIdx.x;
   const int n = src.n;
-  float v[kBatch], w[kBatch];
+  float v[NB], w[NB];
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b) {
+  for (int b = 0; b < NB; ++b) {
     const int i = min(b * kThreads + tid, n - 1);
     v[b] = src.input[i];
     w[b] = MODE == kNorm ? src.aux[i] : 1.0f;
   }
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b)
+  for (int b = 0; b < NB; ++b)
     if (b * kThreads + tid >= n) v[b] = 0.0f;
   float inv_rms = 1.0f;
   if constexpr (MODE == kNorm) {
     float s = 0.0f;
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) s = __builtin_fmaf(v[b], v[b], s);
+    for (int b = 0; b < NB; ++b) s = __builtin_fmaf(v[b], v[b], s);
     inv_rms = 1.0f / __builtin_sqrtf(tree_reduce(s, slots) / (float)n + src.eps);
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b) {
+  for (int b = 0; b < NB; ++b) {
     if constexpr (MODE == kNorm) v[b] = fminf(fmaxf(v[b] * inv_rms, -8.0f), 8.0f) * w[b];
     amax = fmaxf(amax, fabsf(v[b]));
   }
   amax = block_max(amax, slots + 32);
   const float scale = fmaxf(amax / 127.0f, 1e-5f);
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b) {
+  for (int b = 0; b < NB; ++b) {
     const int i = b * kThreads + tid;
     if (i < chunks * kChunk) {
       const int q = i < n ? (int)__builtin_rintf(v[b] / scale) : 0;
