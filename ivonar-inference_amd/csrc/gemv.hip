@@ -210,13 +210,20 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
   const int first = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   const int steps = (chunks + lanes - 1) / lanes;
 
-  // Weights of the first row step go out before the activation prologue.
+  // Weights of the first row step go out before the activation prologue
+  // (for rows the block quantizes from registers, right behind the row).
   // Loads are never predicated (rows past the matrix are clamped inside
   // load_step), so the wait counts before each use stay exact.
   Step<NJ> a, b;
   int it = __builtin_amdgcn_readfirstlane(first);  // wave-uniform: the per-item branches are scalar
-  load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
-                                                          it * rows_per_iter + slot * kRows, 0, sub, chunks);
+  auto first_loads = [&]() {
+    load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
+                                                            it * rows_per_iter + slot * kRows, 0, sub, chunks);
+  };
+  // PLAIN and NORM rows quantized in the block issue the first weights right
+  // behind the row's loads, so the prologue waits for the row only.
+  constexpr bool kWeightsAfterRow = FUSED && MODE != kAttn;
+  if constexpr (!kWeightsAfterRow) first_loads();
 
   float sx;
   int4 qr[QREG ? NJ : 1][4];
@@ -241,9 +248,9 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
       // rows of up to 1024 inputs (the decoder's model width) take a
       // four-batch copy of the prologue (one block-uniform branch).
       unsigned char* q = reinterpret_cast<unsigned char*>(lds_q);
-      if constexpr (LANES == 64) sx = quantize_row_to_lds<MODE, kBatch>(src, chunks, q, slots);
-      else if (sh.n <= 4 * kThreads) sx = quantize_row_to_lds<MODE, 4>(src, chunks, q, slots);
-      else sx = quantize_row_to_lds<MODE, kBatch / 2>(src, chunks, q, slots);
+      if constexpr (LANES == 64) sx = quantize_row_to_lds<MODE, kBatch>(src, chunks, q, slots, first_loads);
+      else if (sh.n <= 4 * kThreads) sx = quantize_row_to_lds<MODE, 4>(src, chunks, q, slots, first_loads);
+      else sx = quantize_row_to_lds<MODE, kBatch / 2>(src, chunks, q, slots, first_loads);
     }
     __syncthreads();
 #pragma unroll

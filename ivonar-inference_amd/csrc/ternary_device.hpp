@@ -413,9 +413,13 @@ __device__ __forceinline__ int chunk_lane_sum(int v) {
 // 16-byte slot w*C + u; word k of a quad holds inputs 16w + k + 4b' at byte
 // b'), zero past n up to C*64.  Returns the token scale.  All threads of the
 // block call it; it ends with the block's writes not yet fenced.
-template <int MODE, int NB = kBatch>
+struct NoLoads {
+  __device__ void operator()() const {}
+};
+
+template <int MODE, int NB = kBatch, typename AfterLoads = NoLoads>
 __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int chunks, unsigned char* lds_q,
-                                                     float* slots) {
+                                                     float* slots, AfterLoads after_loads = AfterLoads{}) {
   static_assert(MODE == kPlain || MODE == kNorm, "register path for PLAIN and NORM rows");
   static_assert(NB >= 1 && NB <= kBatch, "at most kBatch inputs per thread");
   const int tid = threadIdx.x;
@@ -427,6 +431,11 @@ __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int c
     v[b] = src.input[i];
     w[b] = MODE == kNorm ? src.aux[i] : 1.0f;
   }
+  // Loads the caller issues behind the row's (loads return in order, so the
+  // row's wait does not include them).
+  __builtin_amdgcn_sched_barrier(0);
+  after_loads();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int b = 0; b < NB; ++b)
     if (b * kThreads + tid >= n) v[b] = 0.0f;
