@@ -220,9 +220,10 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
     load_step<NJ, EPI != kPartials, LANES, EPI == kResidual, EXACT>(a, packed, scales, output, sh,
                                                             it * rows_per_iter + slot * kRows, 0, sub, chunks);
   };
-  // PLAIN and NORM rows quantized in the block issue the first weights right
-  // behind the row's loads, so the prologue waits for the row only.
-  constexpr bool kWeightsAfterRow = FUSED && MODE != kAttn;
+  // PLAIN and NORM rows quantized in the block, and pre-quantized rows held
+  // in registers, issue the first weights right behind the row's loads, so
+  // the prologue waits for the row only.
+  constexpr bool kWeightsAfterRow = (FUSED && MODE != kAttn) || (!FUSED && QREG);
   if constexpr (!kWeightsAfterRow) first_loads();
 
   float sx;
@@ -274,6 +275,9 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
       for (int w = 0; w < 4; ++w) qr[j][w] = gq[u * 4 + w];
       xr[j] = in.xsum_in[u];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    first_loads();
+    __builtin_amdgcn_sched_barrier(0);
     if (!sh.split) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
