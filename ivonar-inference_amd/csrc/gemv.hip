@@ -248,10 +248,17 @@ __global__ __launch_bounds__(block_threads<ROLL>()) void gemv_kernel(GemvPtrs in
       // lanes have at most 32 chunks (one step per lane), 2048 inputs, and
       // rows of up to 1024 inputs (the decoder's model width) take a
       // four-batch copy of the prologue (one block-uniform branch).
+      // A 16-byte aligned PLAIN row is read as float4.
       unsigned char* q = reinterpret_cast<unsigned char*>(lds_q);
-      if constexpr (LANES == 64) sx = quantize_row_to_lds<MODE, kBatch>(src, chunks, q, slots, first_loads);
-      else if (sh.n <= 4 * kThreads) sx = quantize_row_to_lds<MODE, 4>(src, chunks, q, slots, first_loads);
-      else sx = quantize_row_to_lds<MODE, kBatch / 2>(src, chunks, q, slots, first_loads);
+      const bool vec = MODE == kPlain && (sh.n & 3) == 0 && (reinterpret_cast<uintptr_t>(in.input) & 15) == 0;
+      auto quantize = [&](auto nb_c) {
+        constexpr int NB = decltype(nb_c)::value;
+        if (vec) return quantize_plain_row4_to_lds<NB>(src, chunks, q, slots, first_loads);
+        return quantize_row_to_lds<MODE, NB>(src, chunks, q, slots, first_loads);
+      };
+      if constexpr (LANES == 64) sx = quantize(std::integral_constant<int, kBatch>{});
+      else if (sh.n <= 4 * kThreads) sx = quantize(std::integral_constant<int, 4>{});
+      else sx = quantize(std::integral_constant<int, kBatch / 2>{});
     }
     __syncthreads();
 #pragma unroll

@@ -466,6 +466,50 @@ __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int c
   return scale;
 }
 
+// quantize_row_to_lds for a 16-byte aligned PLAIN row of n inputs (n a
+// multiple of 4): thread t holds float4 t + 256c (inputs 4(t + 256c) .. + 3),
+// one load instruction per four inputs instead of one per input.  The
+// absmax is order-free and every input is quantized on its own, so the q8
+// bytes are the same.
+template <int NB, typename AfterLoads = NoLoads>
+__device__ __forceinline__ float quantize_plain_row4_to_lds(const RowSource& src, int chunks, unsigned char* lds_q,
+                                                            float* slots, AfterLoads after_loads = AfterLoads{}) {
+  static_assert(NB % 4 == 0 && NB <= kBatch, "whole float4 per thread");
+  constexpr int NC = NB / 4;
+  const int tid = threadIdx.x;
+  const int n4 = src.n >> 2;
+  const float4* x4 = reinterpret_cast<const float4*>(src.input);
+  float4 v[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) v[c] = x4[min(c * kThreads + tid, n4 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  after_loads();
+  __builtin_amdgcn_sched_barrier(0);
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c * kThreads + tid >= n4) v[c] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[c].x), fabsf(v[c].y))), fmaxf(fabsf(v[c].z), fabsf(v[c].w)));
+  }
+  amax = block_max(amax, slots + 32);
+  const float scale = fmaxf(amax / 127.0f, 1e-5f);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int f = c * kThreads + tid;
+    if (f < chunks * 16) {
+      const float e[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // inputs past the row (f >= n4) hold zeros, which quantize to 0
+        const int q = (int)__builtin_rintf(e[k] / scale);
+        const int i = 4 * f + k, u = i >> 6, r = i & 63;
+        lds_q[((((r >> 4) & 3) * chunks + u) << 4) + ((r & 3) << 2) + ((r >> 2) & 3)] = (unsigned char)(q & 0xff);
+      }
+    }
+  }
+  return scale;
+}
+
 // One block's share of the PLAIN quantizer for a 16-byte aligned row of n
 // inputs (n a multiple of 4): T/16 chunks (slice `slice`), one q8 word per
 // thread.  Every thread issues all of its loads in one round - its four
