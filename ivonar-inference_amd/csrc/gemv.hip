@@ -591,7 +591,9 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
                                                         const float* __restrict__ bias, float* __restrict__ output,
                                                         int32_t* __restrict__ partials, GemvShape sh) {
   constexpr int kBlock = 512;  // one block of 8 waves per CU: up to 256 VGPRs for the steps in flight
-  constexpr int kCopy = 4;     // int4 words of the q8 row per thread: rows up to 32768 inputs
+  // int4 words of a q8 row per thread: a row of STEPS * 4096 inputs is STEPS * 256 of them (no
+  // clamped duplicate loads: each load instruction costs the CU's memory pipeline).
+  constexpr int kCopy = (STEPS * 256 + kBlock - 1) / kBlock;
   // Loads of a row pair besides its steps: the bias and one residual base per token.
   constexpr int kSide = 1 + MT;
   static_assert(MT == 1 || (!QUANT && EPI != kPartials), "several tokens: pre-quantized rows and an output epilogue");
@@ -710,9 +712,11 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
     issue_step(st[0], pb, it, std::integral_constant<int, 0>{});
     // The copy's loads are older than step 0's three.
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-      asm volatile("s_waitcnt vmcnt(3)" : "+v"(qv[t][0]), "+v"(qv[t][1]), "+v"(qv[t][2]), "+v"(qv[t][3]), "+v"(xv[t])
-                   : : "memory");
+    for (int t = 0; t < MT; ++t) {
+      asm volatile("s_waitcnt vmcnt(3)" : "+v"(xv[t]) : : "memory");
+#pragma unroll
+      for (int k = 0; k < kCopy; ++k) asm volatile("s_waitcnt vmcnt(3)" : "+v"(qv[t][k]) : : "memory");
+    }
     int4* dump = reinterpret_cast<int4*>(lds_dump);
     static_for<kCopy>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
