@@ -594,8 +594,10 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   // int4 words of a q8 row per thread: a row of STEPS * 4096 inputs is STEPS * 256 of them (no
   // clamped duplicate loads: each load instruction costs the CU's memory pipeline).
   constexpr int kCopy = (STEPS * 256 + kBlock - 1) / kBlock;
-  // Loads of a row pair besides its steps: the bias and one residual base per token.
-  constexpr int kSide = 1 + MT;
+  // Loads of a row pair besides its steps: the bias, and one residual base per
+  // token where the epilogue adds to the output.
+  constexpr bool kBase = EPI == kResidual;
+  constexpr int kSide = 1 + (kBase ? MT : 0);
   static_assert(MT == 1 || (!QUANT && EPI != kPartials), "several tokens: pre-quantized rows and an output epilogue");
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int chunks = (sh.n + kChunk - 1) / kChunk;
@@ -670,19 +672,24 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvPtrs in, const uint8
   auto issue_side = [&](int row_pair, int& b, int (&base)[MT]) {
     const int own = min(row_pair * kRows + (sub & 1), sh.rows - 1);
     b = load_b32(bias != nullptr ? static_cast<const void*>(bias + own) : static_cast<const void*>(packed));
+    if constexpr (kBase) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-      base[t] = load_b32(EPI == kResidual ? static_cast<const void*>(output + (size_t)t * sh.out_stride + own)
-                                          : static_cast<const void*>(packed));
+      for (int t = 0; t < MT; ++t) base[t] = load_b32(output + (size_t)t * sh.out_stride + own);
+    } else {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) base[t] = 0;
+    }
   };
   // The wait that covers the side loads, repeated per register group so that
   // every register it covers is tied to a wait instruction (repeating a wait
   // whose count is already reached costs one instruction).
   auto side_wait = [&](int& b, int (&base)[MT], auto count_c) {
     constexpr int count = decltype(count_c)::value;
-    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b), "+v"(base[0]) : "n"(count) : "memory");
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(b) : "n"(count) : "memory");
+    if constexpr (kBase) {
 #pragma unroll
-    for (int t = 1; t < MT; ++t) asm volatile("s_waitcnt vmcnt(%1)" : "+v"(base[t]) : "n"(count) : "memory");
+      for (int t = 0; t < MT; ++t) asm volatile("s_waitcnt vmcnt(%1)" : "+v"(base[t]) : "n"(count) : "memory");
+    }
   };
 
   RowStep st[STEPS];
