@@ -27,7 +27,9 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(QuantArgs a) {
   const int chunks = (a.n + kChunk - 1) / kChunk;
   const RowSource src{a.input + (size_t)t * a.in_stride, a.aux, a.n, a.eps, a.splits, a.head_dim};
   float inv_rms;
-  const float scale = row_scale<MODE>(src, inv_rms, slots);
+  // Rows of up to 1024 inputs (the decoder's model width) load 4 inputs per
+  // thread and pass, not 16 mostly clamped ones (one block-uniform branch).
+  const float scale = a.n <= 4 * kThreads ? row_scale<MODE, 4>(src, inv_rms, slots) : row_scale<MODE>(src, inv_rms, slots);
   const int word = threadIdx.x;
   const int u = blockIdx.x * kSliceChunks + (word >> 4);
   int value = 0;

@@ -277,15 +277,16 @@ __device__ __forceinline__ float tree_reduce(float s, float* slots) {
   return total;  // used once per block, like block_max: no barrier after the reads
 }
 
+template <int NB = kBatch>
 __device__ __forceinline__ float tree_sum_squares(const float* __restrict__ x, int n, float* slots) {
   const int tid = threadIdx.x;
   float s = 0.0f;
-  for (int base = 0; base < n; base += kThreads * kBatch) {
-    float v[kBatch];
+  for (int base = 0; base < n; base += kThreads * NB) {
+    float v[NB];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) v[b] = x[min(base + b * kThreads + tid, n - 1)];
+    for (int b = 0; b < NB; ++b) v[b] = x[min(base + b * kThreads + tid, n - 1)];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
+    for (int b = 0; b < NB; ++b) {
       const float value = base + b * kThreads + tid < n ? v[b] : 0.0f;
       s = __builtin_fmaf(value, value, s);
     }
@@ -329,13 +330,13 @@ struct RowSource {
 // and, for NORM, sets inv_rms.  All 256 threads must call it.  amax is
 // order-free, so its loads are clamped duplicates rather than masked, and a
 // 16-byte aligned PLAIN row is read as float4.
-template <int MODE>
+template <int MODE, int NB = kBatch>
 __device__ __forceinline__ float row_scale(const RowSource& src, float& inv_rms, float* slots) {
   const int tid = threadIdx.x;
   const int n = src.n;
   inv_rms = 1.0f;
   if constexpr (MODE == kNorm) {
-    const float squares = tree_sum_squares(src.input, n, slots);
+    const float squares = tree_sum_squares<NB>(src.input, n, slots);
     inv_rms = 1.0f / __builtin_sqrtf(squares / (float)n + src.eps);
   }
   float amax = 0.0f;
@@ -345,25 +346,25 @@ __device__ __forceinline__ float row_scale(const RowSource& src, float& inv_rms,
   } else if (MODE == kPlain && (n & 3) == 0 && (((uintptr_t)src.input) & 15) == 0) {
     const float4* x4 = reinterpret_cast<const float4*>(src.input);
     const int n4 = n >> 2;
-    for (int base = 0; base < n4; base += kThreads * kBatch) {
-      float4 v[kBatch];
+    for (int base = 0; base < n4; base += kThreads * NB) {
+      float4 v[NB];
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) v[b] = x4[min(base + b * kThreads + tid, n4 - 1)];
+      for (int b = 0; b < NB; ++b) v[b] = x4[min(base + b * kThreads + tid, n4 - 1)];
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b)
+      for (int b = 0; b < NB; ++b)
         amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[b].x), fabsf(v[b].y))), fmaxf(fabsf(v[b].z), fabsf(v[b].w)));
     }
   } else {
-    for (int base = 0; base < n; base += kThreads * kBatch) {
-      float v[kBatch];
-      int idx[kBatch];
+    for (int base = 0; base < n; base += kThreads * NB) {
+      float v[NB];
+      int idx[NB];
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
+      for (int b = 0; b < NB; ++b) {
         idx[b] = min(base + b * kThreads + tid, n - 1);
         v[b] = src.input[idx[b]];
       }
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
+      for (int b = 0; b < NB; ++b) {
         float value = v[b];
         if constexpr (MODE == kNorm) value = fminf(fmaxf(value * inv_rms, -8.0f), 8.0f) * src.aux[idx[b]];
         amax = fmaxf(amax, fabsf(value));
