@@ -44,6 +44,35 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(QuantArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) a.scale[t] = scale;
 }
 
+// NORM rows of up to kSliceChunks chunks (1024 inputs, the decoder's model
+// width), one block per token: the row and its NORM weights are read once
+// into registers (quantize_row_to_lds: the same sum of squares in the same
+// order, the same fp32 operations per input as quantize_word), the q8 bytes
+// are exchanged through LDS, and thread w writes q8 word w and the chunk
+// sums as quantize_rows_kernel does.  One global round trip instead of three
+// (the row for the sum of squares, then row and weights for the absmax, then
+// again per q8 word).
+__global__ __launch_bounds__(kThreads) void quantize_norm_short_kernel(QuantArgs a) {
+  __shared__ float slots[64];
+  __shared__ __align__(16) unsigned char lds_q[kSliceChunks * kChunk];
+  const int t = blockIdx.y;
+  const int chunks = (a.n + kChunk - 1) / kChunk;
+  const RowSource src{a.input + (size_t)t * a.in_stride, a.aux, a.n, a.eps, a.splits, a.head_dim};
+  const float scale = quantize_row_to_lds<kNorm, kSliceChunks * kChunk / kThreads>(src, chunks, lds_q, slots);
+  __syncthreads();
+  const int word = threadIdx.x;
+  const int u = word >> 4, w = (word >> 2) & 3, k = word & 3;
+  const int value = u < chunks ? reinterpret_cast<const int*>(lds_q)[(w * chunks + u) * 4 + k] : 0;
+  const int total = chunk_lane_sum(word_sum(value));
+  const unsigned partner = (unsigned)__builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+  if (u < chunks) {
+    int32_t* q8 = reinterpret_cast<int32_t*>(a.q8 + (size_t)t * chunks * kChunk);
+    q8[u * 16 + (word & 15)] = a.split ? (int)split_quad_word((unsigned)value, partner, word & 3) : value;
+    if ((word & 15) == 0) a.xsum[(size_t)t * chunks + u] = total;
+  }
+  if (threadIdx.x == 0) a.scale[t] = scale;
+}
+
 template <int T>
 __global__ __launch_bounds__(T) void quantize_plain_kernel(QuantArgs a) {
   __shared__ float slots[T / 64];
@@ -65,6 +94,10 @@ hipError_t launch_quantize(hipStream_t stream, const QuantArgs& a) {
     } else {
       hipLaunchKernelGGL(quantize_plain_kernel<1024>, dim3(ceil_div(chunks, 64), a.m), dim3(1024), 0, stream, a);
     }
+    return hipGetLastError();
+  }
+  if (a.mode == kNorm && a.n > 0 && chunks <= kSliceChunks) {
+    hipLaunchKernelGGL(quantize_norm_short_kernel, dim3(1, a.m), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
   }
   const dim3 grid(ceil_div(chunks, kSliceChunks), a.m);
