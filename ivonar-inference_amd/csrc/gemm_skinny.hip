@@ -283,6 +283,25 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
   const v4u w_buf = wide_buffer(packed, (long long)a.rows * a.row_bytes);
   const v4u s_buf = wide_buffer(scales, (long long)a.rows * a.groups * 2);
 
+  // What the epilogue reads from global memory (token scales, biases, residual
+  // bases of this thread's outputs) goes out first: older than every
+  // hand-counted load below, so those waits stay exact, and the epilogue is
+  // not followed by a load round trip of its own.  Output o of the tile is
+  // token o / 16R, row o % 16R.
+  constexpr int kOutputs = T::kTokens * 16 * R;  // a multiple of 64: whole waves stay active together
+  constexpr int kEpi = (kOutputs + 64 * S - 1) / (64 * S);
+  float epi_sx[kEpi], epi_bias[kEpi], epi_base[kEpi];
+#pragma unroll
+  for (int jo = 0; jo < kEpi; ++jo) {
+    const int o = min(tid + jo * 64 * S, kOutputs - 1);
+    const int t = min(o / (16 * R), m - 1), row = min(row0 + o % (16 * R), a.rows - 1);
+    epi_sx[jo] = scale_in[t];
+    // Without a bias the load reads a token scale instead (no branch before the loads below).
+    const float b = *(bias != nullptr ? bias + row : scale_in);
+    epi_bias[jo] = bias != nullptr ? b : 0.0f;
+    epi_base[jo] = EPI == kResidual ? output[(size_t)t * a.out_stride + row] : 0.0f;
+  }
+
   // Scales: lane l < 16R fetches row row0 + l from group g0 on, 32 bytes from the dword below.
   const int scale_byte = ((row0 + lane) * a.groups + g0) * 2;
   const int scale_shift = scale_byte & 3;
@@ -374,9 +393,8 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
       for (int i = 0; i < 4; ++i)
         red[(s * T::kTokens + mt * 16 + 4 * kb + i) * T::kPitch + r * 16 + col] = acc[mt][r][i];
   __syncthreads();
-  constexpr int kOutputs = T::kTokens * 16 * R;  // a multiple of 64: whole waves stay active together
 #pragma unroll
-  for (int jo = 0; jo < (kOutputs + 64 * S - 1) / (64 * S); ++jo) {
+  for (int jo = 0; jo < kEpi; ++jo) {
     const int o = tid + jo * 64 * S;
     if (kOutputs % (64 * S) != 0 && o >= kOutputs) break;
     const int t = o / (16 * R), rr = o % (16 * R);
@@ -386,14 +404,14 @@ __global__ __launch_bounds__(64 * S) void skinny_row_kernel(const int8_t* __rest
     for (int k = 1; k < S; ++k) total = total + red[(k * T::kTokens + t) * T::kPitch + rr];
     const bool row_live = out_row < a.rows;
     const bool live = row_live && t < m;
-    float y = total * scale_in[min(t, m - 1)];
-    if (bias != nullptr) y = y + bias[min(out_row, a.rows - 1)];
+    float y = total * epi_sx[jo];
+    if (bias != nullptr) y = y + epi_bias[jo];
     float* orow = output + (size_t)min(t, m - 1) * a.out_stride;
     if constexpr (EPI == kSiluPair) {
       const float partner = __shfl_xor(y, 1);
       if (live && (out_row & 1) == 0 && out_row + 1 < a.rows) orow[out_row >> 1] = ivo_silu(y) * partner;
     } else if constexpr (EPI == kResidual) {
-      if (live) orow[out_row] = orow[out_row] + y;
+      if (live) orow[out_row] = epi_base[jo] + y;
     } else {
       if (live) orow[out_row] = y;
     }
