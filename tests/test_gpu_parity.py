@@ -173,6 +173,32 @@ def test_gemv_plain_store_model_shapes(cuda, oracle, rows, k):
     _check_gemv_store(cuda, oracle, rows, k, bias=False)
 
 
+@pytest.mark.parametrize("k", [24, 1024, 1102, 2048, 4096])
+def test_fused_gemv_vector_and_scalar_row_loads(cuda, oracle, k):
+    """Rows of up to 4096 inputs are quantized in the GEMV launch's prologue: a 16-byte aligned PLAIN row
+    with K a multiple of 4 is read as float4, other rows one input per load (an input shifted by one
+    float, and K=1102).  Both give the oracle's bits, for rows of 4, 8 and 16 inputs per thread."""
+    import torch
+    from ivonar_amd import ops, runtime
+
+    print(f"fused gemv_plain_store row loads K={k}", flush=True)
+    rows = 600
+    rng = np.random.default_rng(k + 11)
+    codes, packed, scale_bits, b = make_layer(rng, rows, k, bias=False)
+    matrix = device_matrix(packed, scale_bits, k, bias=None, device=cuda)
+    lanes, _ = runtime.gemv_plan(rows, k)
+    x = (rng.standard_normal(k) * 3.0).astype(np.float32)
+    x[rng.integers(0, k)] = 40.0
+    aligned = _t(x, cuda)
+    shifted = torch.zeros(k + 1, dtype=torch.float32, device=cuda)
+    shifted[1:] = aligned
+    q8, xsum, sx = oracle.quantize_rows(T.MODE_PLAIN, x, k)
+    expected = oracle.gemv_pairs(T.EPI_STORE, q8[0], xsum[0], sx[0], packed, scale_bits, None,
+                                 np.zeros(rows, np.float32), k, lanes)
+    assert_bits_equal(to_np(ops.gemv(matrix, aligned)), expected, "aligned input")
+    assert_bits_equal(to_np(ops.gemv(matrix, shifted[1:])), expected, "input shifted by one float")
+
+
 @pytest.mark.parametrize("k", [5000, 8192, 28672, 40000])
 @pytest.mark.parametrize("rows", [2, 600])
 def test_gemv_long_rows_back_to_back(cuda, oracle, rows, k):
