@@ -494,18 +494,32 @@ __device__ __forceinline__ float quantize_plain_row4_to_lds(const RowSource& src
   }
   amax = block_max(amax, slots + 32);
   const float scale = fmaxf(amax / 127.0f, 1e-5f);
+  // The four lanes 4g .. 4g + 3 hold the four float4 of one 16-input quad;
+  // word k of the quad takes byte j of lane j's quantized float4 at byte j
+  // (inputs 16w + k + 4j), so lane j forms word j with three DPP quad
+  // permutations and two v_perm_b32 (the byte transpose of
+  // quantize_row_split) and stores it whole.
+  const int j = tid & 3;
+  unsigned sel_near = 0x0C0C0C0Cu, sel_far = 0x0C0C0C0Cu;
+  sel_near = (sel_near & ~(0xFFu << (8 * j))) | ((unsigned)j << (8 * j));
+  sel_near = (sel_near & ~(0xFFu << (8 * (j ^ 1)))) | ((unsigned)(4 + j) << (8 * (j ^ 1)));
+  sel_far = (sel_far & ~(0xFFu << (8 * (j ^ 2)))) | ((unsigned)j << (8 * (j ^ 2)));
+  sel_far = (sel_far & ~(0xFFu << (8 * (j ^ 3)))) | ((unsigned)(4 + j) << (8 * (j ^ 3)));
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int f = c * kThreads + tid;
-    if (f < chunks * 16) {
-      const float e[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+    const float e[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+    unsigned q4 = 0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        // inputs past the row (f >= n4) hold zeros, which quantize to 0
-        const int q = (int)__builtin_rintf(e[k] / scale);
-        const int i = 4 * f + k, u = i >> 6, r = i & 63;
-        lds_q[((((r >> 4) & 3) * chunks + u) << 4) + ((r & 3) << 2) + ((r >> 2) & 3)] = (unsigned char)(q & 0xff);
-      }
+    for (int k = 0; k < 4; ++k)  // inputs past the row (f >= n4) hold zeros, which quantize to 0
+      q4 |= ((unsigned)(int)__builtin_rintf(e[k] / scale) & 0xffu) << (8 * k);
+    const unsigned p1 = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+    const unsigned p2 = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+    const unsigned p3 = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x1B, 0xF, 0xF, false);  // lane ^ 3
+    const unsigned word = __builtin_amdgcn_perm(p1, q4, sel_near) | __builtin_amdgcn_perm(p3, p2, sel_far);
+    if (f < chunks * 16) {  // whole quads: chunks * 16 is a multiple of 4
+      const int g = f >> 2;  // quad g: chunk g >> 2, quad g & 3
+      reinterpret_cast<unsigned*>(lds_q)[(((g & 3) * chunks + (g >> 2)) << 2) + j] = word;
     }
   }
   return scale;
