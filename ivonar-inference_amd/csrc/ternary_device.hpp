@@ -455,13 +455,50 @@ __device__ __forceinline__ float quantize_row_to_lds(const RowSource& src, int c
   }
   amax = block_max(amax, slots + 32);
   const float scale = fmaxf(amax / 127.0f, 1e-5f);
+  if constexpr (NB % 4 == 0) {
+    // Thread t's input t + 256b is byte j = (t >> 2) & 3 of word (chunk
+    // (t >> 6) + 4b, quad (t >> 4) & 3, field t & 3): the four bytes of a word
+    // sit in lanes 4 apart within a 16-lane row, one per j.  For each four
+    // batches b = 4c .. 4c + 3 the lanes rotate their four bytes by 4, 8 and
+    // 12 lanes (DPP row_ror) and lane j keeps word b = 4c + j, whose byte i
+    // is lane i's byte j; each rotated value's source is found by rotating
+    // j the same way.  One word store instead of four byte stores.
+    const int j = (tid >> 2) & 3;
+    const int ja = __builtin_amdgcn_mov_dpp(j, 0x124, 0xF, 0xF, false);  // row_ror:4
+    const int jb = __builtin_amdgcn_mov_dpp(j, 0x128, 0xF, 0xF, false);  // row_ror:8
+    const int jc = __builtin_amdgcn_mov_dpp(j, 0x12C, 0xF, 0xF, false);  // row_ror:12
+    // v_perm_b32 selectors: 0..3 pick the second operand's bytes, 4..7 the first's, 0x0C zero.
+    auto place = [](unsigned sel, int position, unsigned source) {
+      return (sel & ~(0xFFu << (8 * position))) | (source << (8 * position));
+    };
+    const unsigned sel_a = place(place(0x0C0C0C0Cu, j, (unsigned)j), ja, 4u + j);   // own byte j, lane ja's
+    const unsigned sel_b = place(place(0x0C0C0C0Cu, jb, (unsigned)j), jc, 4u + j);  // lanes jb and jc
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int i = b * kThreads + tid;
-    if (i < chunks * kChunk) {
-      const int q = i < n ? (int)__builtin_rintf(v[b] / scale) : 0;
-      const int u = i >> 6, r = i & 63;
-      lds_q[((((r >> 4) & 3) * chunks + u) << 4) + ((r & 3) << 2) + ((r >> 2) & 3)] = (unsigned char)(q & 0xff);
+    for (int c = 0; c < NB / 4; ++c) {
+      unsigned q4 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = (4 * c + e) * kThreads + tid;
+        const int q = i < n ? (int)__builtin_rintf(v[4 * c + e] / scale) : 0;
+        q4 |= ((unsigned)q & 0xffu) << (8 * e);
+      }
+      const unsigned pa = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x124, 0xF, 0xF, false);
+      const unsigned pb = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x128, 0xF, 0xF, false);
+      const unsigned pc = (unsigned)__builtin_amdgcn_mov_dpp((int)q4, 0x12C, 0xF, 0xF, false);
+      const unsigned word = __builtin_amdgcn_perm(pa, q4, sel_a) | __builtin_amdgcn_perm(pc, pb, sel_b);
+      const int u = (tid >> 6) + 4 * (4 * c + j);
+      if (u < chunks)
+        reinterpret_cast<unsigned*>(lds_q)[((((tid >> 4) & 3) * chunks + u) << 2) + (tid & 3)] = word;
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int i = b * kThreads + tid;
+      if (i < chunks * kChunk) {
+        const int q = i < n ? (int)__builtin_rintf(v[b] / scale) : 0;
+        const int u = i >> 6, r = i & 63;
+        lds_q[((((r >> 4) & 3) * chunks + u) << 4) + ((r & 3) << 2) + ((r >> 2) & 3)] = (unsigned char)(q & 0xff);
+      }
     }
   }
   return scale;
